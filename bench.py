@@ -1,0 +1,293 @@
+#!/usr/bin/env python3
+"""Benchmark of the single-GPU layer-streaming training step.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+Default workload ``llama3-8b``: one causal-LM training step of a Llama-3.1-8B
+shaped model (32 layers, hidden 4096, 32/8 heads of 128, intermediate 14336,
+vocab 128256, RoPE theta 500000), random N(0, 0.02) weights, batch 4 x 1024
+uniform random tokens, through SlideFSDP: fp32 masters in pinned host
+memory, layer-wise H2D + on-GPU cast, checkpointed activations offloaded to
+host, bf16 grads D2H into the host LayerAdam.  Other workloads:
+``qwen2.5-14b`` (48 layers, hidden 5120, batch 2 x 4096), ``tiny`` (a small
+Llama for a quick check).
+
+One JSON line is printed with the metric (tokens/s), the roofline of the
+staging cast kernel (HBM-bound, measured with HIP events on its stream over
+the timed region), host-link rates of the H2D/D2H copies, and the reference's
+host-side staging + LayerAdam path timed on this machine's cores
+(``cpu_baseline``).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from concurrent.futures import ThreadPoolExecutor
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, GB/s
+LINK_PEAK_GBS = 63.0      # PCIe 5.0 x16, per direction, GB/s
+
+WORKLOADS = {
+    "llama3-8b": dict(vocab=128256, hidden=4096, inter=14336, layers=32, heads=32, kv=8, head_dim=128,
+                      theta=500000.0, batch=4, seq=1024, model="Llama-3.1-8B", arch="llama"),
+    "qwen2.5-14b": dict(vocab=152064, hidden=5120, inter=13824, layers=48, heads=40, kv=8, head_dim=128,
+                        theta=1000000.0, batch=2, seq=4096, model="Qwen2.5-14B", arch="qwen2"),
+    "tiny": dict(vocab=4096, hidden=512, inter=1024, layers=4, heads=8, kv=4, head_dim=64,
+                 theta=500000.0, batch=2, seq=256, model="tiny-llama", arch="llama"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_model(w: dict, seed: int = 42):
+    """Random-init model of the workload's architecture, N(0, 0.02) weights and
+    unit RMSNorm weights, built without materialising HF's own init."""
+    import torch
+
+    if w["arch"] == "llama":
+        from transformers import LlamaConfig as C, LlamaForCausalLM as M
+    else:
+        from transformers import Qwen2Config as C, Qwen2ForCausalLM as M
+    cfg = C(vocab_size=w["vocab"], hidden_size=w["hidden"], intermediate_size=w["inter"],
+            num_hidden_layers=w["layers"], num_attention_heads=w["heads"], num_key_value_heads=w["kv"],
+            head_dim=w["head_dim"], rope_theta=w["theta"], max_position_embeddings=max(8192, w["seq"]),
+            tie_word_embeddings=False, torch_dtype=torch.float32)
+    cfg._attn_implementation = "sdpa"
+    with torch.device("meta"):
+        model = M(cfg)
+    model = model.to_empty(device="cpu")
+    # buffers created on meta (rotary inv_freq) must be rebuilt on the host
+    rope_cls = type(model.model.rotary_emb)
+    model.model.rotary_emb = rope_cls(config=cfg)
+    params = list(model.named_parameters())
+
+    def init(i_np):
+        i, (name, p) = i_np
+        g = torch.Generator().manual_seed(seed * 100003 + i)
+        with torch.no_grad():
+            if "norm" in name:
+                p.fill_(1.0)
+            elif name.endswith(".bias"):
+                p.zero_()
+            else:
+                p.normal_(0.0, 0.02, generator=g)
+
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
+        list(ex.map(init, enumerate(params)))
+    return model
+
+
+def elapsed_stats(records):
+    """(total ms, total bytes or elements) from (start, end, amount) event records."""
+    ms = sum(a.elapsed_time(b) for a, b, _ in records)
+    amt = sum(n for _, _, n in records)
+    return ms, amt
+
+
+def cpu_baseline(layer_numel: int, total_params: int, tokens: int, resident_params: int, iters: int = 4):
+    """The reference's host-side work, timed on this host: per unit the fp32 ->
+    bf16 cast of the master (reference layer_state.py:301, torch CPU copy),
+    twice per step (forward and backward load), the ``grad.float()`` unpack
+    (layer_adam.py:404) and the CPU Adam (the reference's own cpu_adam when
+    oracle/_ref is built, else the oracle's scalar port), on a sample of one
+    Llama-3-8B decoder layer, scaled to the model's parameter count."""
+    import torch
+
+    n = layer_numel
+    threads = torch.get_num_threads()
+    ref = None
+    kind = "port"
+    path = os.path.join(ROOT, "oracle", "_ref", "cpu_adam_ref.so")
+    if os.path.exists(path):
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("cpu_adam_ref", path)
+        ref = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(ref)
+        kind = "reference"
+    g = torch.Generator().manual_seed(42)
+    master = torch.randn(n, generator=g) * 0.02
+    bf = torch.empty(n, dtype=torch.bfloat16)
+    grad = (torch.randn(n, generator=g) * 1e-3).bfloat16()
+    m = torch.zeros(n)
+    v = torch.zeros(n)
+    if ref is not None:
+        ref.create_adam(77, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, False)
+
+        def adam(step, gf):
+            ref.adam_update(77, step, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, master, gf, m, v)
+    else:
+        import numpy as np
+
+        import oracle
+        opt = oracle.OracleAdam(1e-5, (0.9, 0.999), 1e-8, 0.01, True)
+        n = min(n, 8_000_000)  # the scalar port is single-threaded: sample fewer elements
+        master, grad, m, v, bf = master[:n], grad[:n], m[:n], v[:n], bf[:n]
+
+        def adam(step, gf):
+            opt.update(step, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, master.numpy(), gf.numpy(), m.numpy(), v.numpy())
+        threads = 1
+    t_cast = t_unpack = t_adam = 0.0
+    for it in range(iters + 1):
+        t0 = time.perf_counter()
+        bf.copy_(master)
+        t1 = time.perf_counter()
+        gf = grad.float()
+        t2 = time.perf_counter()
+        adam(it + 1, gf)
+        t3 = time.perf_counter()
+        if it > 0:
+            t_cast += t1 - t0
+            t_unpack += t2 - t1
+            t_adam += t3 - t2
+    t_cast, t_unpack, t_adam = (x / iters for x in (t_cast, t_unpack, t_adam))
+    per_param = (t_cast * 2 + t_unpack + t_adam) / n
+    # units that stay resident are cast once per step, not twice
+    step_s = per_param * total_params - t_cast / n * resident_params
+    if ref is not None:
+        ref.destroy_adam(77)
+    return {
+        "value": tokens / step_s,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": (f"one Llama-3-8B decoder layer sample ({n:,} params): torch CPU fp32->bf16 cast "
+                   f"{t_cast * 1e3:.1f} ms, grad.float() {t_unpack * 1e3:.1f} ms, CPU Adam {t_adam * 1e3:.1f} ms "
+                   f"({28 * n / t_adam / 1e9:.1f} GB/s at 28 B/param); per-step time = per-param cost x "
+                   f"{total_params:,} params (cast twice, resident units once)"),
+        "ms_per_layer": {"cast": t_cast * 1e3, "unpack": t_unpack * 1e3, "adam": t_adam * 1e3},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", default="llama3-8b", choices=sorted(WORKLOADS))
+    ap.add_argument("--layers", type=int, default=0, help="override the number of decoder layers")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs the layer-streaming path on one GPU only; use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from test1_amd import SlideFSDP, SlideFSDPConfig
+
+    w = dict(WORKLOADS[args.workload])
+    if args.layers:
+        w["layers"] = args.layers
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    t0 = time.time()
+    model = build_model(w)
+    log(f"[bench] model built in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    cfg = SlideFSDPConfig(device=dev, lr=1e-5, weight_decay=0.01, attention_implementation="sdpa")
+    sf = SlideFSDP(model, cfg)
+    log(f"[bench] SlideFSDP ready in {time.time() - t0:.1f}s")
+    B, S = w["batch"], w["seq"]
+    g = torch.Generator().manual_seed(0)
+    batches = [torch.randint(0, w["vocab"], (B, S), generator=g).to(dev) for _ in range(args.warmup + args.steps)]
+
+    for i in range(args.warmup):
+        t = time.time()
+        out = sf(input_ids=batches[i], labels=batches[i])
+        sf.wait_for_updates()
+        torch.cuda.synchronize()
+        log(f"[bench] warmup {i}: loss {out.loss.item():.4f} {time.time() - t:.2f}s")
+
+    rt = sf.runtime
+    rt.stager.cast_timing, rt.stager.copy_timing, rt.d2h_timing = [], [], []
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    losses = []
+    for i in range(args.steps):
+        out = sf(input_ids=batches[args.warmup + i], labels=batches[args.warmup + i])
+        losses.append(out.loss)
+        log(f"[bench] step {i} issued")
+    sf.wait_for_updates()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    losses = [x.item() for x in losses]
+    log(f"[bench] timed {args.steps} steps in {elapsed:.2f}s, losses {losses}")
+
+    cast_ms, cast_elems = elapsed_stats(rt.stager.cast_timing)
+    h2d_ms, h2d_bytes = elapsed_stats(rt.stager.copy_timing)
+    d2h_ms, d2h_bytes = elapsed_stats(rt.d2h_timing)
+    ncast = len(rt.stager.cast_timing)
+    cast_bytes = 6 * cast_elems  # read fp32 + write bf16 per element
+    cast_gbs = cast_bytes / (cast_ms * 1e-3) / 1e9 if cast_ms > 0 else 0.0
+    tokens = B * S * args.steps
+    value = tokens / elapsed
+
+    total_params = sf.total_params
+    layer_numel = sum(p.numel() for p in sf.decoder_layers[0].parameters())
+    resident = layer_numel + sum(p.numel() for p in sf.output_layer.parameters())
+    cpu = None
+    if not args.no_cpu_baseline:
+        t = time.time()
+        cpu = cpu_baseline(218_112_000 if w["arch"] == "llama" and w["hidden"] == 4096 else layer_numel,
+                           total_params, B * S, resident)
+        log(f"[bench] cpu baseline in {time.time() - t:.1f}s: {cpu['sample']}")
+
+    res = {
+        "metric": f"train tokens/s ({w['model']} layer offload, 1 GPU)",
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (uniform random token ids, random-init N(0,0.02) weights)",
+        "config": {"workload": f"{w['model']} causal-LM training step, fp32 masters in pinned host memory, "
+                               f"layer-wise H2D + GPU cast, activation checkpoint offload, host LayerAdam",
+                   "global_batch": B, "seq_len": S, "layers": w["layers"], "hidden": w["hidden"],
+                   "params": total_params, "parallelism": "none (1 GPU)"},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "cast_flat_kernel (fp32 -> bf16 RNE staging cast)",
+            "achieved": cast_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": cast_gbs / HBM_PEAK_GBS,
+            "traffic": None,
+            "launches": ncast,
+            "avg_launch_ms": cast_ms / ncast if ncast else None,
+            "algorithmic_bytes_per_launch": cast_bytes / ncast if ncast else None,
+        },
+        "host_link": {
+            "h2d_gbs": h2d_bytes / (h2d_ms * 1e-3) / 1e9 if h2d_ms > 0 else None,
+            "d2h_gbs": d2h_bytes / (d2h_ms * 1e-3) / 1e9 if d2h_ms > 0 else None,
+            "h2d_frac": (h2d_bytes / (h2d_ms * 1e-3) / 1e9) / LINK_PEAK_GBS if h2d_ms > 0 else None,
+            "d2h_frac": (d2h_bytes / (d2h_ms * 1e-3) / 1e9) / LINK_PEAK_GBS if d2h_ms > 0 else None,
+            "peak_gbs": LINK_PEAK_GBS,
+            "h2d_bytes_per_step": h2d_bytes / args.steps,
+            "d2h_bytes_per_step": d2h_bytes / args.steps,
+            "h2d_busy_frac": (h2d_ms * 1e-3) / elapsed,
+        },
+        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "losses": losses,
+    }
+    print(json.dumps(res), flush=True)
+    sf.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,192 @@
+/*
+ * slidefsdp.h -- C ABI of the MI355X layer-streaming library.
+ *
+ * Two shared libraries implement this header:
+ *   libsf_hip.so  device kernels, copies and pinned host memory (HIP, gfx950)
+ *   libsf_cpu.so  the host AdamW used by LayerAdam (C++, AVX-512 + OpenMP)
+ *
+ * Conventions shared by every entry point:
+ *   - Plain pointers and sizes only; no framework types cross this boundary.
+ *   - Return 0 on success. Nonzero values are either a hipError_t or one of
+ *     the SF_E* codes below; sf_error_string() turns any of them into text.
+ *   - Device entry points are asynchronous on the caller's stream, allocate
+ *     nothing and keep no global mutable state, so any host thread may call
+ *     them concurrently on different streams.
+ *   - Sizes are element counts unless the name says bytes.
+ *
+ * Each declaration names the reference interface (file:line in the
+ * SlideFSDP sources) whose work it takes over.
+ */
+#ifndef SLIDEFSDP_H
+#define SLIDEFSDP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* An opaque HIP stream handle (hipStream_t); 0 is the null stream. */
+typedef void* sf_stream_t;
+
+/* Library-specific status codes, disjoint from hipError_t values. */
+#define SF_OK 0
+#define SF_EINVAL 9001      /* null pointer, negative count, bad enum */
+#define SF_ETOOMANY 9002    /* more segments than SF_MAX_SEGS in one call */
+#define SF_EDTYPE 9003      /* dtype combination not supported */
+#define SF_ENOOPT 9004      /* unknown optimizer id */
+#define SF_EOVERLAP 9005    /* source and destination ranges overlap */
+
+/* Maximum number of segments one segment-table call accepts. */
+#define SF_MAX_SEGS 64
+
+/* One contiguous run of n elements copied from src to dst.  Both are
+ * absolute addresses (device or host-mapped); n counts elements of the
+ * entry point's element type. */
+typedef struct sf_seg {
+    uint64_t src;
+    uint64_t dst;
+    uint64_t n;
+} sf_seg;
+
+/* ---------------------------------------------------------------------
+ * Status and version
+ * ------------------------------------------------------------------- */
+
+/* Text for any status returned by this library (never NULL). */
+const char* sf_error_string(int status);
+
+/* ABI version, bumped on any incompatible change. */
+int sf_abi_version(void);
+
+/* ---------------------------------------------------------------------
+ * Parameter staging (libsf_hip.so)
+ * ------------------------------------------------------------------- */
+
+/* fp32 -> bf16, round to nearest even, NaN -> 0xFFFF, dst[i] = rne(src[i])
+ * for i < n.  Replaces the host-side cast of the flat fp32 master into the
+ * pinned bf16 convert buffer, layer_state.py:301
+ * (`_bf16_convert_buffer[:total_size].copy_(_cpu_params_flat)`); here it
+ * runs in HBM after the fp32 master has been copied to the device. */
+int sf_cast_f32_bf16(const float* src, uint16_t* dst, size_t n,
+                     sf_stream_t stream);
+
+/* The same cast over a table of segments (src: fp32, dst: bf16), for a
+ * device layer buffer whose per-parameter views are not offset-identical
+ * to the flat master.  The reference's views are offset-identical
+ * (layer_state.py:246-250 and :318-320), where one sf_cast_f32_bf16 over
+ * the whole layer is the same operation. */
+int sf_cast_scatter_f32_bf16(const sf_seg* segs, int nsegs,
+                             sf_stream_t stream);
+
+/* ---------------------------------------------------------------------
+ * Gradient and activation packing (libsf_hip.so)
+ * ------------------------------------------------------------------- */
+
+/* Gather: for each segment k, copy segs[k].n 16-bit elements from
+ * segs[k].src to dst + (sum of the n of segments before k).  segs[k].dst
+ * is ignored.  Packs a layer's per-parameter bf16 gradients into one
+ * contiguous buffer that a single D2H copy can move; it replaces the
+ * per-parameter grad views into the shared grad buffer that
+ * layer_state.py:250 and :321-322 set up and the D2H at
+ * distributed_sync.py:353 reads. */
+int sf_pack_b16(const sf_seg* segs, int nsegs, uint16_t* dst,
+                sf_stream_t stream);
+
+/* Scatter, the inverse of sf_pack_b16: for each segment k, copy segs[k].n
+ * elements from src + (sum of earlier n) to segs[k].dst.  segs[k].src is
+ * ignored.  Restores packed checkpoint tensors (sliding_checkpoint.py:
+ * 104-105) when they were packed from non-contiguous sources. */
+int sf_unpack_b16(const uint16_t* src, const sf_seg* segs, int nsegs,
+                  sf_stream_t stream);
+
+/* General 16-bit segment copy: both addresses taken from each segment. */
+int sf_copy_segs_b16(const sf_seg* segs, int nsegs, sf_stream_t stream);
+
+/* dst[i] = value for i < n (16-bit elements), as a kernel rather than a
+ * memset node so it is safe inside captured graphs.  Replaces
+ * `_current_gpu_cache["grad"].zero_()`, layer_state.py:296-297. */
+int sf_fill_b16(uint16_t* dst, size_t n, uint16_t value,
+                sf_stream_t stream);
+
+/* ---------------------------------------------------------------------
+ * Copies and pinned host memory (libsf_hip.so)
+ * ------------------------------------------------------------------- */
+
+#define SF_COPY_H2D 1
+#define SF_COPY_D2H 2
+#define SF_COPY_D2D 3
+
+/* Asynchronous copy of `bytes` bytes on `stream`.  Host memory must be
+ * pinned (sf_host_alloc) for the copy to be asynchronous.  Replaces the
+ * non_blocking copies at distributed_sync.py:332 (params H2D),
+ * distributed_sync.py:353 (grads D2H), sliding_checkpoint.py:73
+ * (activation D2H) and sliding_checkpoint.py:105 (activation H2D). */
+int sf_memcpy_async(void* dst, const void* src, size_t bytes, int kind,
+                    sf_stream_t stream);
+
+/* Exact-size pinned host allocation (no power-of-two rounding).  Replaces
+ * `torch.empty(..., pin_memory=True)` for the fp32 flat masters
+ * (layer_state.py:203-208), the shared grad and convert buffers
+ * (slide_fsdp.py:174-186) and the activation slots (slide_fsdp.py:
+ * 480-503). */
+int sf_host_alloc(void** out, size_t bytes);
+int sf_host_free(void* ptr);
+
+/* ---------------------------------------------------------------------
+ * Host AdamW (libsf_cpu.so)
+ * ------------------------------------------------------------------- */
+
+#define SF_DTYPE_F32 0
+#define SF_DTYPE_BF16 1
+#define SF_DTYPE_F16 2
+
+/* Scalars of one update, precomputed by the caller. */
+typedef struct sf_adam_hparams {
+    float beta1;
+    float beta2;
+    float eps;
+    float weight_decay;
+    float step_size;        /* -lr / bias_correction1                   */
+    float bias_correction2; /* 1 / sqrt(1 - beta2^t), or 1 if disabled  */
+    float lr;
+    int adamw_mode;         /* 1: decoupled decay; 0: L2 into the grad  */
+} sf_adam_hparams;
+
+/* Stateless AdamW over n elements: fp32 params and moments updated in
+ * place, grads read as g_dtype (SF_DTYPE_F32 or SF_DTYPE_BF16; bf16 is
+ * widened exactly, so the result equals the fp32 call on `grad.float()`).
+ * Per-element operation order follows Adam_Optimizer::Step_AVX,
+ * optimizer/layer_adam/csrc/cpu_adam.h:143-192. */
+int sf_cpu_adam_step(float* params, const void* grads, int g_dtype,
+                     float* exp_avg, float* exp_avg_sq, size_t n,
+                     const sf_adam_hparams* hp);
+
+/* Stateful interface with the reference's pybind11 `cpu_adam` module
+ * semantics (optimizer/layer_adam/csrc/cpu_adam.cpp:8-13):
+ *   create_adam  -> sf_adam_create   (cpu_adam_impl.cpp:89-127)
+ *   adam_update  -> sf_adam_update   (cpu_adam_impl.cpp:211-237)
+ *   destroy_adam -> sf_adam_destroy  (cpu_adam_impl.cpp:239-244)
+ * sf_adam_update keeps the reference's per-optimizer beta^t running
+ * state (cpu_adam.h:57-89).  Unlike the reference, an unknown id returns
+ * SF_ENOOPT and the registry is locked. */
+int sf_adam_create(int optimizer_id, float alpha, float beta1, float beta2,
+                   float eps, float weight_decay, int adamw_mode,
+                   int should_log);
+int sf_adam_update(int optimizer_id, size_t step, float lr, float beta1,
+                   float beta2, float eps, float weight_decay,
+                   int bias_correction, float* params, const void* grads,
+                   int g_dtype, float* exp_avg, float* exp_avg_sq, size_t n);
+int sf_adam_destroy(int optimizer_id);
+
+/* OpenMP team size used by the host AdamW (<= 0: library default). */
+int sf_cpu_set_threads(int nthreads);
+/* 1 if the AVX-512 path is used on this host, 0 for the portable path. */
+int sf_cpu_has_avx512(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SLIDEFSDP_H */

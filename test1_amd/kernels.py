@@ -1,0 +1,167 @@
+"""Tensor-level wrappers over the device entry points of the C ABI.
+
+Every wrapper checks dtype, device, contiguity and sizes on the host before
+anything is launched, passes raw pointers and the stream handle, and turns a
+nonzero status into ``NativeError`` (a ``RuntimeError``).  The work is
+asynchronous on ``stream`` (default: the current stream).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _native
+
+_B16 = (torch.bfloat16, torch.float16, torch.int16, torch.uint16)
+
+
+def _stream_ptr(stream: Optional[torch.cuda.Stream]) -> ctypes.c_void_p:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _require_cuda(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise ValueError(f"{what} must be a GPU tensor, got {t.device}")
+
+
+def _require_contig(t: torch.Tensor, what: str) -> None:
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+
+
+def cast_f32_bf16_(dst: torch.Tensor, src: torch.Tensor, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """dst[:] = RNE-bf16(src), both flat-contiguous GPU tensors of equal numel."""
+    if src.dtype != torch.float32 or dst.dtype != torch.bfloat16:
+        raise TypeError(f"cast_f32_bf16_: need float32 -> bfloat16, got {src.dtype} -> {dst.dtype}")
+    _require_cuda(src, "src")
+    _require_cuda(dst, "dst")
+    _require_contig(src, "src")
+    _require_contig(dst, "dst")
+    if src.numel() != dst.numel():
+        raise ValueError(f"cast_f32_bf16_: numel mismatch {src.numel()} vs {dst.numel()}")
+    _native.check(
+        _native.hip().sf_cast_f32_bf16(src.data_ptr(), dst.data_ptr(), src.numel(), _stream_ptr(stream)),
+        "sf_cast_f32_bf16",
+    )
+    return dst
+
+
+def _seg_array(segs: Sequence[Tuple[int, int, int]]):
+    arr = (_native.SfSeg * max(1, len(segs)))()
+    for i, (s, d, n) in enumerate(segs):
+        arr[i].src, arr[i].dst, arr[i].n = s, d, n
+    return arr
+
+
+def cast_scatter_f32_bf16(pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]],
+                          stream: Optional[torch.cuda.Stream] = None) -> None:
+    """For each (src fp32, dst bf16) pair of contiguous GPU tensors: dst = RNE(src)."""
+    segs = []
+    for k, (src, dst) in enumerate(pairs):
+        if src.dtype != torch.float32 or dst.dtype != torch.bfloat16:
+            raise TypeError(f"pair {k}: need float32 -> bfloat16")
+        _require_cuda(src, f"pair {k} src")
+        _require_cuda(dst, f"pair {k} dst")
+        _require_contig(src, f"pair {k} src")
+        _require_contig(dst, f"pair {k} dst")
+        if src.numel() != dst.numel():
+            raise ValueError(f"pair {k}: numel mismatch")
+        segs.append((src.data_ptr(), dst.data_ptr(), src.numel()))
+    arr = _seg_array(segs)
+    _native.check(_native.hip().sf_cast_scatter_f32_bf16(arr, len(segs), _stream_ptr(stream)),
+                  "sf_cast_scatter_f32_bf16")
+
+
+def _check_b16(t: torch.Tensor, what: str) -> None:
+    if t.dtype not in _B16:
+        raise TypeError(f"{what}: need a 16-bit dtype, got {t.dtype}")
+    _require_cuda(t, what)
+    _require_contig(t, what)
+
+
+def pack_b16(srcs: Sequence[torch.Tensor], dst: torch.Tensor,
+             stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """dst[off_k : off_k + n_k] = srcs[k].flatten(), offsets in order from 0."""
+    _check_b16(dst, "dst")
+    total = 0
+    segs = []
+    for k, s in enumerate(srcs):
+        _check_b16(s, f"srcs[{k}]")
+        segs.append((s.data_ptr(), 0, s.numel()))
+        total += s.numel()
+    if total > dst.numel():
+        raise ValueError(f"pack_b16: {total} elements do not fit in dst of {dst.numel()}")
+    arr = _seg_array(segs)
+    _native.check(_native.hip().sf_pack_b16(arr, len(segs), dst.data_ptr(), _stream_ptr(stream)), "sf_pack_b16")
+    return dst
+
+
+def copy_segs_b16(pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]],
+                  stream: Optional[torch.cuda.Stream] = None) -> None:
+    """For each (src, dst) pair of contiguous 16-bit GPU tensors of equal numel,
+    dst = src, all in one launch."""
+    segs = []
+    for k, (src, dst) in enumerate(pairs):
+        _check_b16(src, f"pair {k} src")
+        _check_b16(dst, f"pair {k} dst")
+        if src.numel() != dst.numel():
+            raise ValueError(f"pair {k}: numel mismatch {src.numel()} vs {dst.numel()}")
+        segs.append((src.data_ptr(), dst.data_ptr(), src.numel()))
+    if not segs:
+        return
+    arr = _seg_array(segs)
+    _native.check(_native.hip().sf_copy_segs_b16(arr, len(segs), _stream_ptr(stream)), "sf_copy_segs_b16")
+
+
+def unpack_b16(src: torch.Tensor, dsts: Sequence[torch.Tensor],
+               stream: Optional[torch.cuda.Stream] = None) -> None:
+    """dsts[k].flatten() = src[off_k : off_k + n_k], the inverse of pack_b16."""
+    _check_b16(src, "src")
+    total = 0
+    segs = []
+    for k, d in enumerate(dsts):
+        _check_b16(d, f"dsts[{k}]")
+        segs.append((0, d.data_ptr(), d.numel()))
+        total += d.numel()
+    if total > src.numel():
+        raise ValueError(f"unpack_b16: src of {src.numel()} holds fewer than {total} elements")
+    arr = _seg_array(segs)
+    _native.check(_native.hip().sf_unpack_b16(src.data_ptr(), arr, len(segs), _stream_ptr(stream)),
+                  "sf_unpack_b16")
+
+
+def fill_b16_(dst: torch.Tensor, value: int = 0, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """dst[:] = value (a 16-bit pattern), as a kernel (graph-capture safe)."""
+    _check_b16(dst, "dst")
+    _native.check(_native.hip().sf_fill_b16(dst.data_ptr(), dst.numel(), int(value) & 0xFFFF, _stream_ptr(stream)),
+                  "sf_fill_b16")
+    return dst
+
+
+def memcpy_async(dst: torch.Tensor, src: torch.Tensor, stream: Optional[torch.cuda.Stream] = None,
+                 nbytes: Optional[int] = None) -> None:
+    """Asynchronous byte copy between contiguous tensors on ``stream``.
+
+    Host tensors must be pinned for the copy to overlap; direction is taken
+    from the devices.
+    """
+    _require_contig(src, "src")
+    _require_contig(dst, "dst")
+    n = nbytes if nbytes is not None else src.numel() * src.element_size()
+    if n > src.numel() * src.element_size() or n > dst.numel() * dst.element_size():
+        raise ValueError(f"memcpy_async: {n} bytes exceed a buffer")
+    sd, dd = src.device.type, dst.device.type
+    if sd == "cpu" and dd == "cuda":
+        kind = _native.SF_COPY_H2D
+    elif sd == "cuda" and dd == "cpu":
+        kind = _native.SF_COPY_D2H
+    elif sd == "cuda" and dd == "cuda":
+        kind = _native.SF_COPY_D2D
+    else:
+        raise ValueError(f"memcpy_async: unsupported direction {sd} -> {dd}")
+    _native.check(_native.hip().sf_memcpy_async(dst.data_ptr(), src.data_ptr(), n, kind, _stream_ptr(stream)),
+                  "sf_memcpy_async")

@@ -1,0 +1,441 @@
+"""Device buffer pool and per-unit runtime of the layer-streaming path.
+
+Reference layer_state.py:28-467.  The reference casts each unit's fp32
+master to bf16 on the host (one thread, layer_state.py:301), copies the bf16
+layer to the GPU and blocks on the copy stream (:326); gradients come back
+through one shared pinned buffer (:367-381), which serialises each offload
+behind the previous unit's CPU update (:362-363).
+
+Here the GPU does the staging, and everything on the GPU is ordered with
+events instead of host waits:
+
+* H2D: the pinned fp32 master is copied by DMA into a device fp32 staging
+  ring (``H2DStager``), one chunk per slot, on ``h2d_stream``; a HIP kernel
+  casts each chunk to bf16 (RNE) into the pool unit on ``cast_stream``.
+  The cast waits for the unit's ``ready`` event: the event after which the
+  unit's previous contents are no longer read (the compute that used it, or
+  the D2H of its gradients).  The reference has no such fence
+  (layer_state.py:292-315 start the next H2D into a unit released on the
+  host without waiting for the compute stream).
+* The compute stream waits for the unit's load with ``wait_event``; no host
+  thread blocks on a copy.
+* Gradients: after the last gradient of a unit is accumulated, one pack
+  kernel gathers the per-parameter bf16 grads into the unit's contiguous
+  grad buffer (offset-identical to the fp32 master), a DMA copies it into a
+  pinned slot of ``GradStagingRing`` (2 deep, so unit i's offload waits for
+  unit i+2's update, not unit i+1's), and the update thread runs LayerAdam
+  on the slot in place.
+
+Memory layout in HBM (per pool unit, ``max_param_size`` elements):
+  unit["param"]  bf16, views offset-identical to the fp32 master
+  unit["grad"]   bf16, packed gradients in the same layout
+plus the fp32 staging ring (``depth`` chunks of ``chunk_elems``).
+"""
+
+from __future__ import annotations
+
+import queue
+import threading
+import time
+from collections import OrderedDict, deque
+from concurrent.futures import Future, ThreadPoolExecutor
+from typing import Any, Callable, Dict, List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import kernels
+from .pinned import pinned_empty
+
+
+def _new_event() -> torch.cuda.Event:
+    return torch.cuda.Event(enable_timing=False, blocking=False)
+
+
+class LayerBufferPool:
+    """Fixed set of device units ``{"param", "grad"}`` reused round-robin.
+
+    Reference layer_state.py:28-101 (``acquire`` = popleft, ``release`` =
+    append).  Two differences: ``acquire`` blocks until a unit is released
+    (units come back from the gradient-offload thread, not only from the
+    thread that acquires), and every unit carries a ``ready`` event that the
+    next writer of the unit must wait on.
+    """
+
+    def __init__(self, max_param_size: int, dtype: torch.dtype, device: torch.device, pool_size: int = 2):
+        if pool_size < 2:
+            raise ValueError("gpu_buffer_pool_size must be at least 2 (current + prefetched unit)")
+        self.max_param_size = max_param_size
+        self.dtype = dtype
+        self.device = device
+        self.pool_size = pool_size
+        self.pool: deque = deque()
+        for _ in range(pool_size):
+            self.pool.append({
+                "param": torch.empty(max_param_size, dtype=dtype, device=device),
+                "grad": torch.empty(max_param_size, dtype=dtype, device=device),
+                "ready": None,
+            })
+        self._cv = threading.Condition()
+
+    def acquire(self, timeout: Optional[float] = None) -> Dict[str, Any]:
+        with self._cv:
+            if not self._cv.wait_for(lambda: len(self.pool) > 0, timeout=timeout):
+                raise TimeoutError("LayerBufferPool.acquire: no unit released in time")
+            return self.pool.popleft()
+
+    def release(self, unit: Dict[str, Any]) -> None:
+        with self._cv:
+            self.pool.append(unit)
+            self._cv.notify()
+
+    def available(self) -> int:
+        with self._cv:
+            return len(self.pool)
+
+
+class H2DStager:
+    """Pinned fp32 master -> device bf16 unit, through a device fp32 ring.
+
+    Each chunk: DMA into slot s on ``h2d_stream`` (after the cast that last
+    read slot s), then the cast kernel on ``cast_stream``.  Copies of later
+    chunks and layers keep the host link busy while earlier chunks are cast
+    or while a cast waits for its unit to become free.
+    """
+
+    def __init__(self, device: torch.device, chunk_elems: int, depth: int,
+                 h2d_stream: torch.cuda.Stream, cast_stream: torch.cuda.Stream):
+        if depth < 1 or chunk_elems < 1:
+            raise ValueError("H2DStager: depth and chunk_elems must be positive")
+        self.chunk = int(chunk_elems)
+        self.depth = int(depth)
+        self.buf = torch.empty(self.depth * self.chunk, dtype=torch.float32, device=device)
+        self.slot_free: List[Optional[torch.cuda.Event]] = [None] * self.depth
+        self.next_slot = 0
+        self.h2d_stream = h2d_stream
+        self.cast_stream = cast_stream
+        self._lock = threading.Lock()
+        # Optional instrumentation: when a list, each cast appends
+        # (start_event, end_event, n_elements); each copy appends to copy_timing.
+        self.cast_timing: Optional[list] = None
+        self.copy_timing: Optional[list] = None
+
+    def load(self, host_f32: torch.Tensor, dst_bf16: torch.Tensor,
+             wait_event: Optional[torch.cuda.Event]) -> torch.cuda.Event:
+        n = host_f32.numel()
+        if dst_bf16.numel() < n:
+            raise ValueError("H2DStager.load: destination smaller than source")
+        with self._lock:
+            if wait_event is not None:
+                self.cast_stream.wait_event(wait_event)
+            for off in range(0, n, self.chunk):
+                c = min(self.chunk, n - off)
+                s = self.next_slot
+                self.next_slot = (s + 1) % self.depth
+                slot = self.buf[s * self.chunk: s * self.chunk + c]
+                if self.slot_free[s] is not None:
+                    self.h2d_stream.wait_event(self.slot_free[s])
+                if self.copy_timing is not None:
+                    t0 = torch.cuda.Event(enable_timing=True)
+                    t0.record(self.h2d_stream)
+                kernels.memcpy_async(slot, host_f32[off:off + c], self.h2d_stream)
+                copied = _new_event() if self.copy_timing is None else torch.cuda.Event(enable_timing=True)
+                copied.record(self.h2d_stream)
+                if self.copy_timing is not None:
+                    self.copy_timing.append((t0, copied, c * 4))
+                self.cast_stream.wait_event(copied)
+                if self.cast_timing is not None:
+                    c0 = torch.cuda.Event(enable_timing=True)
+                    c0.record(self.cast_stream)
+                kernels.cast_f32_bf16_(dst_bf16[off:off + c], slot, self.cast_stream)
+                freed = _new_event() if self.cast_timing is None else torch.cuda.Event(enable_timing=True)
+                freed.record(self.cast_stream)
+                if self.cast_timing is not None:
+                    self.cast_timing.append((c0, freed, c))
+                self.slot_free[s] = freed
+            done = _new_event()
+            done.record(self.cast_stream)
+            return done
+
+
+class GradStagingRing:
+    """``depth`` pinned bf16 host slots of ``max_elems`` for gradient D2H.
+
+    Replaces the single shared ``_cpu_grad_buffer`` of reference
+    slide_fsdp.py:174-179; a slot is handed back by the update thread once
+    LayerAdam has consumed it.
+    """
+
+    def __init__(self, depth: int, max_elems: int, dtype: torch.dtype = torch.bfloat16):
+        self.slots = [pinned_empty(max_elems, dtype) for _ in range(depth)]
+        self._free: "queue.Queue[int]" = queue.Queue()
+        for i in range(depth):
+            self._free.put(i)
+
+    def acquire(self, timeout: Optional[float] = None) -> int:
+        try:
+            return self._free.get(timeout=timeout)
+        except queue.Empty:
+            raise TimeoutError("GradStagingRing.acquire: no slot released in time") from None
+
+    def release(self, idx: int) -> None:
+        self._free.put(idx)
+
+
+class StreamingRuntime:
+    """Objects shared by all units of one model: streams, pool, stager, grad
+    ring, worker threads and the optional event trace."""
+
+    def __init__(self, device: torch.device, dtype: torch.dtype, max_param_size: int, pool_size: int,
+                 stage_chunk_elems: int, stage_depth: int, grad_ring_depth: int, wait_timeout: Optional[float]):
+        self.device = device
+        self.h2d_stream = torch.cuda.Stream(device=device)
+        self.cast_stream = torch.cuda.Stream(device=device)
+        self.d2h_stream = torch.cuda.Stream(device=device)
+        self.pool = LayerBufferPool(max_param_size, dtype, device, pool_size)
+        self.stager = H2DStager(device, stage_chunk_elems, stage_depth, self.h2d_stream, self.cast_stream)
+        self.grad_ring = GradStagingRing(grad_ring_depth, max_param_size, dtype)
+        # One thread issues gradient offloads (it may wait for a free host
+        # slot); one thread runs the host optimizer, as the reference's
+        # update executor (slide_fsdp.py:163).
+        self.offload_executor = ThreadPoolExecutor(max_workers=1, thread_name_prefix="sf-offload")
+        self.update_executor = ThreadPoolExecutor(max_workers=1, thread_name_prefix="sf-update")
+        self.wait_timeout = wait_timeout
+        self.trace: Optional[List[Tuple]] = None
+        self._trace_lock = threading.Lock()
+        self.d2h_timing: Optional[list] = None
+        # Test hook: when a dict, each update stores {unit: (host grads, fp32
+        # master before the update)} copies, for checking against the oracle.
+        self.capture: Optional[dict] = None
+
+    def log(self, *event) -> None:
+        if self.trace is not None:
+            with self._trace_lock:
+                self.trace.append(tuple(event))
+
+    def shutdown(self) -> None:
+        self.offload_executor.shutdown(wait=True)
+        self.update_executor.shutdown(wait=True)
+
+
+class LayerRuntimeState(nn.Module):
+    """Runtime of one unit: fp32 pinned master, device residency, gradient
+    offload and the asynchronous host update.
+
+    Reference layer_state.py:105-467; method names and meanings are kept:
+    ``to_device_async``, ``wait_for_h2d``, ``to_offload_async``,
+    ``wait_for_d2h``, ``update_params``, ``wait_for_update``.
+    """
+
+    def __init__(self, layer: nn.Module, layer_idx: int, config, runtime: StreamingRuntime,
+                 layer_optimizer: Any, is_last_layer: bool = False):
+        super().__init__()
+        self.layer = layer
+        self.layer_idx = layer_idx
+        self.config = config
+        self.runtime = runtime
+        self.buffer_pool = runtime.pool
+        self.layer_optimizer = layer_optimizer
+        self.is_last_layer = is_last_layer
+
+        self.update_finished = threading.Event()
+        self.update_finished.set()
+        self.update_lock = threading.Lock()
+        self._h2d_done: Optional[torch.cuda.Event] = None
+        self._d2h_future: Optional[Future] = None
+        self._update_future: Optional[Future] = None
+        self._current_gpu_cache: Optional[Dict[str, Any]] = None
+        self._post_called = False
+        self._bwd_armed = False
+
+        params = list(self.layer.parameters())
+        self.total_size = sum(p.numel() for p in params)
+        self._cpu_params_flat = pinned_empty(self.total_size, torch.float32)
+        self._param_maps: "OrderedDict[str, Tuple[int, torch.Size, int]]" = OrderedDict()
+        self._param_views: "OrderedDict[str, torch.Tensor]" = OrderedDict()
+        self._params: List[nn.Parameter] = []
+        self._init_param_views()
+        self._grad_params = [p for p in self._params if p.requires_grad]
+        self._grads_seen = 0
+        self._grad_lock = threading.Lock()
+        if self.layer_optimizer is not None:
+            self.layer_optimizer.add_layer_params(layer_idx, self._params)
+
+    # ------------------------------------------------------------------
+    def _init_param_views(self) -> None:
+        """Flatten in ``named_parameters()`` order into the pinned fp32 master and
+        point every ``param.data`` at its view (reference layer_state.py:240-264)."""
+        with torch.no_grad():
+            offset = 0
+            for name, param in self.layer.named_parameters():
+                size = param.numel()
+                self._param_maps[name] = (offset, param.shape, size)
+                view = self._cpu_params_flat[offset:offset + size].view(param.shape)
+                view.copy_(param.data)
+                self._param_views[name] = view
+                param.data = view
+                param.grad = None
+                self._params.append(param)
+                offset += size
+
+    def _named(self):
+        return zip(self._param_maps.items(), self._params)
+
+    def _bind_device_views(self, unit: Dict[str, Any]) -> None:
+        buf = unit["param"]
+        for (name, (off, shape, size)), p in self._named():
+            p.data = buf[off:off + size].view(shape)
+            p.grad = None
+
+    def _bind_host_views(self) -> None:
+        for (name, _), p in self._named():
+            p.data = self._param_views[name]
+            p.grad = None
+
+    # ------------------------------------------------------------------
+    def to_device_async(self, is_backward: bool = False) -> None:
+        """Start loading this unit; returns once the work is enqueued.
+
+        Waits on the host only for this unit's previous update (so the master
+        is current) and for a free pool unit.
+        """
+        if self._current_gpu_cache is not None:
+            return  # already resident (last decoder / output unit)
+        self.wait_for_update()
+        unit = self.buffer_pool.acquire(timeout=self.runtime.wait_timeout)
+        self._h2d_done = self.runtime.stager.load(self._cpu_params_flat, unit["param"], unit["ready"])
+        unit["ready"] = None
+        self._bind_device_views(unit)
+        self._current_gpu_cache = unit
+        self.runtime.log("h2d", self.layer_idx, is_backward)
+
+    def wait_for_h2d(self, timeout: Optional[float] = None) -> None:
+        """Make the current stream wait for this unit's load (no host block)."""
+        if self._h2d_done is not None:
+            torch.cuda.current_stream().wait_event(self._h2d_done)
+
+    def is_resident(self) -> bool:
+        return self._current_gpu_cache is not None
+
+    # ------------------------------------------------------------------
+    def to_offload_async(self, is_backward: bool = False, prev_update=None) -> None:
+        """Release this unit after its forward (``is_backward=False``) or offload
+        its gradients after its backward (``is_backward=True``).
+
+        Forward: the unit becomes reusable once the current stream has passed
+        this point.  Backward: pack the gradients on the current stream, then
+        hand the D2H and update to the worker threads.  ``prev_update`` is
+        accepted for signature compatibility; the two-slot grad ring makes it
+        unnecessary.
+        """
+        unit = self._current_gpu_cache
+        if unit is None:
+            return
+        cur = torch.cuda.current_stream()
+        if not is_backward:
+            ev = _new_event()
+            ev.record(cur)
+            unit["ready"] = ev
+            self._bind_host_views()
+            self._current_gpu_cache = None
+            self.buffer_pool.release(unit)
+            return
+
+        gbuf = unit["grad"]
+        pairs, missing = [], []
+        for (name, (off, shape, size)), p in self._named():
+            g = p.grad
+            if g is None:
+                missing.append((off, size))
+                continue
+            if g.dtype != gbuf.dtype or g.device != gbuf.device:
+                raise RuntimeError(f"unit {self.layer_idx}: grad of {name} is {g.dtype} on {g.device}, "
+                                   f"expected {gbuf.dtype} on {gbuf.device}")
+            pairs.append((g.detach().contiguous().reshape(-1), gbuf[off:off + size]))
+        # One launch gathers every gradient into its offset in the unit's
+        # grad buffer; parameters that received no gradient contribute zeros,
+        # as the zeroed grad buffer of the reference does (layer_state.py:297).
+        kernels.copy_segs_b16(pairs, cur)
+        for off, size in missing:
+            kernels.fill_b16_(gbuf[off:off + size], 0, cur)
+        grad_ready = _new_event()
+        grad_ready.record(cur)
+        # The grads were produced on the current stream and are read there by
+        # the pack kernel; dropping them now lets the allocator reuse them in
+        # stream order.
+        self._bind_host_views()
+        self._current_gpu_cache = None
+        self.update_finished.clear()
+        self.runtime.log("d2h", self.layer_idx)
+        self._d2h_future = self.runtime.offload_executor.submit(self._d2h_task, unit, grad_ready)
+
+    def _d2h_task(self, unit: Dict[str, Any], grad_ready: torch.cuda.Event) -> None:
+        rt = self.runtime
+        slot = rt.grad_ring.acquire(timeout=rt.wait_timeout)
+        try:
+            host = rt.grad_ring.slots[slot]
+            rt.d2h_stream.wait_event(grad_ready)
+            if rt.d2h_timing is not None:
+                t0 = torch.cuda.Event(enable_timing=True)
+                t0.record(rt.d2h_stream)
+            kernels.memcpy_async(host[:self.total_size], unit["grad"][:self.total_size], rt.d2h_stream)
+            done = _new_event() if rt.d2h_timing is None else torch.cuda.Event(enable_timing=True)
+            done.record(rt.d2h_stream)
+            if rt.d2h_timing is not None:
+                rt.d2h_timing.append((t0, done, self.total_size * 2))
+        except BaseException:
+            rt.grad_ring.release(slot)
+            self.buffer_pool.release(unit)
+            raise
+        unit["ready"] = done
+        self.buffer_pool.release(unit)
+        self._update_future = rt.update_executor.submit(self._do_update, slot, done)
+
+    def wait_for_d2h(self, timeout: Optional[float] = None) -> None:
+        """Wait until the gradient offload has been issued (and re-raise its
+        errors).  Unlike the reference (layer_state.py:407-408), errors of
+        finished tasks are not swallowed."""
+        f = self._d2h_future
+        if f is not None:
+            f.result(timeout=timeout)
+
+    # ------------------------------------------------------------------
+    def _grad_views(self, host: torch.Tensor) -> Dict[nn.Parameter, torch.Tensor]:
+        views = {}
+        for (name, (off, shape, size)), p in self._named():
+            views[p] = host[off:off + size].view(shape)
+        return views
+
+    def _do_update(self, slot: int, d2h_done: torch.cuda.Event) -> bool:
+        rt = self.runtime
+        try:
+            d2h_done.synchronize()
+            if rt.capture is not None:
+                rt.capture[self.layer_idx] = (rt.grad_ring.slots[slot][:self.total_size].clone(),
+                                              self._cpu_params_flat.clone())
+            with self.update_lock:
+                if self.layer_optimizer is not None:
+                    self.layer_optimizer.step_with_grad_views(self.layer_idx, self._grad_views(rt.grad_ring.slots[slot]))
+        finally:
+            rt.grad_ring.release(slot)
+            self.update_finished.set()
+        return True
+
+    def update_params(self) -> None:
+        """Kept for API compatibility: the update is queued by the offload
+        task as soon as the gradients' D2H is issued."""
+
+    def wait_for_update(self, timeout: Optional[float] = None) -> None:
+        """Block until this unit's last update finished; re-raise its error.
+        A unit whose offload is still queued is waited for as well."""
+        t = timeout if timeout is not None else self.runtime.wait_timeout
+        if self._d2h_future is not None:
+            self._d2h_future.result(timeout=t)
+        f = self._update_future
+        if f is not None:
+            f.result(timeout=t)
+        if not self.update_finished.wait(timeout=t):
+            raise TimeoutError(f"Layer {self.layer_idx} parameter update timed out")
+
+    def forward(self, *args, **kwargs):
+        raise NotImplementedError("LayerRuntimeState manages state; call .layer(...) for compute")

@@ -1,0 +1,94 @@
+"""Tensor-level shim with the reference's native ``cpu_adam`` module interface.
+
+Reference optimizer/layer_adam/csrc/cpu_adam.cpp:8-13 binds three functions
+through pybind11; the same three are offered here over the C ABI of
+``libsf_cpu.so`` (include/slidefsdp.h):
+
+  create_adam(id, alpha, beta1, beta2, eps, weight_decay, adamw_mode, should_log) -> 0
+  adam_update(id, step, lr, beta1, beta2, eps, weight_decay, bias_correction,
+              params, grads, exp_avg, exp_avg_sq) -> 0
+  destroy_adam(id) -> 0
+
+Supported dtypes: fp32 params and fp32 moments (the combination LayerAdam
+uses, layer_adam.py:158 with fp32_optimizer_state=True), with fp32 or bf16
+grads; bf16 grads are widened exactly, so they give the bits of the
+reference's ``grad.float()`` call.  Other combinations raise the reference's
+RuntimeError.  Deliberate differences from the reference: a non-contiguous
+params/exp_avg/exp_avg_sq raises ValueError instead of silently updating a
+``.contiguous()`` copy (cpu_adam_impl.cpp:224-227), and an unknown id raises
+RuntimeError instead of dereferencing a null pointer (cpu_adam_impl.cpp:229-231).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .. import _native
+
+
+def _lib():
+    return _native.cpu()
+
+
+def _check(status: int, what: str) -> None:
+    _native.check(status, what, _lib())
+
+
+def create_adam(optimizer_id: int, alpha: float = 1e-3, beta1: float = 0.9, beta2: float = 0.999,
+                eps: float = 1e-8, weight_decay: float = 0.0, adamw_mode: bool = True,
+                should_log: bool = False) -> int:
+    _check(_lib().sf_adam_create(int(optimizer_id), alpha, beta1, beta2, eps, weight_decay,
+                                 1 if adamw_mode else 0, 1 if should_log else 0), "create_adam")
+    return 0
+
+
+def destroy_adam(optimizer_id: int) -> int:
+    _check(_lib().sf_adam_destroy(int(optimizer_id)), "destroy_adam")
+    return 0
+
+
+def _grad_dtype_code(g: torch.Tensor) -> int:
+    if g.dtype == torch.float32:
+        return _native.SF_DTYPE_F32
+    if g.dtype == torch.bfloat16:
+        return _native.SF_DTYPE_BF16
+    return -1
+
+
+def adam_update(optimizer_id: int, step: int, lr: float, beta1: float, beta2: float, eps: float,
+                weight_decay: float, bias_correction: bool, params: torch.Tensor, grads: torch.Tensor,
+                exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor) -> int:
+    if params.dtype != torch.float32 or exp_avg.dtype != torch.float32 or exp_avg_sq.dtype != torch.float32:
+        raise RuntimeError(
+            f"Adam optimizer with param type {params.dtype} and state type {exp_avg.dtype} "
+            "is not supported on current hardware"
+        )
+    gcode = _grad_dtype_code(grads)
+    if gcode < 0:
+        raise RuntimeError(f"Adam optimizer with grad type {grads.dtype} is not supported on current hardware")
+    for t, name in ((params, "params"), (grads, "grads"), (exp_avg, "exp_avg"), (exp_avg_sq, "exp_avg_sq")):
+        if t.device.type != "cpu":
+            raise RuntimeError(f"adam_update: {name} must be a CPU tensor, got {t.device}")
+    for t, name in ((params, "params"), (exp_avg, "exp_avg"), (exp_avg_sq, "exp_avg_sq")):
+        if not t.is_contiguous():
+            raise ValueError(f"adam_update: {name} is updated in place and must be contiguous")
+    n = params.numel()
+    if grads.numel() != n or exp_avg.numel() != n or exp_avg_sq.numel() != n:
+        raise ValueError("adam_update: params, grads and moments must have the same numel")
+    if not grads.is_contiguous():
+        grads = grads.contiguous()
+    _check(_lib().sf_adam_update(int(optimizer_id), int(step), lr, beta1, beta2, eps, weight_decay,
+                                 1 if bias_correction else 0, params.data_ptr(), grads.data_ptr(), gcode,
+                                 exp_avg.data_ptr(), exp_avg_sq.data_ptr(), n), "adam_update")
+    return 0
+
+
+def set_num_threads(n: int) -> None:
+    """OpenMP team size of the host AdamW (<= 0 restores the default)."""
+    _check(_lib().sf_cpu_set_threads(int(n)), "sf_cpu_set_threads")
+
+
+def has_avx512() -> bool:
+    return bool(_lib().sf_cpu_has_avx512())

@@ -1,0 +1,421 @@
+"""SlideFSDP: train a HuggingFace causal LM one unit at a time on one GPU.
+
+Drop-in for reference slide_fsdp.py:116-744: ``SlideFSDP(model, config)``
+is an ``nn.Module`` whose ``forward(input_ids, attention_mask, labels)``
+runs the forward, runs the backward itself and returns
+``CausalLMOutputWithPast``; the host LayerAdam updates every unit as soon as
+its gradients are on the host, so callers never call ``optimizer.step()``.
+
+The model is split into units ``[embedding] + decoder layers + [norm +
+lm_head]`` (reference slide_fsdp.py:213-244).  fp32 masters of every unit
+live in pinned host memory; at most ``gpu_buffer_pool_size`` units are on the
+GPU at once, as bf16.  Unit i+1 is loaded while unit i computes
+(``PreLayerFunction``), unit i is released after its forward
+(``PostLayerFunction``), and in backward each unit's gradients go to the host
+and into LayerAdam while earlier units are still computing.  Checkpoint
+inputs are offloaded by ``SlidingCheckpoint``.
+
+Single GPU only: ``param_transfer_mode="full"`` and no collectives (the
+reference's ``NoOpSync``, distributed_sync.py:313-362).
+
+Differences from the reference, each a correctness or memory fix:
+  * a unit's gradients are offloaded when all of them have been accumulated
+    (post-accumulate-grad hooks on every parameter), not from a pre-hook on
+    its first parameter (slide_fsdp.py:419-430), which fires before the
+    unit's backward has finished;
+  * the last decoder's gradients are the ones autograd produced: the
+    reference leaves its ``param.grad`` outside the unit grad buffer and then
+    offloads a stale buffer (layer_state.py:286-287, 370-375);
+  * a decoder layer returning a tensor (transformers >= 5) is not indexed
+    with ``[0]``, which would drop all but the first sequence of the batch
+    (slide_fsdp.py:584-590);
+  * ``save_pretrained`` restores the fp32 masters after writing bf16 weights
+    (slide_fsdp.py:721-725 leaves the parameters detached from them);
+  * the mask slot of the activation offload is allocated only if a mask
+    tensor is actually saved.
+"""
+
+from __future__ import annotations
+
+import os
+from typing import Any, List, Optional
+
+import torch
+import torch.nn as nn
+from torch.utils.checkpoint import checkpoint
+from transformers.modeling_outputs import CausalLMOutputWithPast
+
+from .config import SlideFSDPConfig
+from .distributed_sync import create_distributed_sync
+from .layer_state import LayerRuntimeState, StreamingRuntime
+from .optimizer import LayerAdam
+from .pinned import pinned_empty
+from .sliding_checkpoint import ActivationRing, SlidingCheckpoint
+
+
+class OutputLayer(nn.Module):
+    """Final norm + lm_head + shifted cross-entropy as one unit (reference
+    slide_fsdp.py:45-113, the branch without the optional fused kernel:
+    full logits and ``nn.CrossEntropyLoss``)."""
+
+    def __init__(self, norm: nn.Module, lm_head: nn.Module, hidden_size: int):
+        super().__init__()
+        self.norm = norm
+        self.lm_head = lm_head
+        self.hidden_size = hidden_size
+        self.lce = None
+        self.loss_fn = nn.CrossEntropyLoss()
+
+    def forward(self, hidden_states: torch.Tensor, labels: Optional[torch.Tensor] = None):
+        hidden_states = self.norm(hidden_states)
+        logits = self.lm_head(hidden_states)
+        loss = None
+        if labels is not None:
+            shift_logits = logits[..., :-1, :].contiguous()
+            shift_labels = labels[..., 1:].contiguous()
+            loss = self.loss_fn(shift_logits.view(-1, shift_logits.size(-1)), shift_labels.view(-1))
+        return loss, logits
+
+
+def _cpu_count() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+class SlideFSDP(nn.Module):
+    """Layer-streaming trainer (reference slide_fsdp.py:116-211).
+
+    Extra keyword arguments (all optional, not in the reference):
+      stage_chunk_elems  fp32 elements per H2D staging chunk (default: the
+                         largest unit, i.e. one chunk per unit)
+      stage_depth        staging ring depth (default 2)
+      grad_ring_depth    pinned gradient slots (default 2)
+      wait_timeout       seconds before a host wait raises TimeoutError
+                         (default None: wait forever, as the reference)
+    """
+
+    def __init__(self, model, config: SlideFSDPConfig, *, stage_chunk_elems: Optional[int] = None,
+                 stage_depth: int = 2, grad_ring_depth: int = 2, wait_timeout: Optional[float] = None):
+        super().__init__()
+        if config.param_transfer_mode != "full":
+            raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
+        if config.dtype != torch.bfloat16:
+            raise NotImplementedError("SlideFSDP stages parameters as bfloat16; dtype=float16 is not supported")
+        if config.ac_offload_mode == "nvme":
+            raise NotImplementedError("ac_offload_mode='nvme' (GPUDirect Storage) is not supported")
+        if not config.enable_activation_checkpoint:
+            raise NotImplementedError(
+                "enable_activation_checkpoint=False would keep every unit's weights saved for backward "
+                "while its pool buffer is reused; set it to True")
+        self.config = config
+        self.device = torch.device(config.device)
+        if self.device.type != "cuda":
+            raise ValueError(f"SlideFSDP needs a GPU device, got {self.device}")
+        self.dtype = config.dtype
+        self.base_model = model
+        self.model_config = model.config
+        self.rank = 0
+        self.world_size = 1
+        self.dist_sync = create_distributed_sync(config)
+
+        self._split_model(model)
+        self.max_param_size = self._calculate_max_param_size()
+        self.total_params = sum(sum(p.numel() for p in layer.parameters()) for layer in self.all_layers)
+
+        chunk = int(stage_chunk_elems) if stage_chunk_elems else self.max_param_size
+        self.runtime = StreamingRuntime(self.device, self.dtype, self.max_param_size, config.gpu_buffer_pool_size,
+                                        chunk, stage_depth, grad_ring_depth, wait_timeout)
+        self.buffer_pool = self.runtime.pool
+        self.layer_optimizer = self._create_optimizer(config)
+        self.layer_states: List[LayerRuntimeState] = []
+        self._create_layer_states()
+        self._setup_autograd_functions()
+
+        self.layer_tensors: Optional[List[List[torch.Tensor]]] = None
+        self.position_embeddings = None
+        self._act_ring = ActivationRing(self.device)
+        self._print_model_info()
+
+    # ------------------------------------------------------------------
+    def _split_model(self, model) -> None:
+        decoder = model.get_decoder()
+        if hasattr(decoder, "layers"):
+            layers = decoder.layers
+        elif hasattr(decoder, "block"):
+            layers = decoder.block
+        else:
+            raise ValueError("Cannot find decoder layers in model")
+        self.num_decoder_layers = len(layers)
+        self.embed_tokens = model.get_input_embeddings()
+        self.decoder_layers = nn.ModuleList(layers)
+        self.rotary_emb = getattr(decoder, "rotary_emb", None)
+        self._update_causal_mask = getattr(decoder, "_update_causal_mask", None)
+        lm_head = model.get_output_embeddings()
+        if lm_head is not None and lm_head.weight is self.embed_tokens.weight:
+            raise NotImplementedError("tied input/output embeddings are not supported (one parameter in two units)")
+        self.output_layer = OutputLayer(norm=decoder.norm, lm_head=lm_head, hidden_size=model.config.hidden_size)
+        self.all_layers = [self.embed_tokens] + list(self.decoder_layers) + [self.output_layer]
+
+    def _calculate_max_param_size(self) -> int:
+        return max(sum(p.numel() for p in layer.parameters()) for layer in self.all_layers)
+
+    def _create_optimizer(self, config: SlideFSDPConfig) -> LayerAdam:
+        opt = LayerAdam(lr=config.lr, betas=config.adam_betas, eps=config.adam_eps,
+                        weight_decay=config.weight_decay, bias_correction=config.bias_correction,
+                        fp32_optimizer_state=True, num_layer=len(self.all_layers),
+                        nvme_offload_fraction=config.optimizer_nvme_offload_fraction,
+                        offload_dir=config.optimizer_offload_dir, prefetch=True)
+        threads = int(os.environ.get("SF_ADAM_THREADS", "0") or 0)
+        if threads <= 0:
+            threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or _cpu_count()
+        opt.cpu_adam.set_num_threads(threads)
+        return opt
+
+    def _create_layer_states(self) -> None:
+        n = len(self.all_layers)
+        for idx, layer in enumerate(self.all_layers):
+            self.layer_states.append(LayerRuntimeState(layer, idx, self.config, self.runtime, self.layer_optimizer,
+                                                       is_last_layer=(idx == n - 1)))
+
+    # ------------------------------------------------------------------
+    def _setup_autograd_functions(self) -> None:
+        """Autograd functions around each unit (reference slide_fsdp.py:343-430).
+
+        ``PreLayerFunction`` (forward: prefetch the next unit, make the compute
+        stream wait for this one) and ``PostLayerFunction`` (forward: release
+        the unit; backward: prefetch the previous unit) are not re-run by the
+        checkpoint recompute.  Gradient offload is driven by post-accumulate
+        hooks on every parameter: when the last gradient of a unit lands, the
+        unit is offloaded.
+        """
+        sf = self
+
+        class PreLayerFunction(torch.autograd.Function):
+            @staticmethod
+            def forward(ctx, hidden_states, layer_state, next_layer_state):
+                ctx.set_materialize_grads(False)
+                if next_layer_state is not None:
+                    is_output = next_layer_state.layer_idx == len(sf.layer_states) - 1
+                    next_layer_state.to_device_async(is_backward=is_output)
+                layer_state._post_called = False
+                layer_state.wait_for_h2d()
+                return hidden_states
+
+            @staticmethod
+            def backward(ctx, grad_output):
+                return grad_output, None, None
+
+        class PostLayerFunction(torch.autograd.Function):
+            @staticmethod
+            def forward(ctx, hidden_states, layer_state, is_last_layer):
+                ctx.layer_state = layer_state
+                ctx.set_materialize_grads(False)
+                if not is_last_layer:
+                    layer_state.to_offload_async(is_backward=False)
+                return hidden_states
+
+            @staticmethod
+            def backward(ctx, grad_output):
+                sf._on_pre_backward(ctx.layer_state)
+                return grad_output, None, None
+
+        self._PreLayerFunction = PreLayerFunction
+        self._PostLayerFunction = PostLayerFunction
+
+        for idx, state in enumerate(self.layer_states):
+            state._post_called = False
+            for p in state._grad_params:
+                p.register_post_accumulate_grad_hook(self._make_grad_hook(state, idx))
+
+    def _make_grad_hook(self, state: LayerRuntimeState, idx: int):
+        def hook(param):
+            with state._grad_lock:
+                if not state._bwd_armed or state._post_called:
+                    return
+                state._grads_seen += 1
+                done = state._grads_seen == len(state._grad_params)
+            if done:
+                self._on_post_backward(state, idx)
+        return hook
+
+    def _on_pre_backward(self, layer_state: LayerRuntimeState) -> None:
+        """Before a unit's backward: prefetch the unit before it, then order
+        the compute stream after this unit's load (reference slide_fsdp.py:432-448)."""
+        idx = layer_state.layer_idx
+        if idx == len(self.layer_states) - 1:
+            # First backward node of the step: flush units that never received
+            # all their gradients once the backward pass has finished.
+            torch.autograd.Variable._execution_engine.queue_callback(self._finish_backward)
+        with layer_state._grad_lock:
+            layer_state._bwd_armed = True
+            layer_state._grads_seen = 0
+        if idx - 1 >= 0:
+            self.layer_states[idx - 1].to_device_async(is_backward=True)
+        layer_state.wait_for_h2d()
+
+    def _on_post_backward(self, layer_state: LayerRuntimeState, idx: int) -> None:
+        """After a unit's last gradient: pack, offload and queue the update
+        (reference slide_fsdp.py:450-464)."""
+        with layer_state._grad_lock:
+            if layer_state._post_called:
+                return
+            layer_state._post_called = True
+            layer_state._bwd_armed = False
+        layer_state.to_offload_async(is_backward=True)
+
+    def _finish_backward(self) -> None:
+        for idx, state in enumerate(self.layer_states):
+            if state._bwd_armed and state.is_resident():
+                self._on_post_backward(state, idx)
+
+    # ------------------------------------------------------------------
+    def _allocate_activation_tensors(self, batch_size: int, seq_length: int, hidden_size: int) -> None:
+        """Pinned host slot of the hidden-state checkpoint per decoder layer
+        (reference slide_fsdp.py:466-505); the mask slot is created on demand."""
+        if self.config.ac_offload_mode == "none":
+            return
+        self.layer_tensors = [
+            [pinned_empty((batch_size, seq_length, hidden_size), self.dtype)]
+            for _ in range(self.num_decoder_layers)
+        ]
+
+    @staticmethod
+    def _first(out):
+        return out[0] if isinstance(out, (tuple, list)) else out
+
+    def forward(self, input_ids: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
+                labels: Optional[torch.Tensor] = None, **kwargs) -> CausalLMOutputWithPast:
+        """One training step (reference slide_fsdp.py:507-640)."""
+        batch_size, seq_length = input_ids.shape
+        hidden_size = self.model_config.hidden_size
+        if self.config.ac_offload_mode != "none":
+            if self.layer_tensors is None or self.layer_tensors[0][0].shape != (batch_size, seq_length, hidden_size):
+                self._allocate_activation_tensors(batch_size, seq_length, hidden_size)
+        self._act_ring.reset()
+
+        embed_state = self.layer_states[0]
+        next_state = self.layer_states[1] if len(self.layer_states) > 1 else None
+        embed_state.to_device_async(is_backward=False)
+        if next_state is not None:
+            next_state.to_device_async(is_backward=False)
+        embed_state._post_called = False
+        embed_state.wait_for_h2d()
+        hidden_states = embed_state.layer(input_ids)
+        hidden_states = self._PostLayerFunction.apply(hidden_states, embed_state, False)
+
+        cache_position = torch.arange(0, seq_length, device=hidden_states.device)
+        causal_mask = None
+        if self._update_causal_mask is not None:
+            causal_mask = self._update_causal_mask(attention_mask, hidden_states, cache_position, None, None)
+        if self.position_embeddings is None and self.rotary_emb is not None:
+            self.position_embeddings = self.rotary_emb(hidden_states, cache_position.unsqueeze(0))
+
+        num_decoder_states = len(self.layer_states) - 2
+        trace = self.runtime.log if self.runtime.trace is not None else None
+        for i in range(num_decoder_states):
+            layer_state = self.layer_states[i + 1]
+            is_last_decoder = i == num_decoder_states - 1
+            next_state = self.layer_states[i + 2]
+            hidden_states = self._PreLayerFunction.apply(hidden_states, layer_state, next_state)
+
+            def _layer_forward(h, mask, pos, layer):
+                return self._first(layer(h, attention_mask=mask, position_embeddings=pos,
+                                         output_attentions=False, use_cache=False))
+
+            if self.config.ac_offload_mode != "none":
+                with SlidingCheckpoint(layer_idx=i + 1, layer_tensors=self.layer_tensors, is_last_layer=is_last_decoder,
+                                       no_mask=attention_mask is None, device=str(self.device),
+                                       prefetch_ring=self._act_ring, trace=trace):
+                    hidden_states = checkpoint(_layer_forward, hidden_states, causal_mask, self.position_embeddings,
+                                               layer_state.layer, use_reentrant=False)
+            else:
+                hidden_states = checkpoint(_layer_forward, hidden_states, causal_mask, self.position_embeddings,
+                                           layer_state.layer, use_reentrant=False)
+            hidden_states = self._PostLayerFunction.apply(hidden_states, layer_state, is_last_decoder)
+
+        output_state = self.layer_states[-1]
+        hidden_states = self._PreLayerFunction.apply(hidden_states, output_state, None)
+        loss, logits = self.output_layer(hidden_states, labels)
+        if loss is not None:
+            loss = self._PostLayerFunction.apply(loss, output_state, True)
+            loss.backward()
+        return CausalLMOutputWithPast(loss=loss, logits=logits)
+
+    # ------------------------------------------------------------------
+    def wait_for_updates(self) -> None:
+        """Block until every queued host update has finished."""
+        for s in self.layer_states:
+            s.wait_for_update()
+
+    def update_learning_rate(self, new_lr: float) -> None:
+        if self.layer_optimizer is not None:
+            self.layer_optimizer.update_learning_rate(new_lr)
+
+    def clip_grad_norm_(self, max_norm: float) -> torch.Tensor:
+        """Reference slide_fsdp.py:651-681, including its behaviour: updates run
+        as each unit's gradients arrive, so by the time this is called every
+        ``param.grad`` has been released and the norm is taken over none."""
+        self.wait_for_updates()
+        total = 0.0
+        for s in self.layer_states:
+            for p in s.layer.parameters():
+                if p.grad is not None:
+                    total += p.grad.data.float().norm(2).item() ** 2
+        total = total ** 0.5
+        coef = max_norm / (total + 1e-6)
+        if coef < 1:
+            for s in self.layer_states:
+                for p in s.layer.parameters():
+                    if p.grad is not None:
+                        p.grad.data.mul_(coef)
+        return torch.tensor(total)
+
+    def _print_model_info(self) -> None:
+        opt_bytes = self.total_params * 4 * 2
+        print(f"\n{'=' * 60}\nSlideFSDP Model Info\n{'=' * 60}")
+        print(f"Model type: {getattr(self.model_config, 'model_type', '?')}")
+        print(f"Num decoder layers: {self.num_decoder_layers}")
+        print(f"Total parameters: {self.total_params:,}")
+        print(f"Max layer param size: {self.max_param_size:,}")
+        print(f"Param transfer mode: {self.config.param_transfer_mode}")
+        print(f"Grad sync mode: {self.config.grad_sync_mode}")
+        print(f"World size: {self.world_size}")
+        print("Estimated CPU memory:")
+        print(f"  - Parameters (FP32): {self.total_params * 4 / 1e9:.2f} GB")
+        print(f"  - Optimizer states: {opt_bytes / 1e9:.2f} GB")
+        print(f"  - Total: {(self.total_params * 4 + opt_bytes) / 1e9:.2f} GB")
+        print(f"GPU buffer pool: {self.config.gpu_buffer_pool_size} units\n{'=' * 60}\n")
+
+    def save_pretrained(self, output_dir: str) -> str:
+        """Write the model with bf16 weights (reference slide_fsdp.py:705-733),
+        then point the parameters back at their fp32 masters."""
+        os.makedirs(output_dir, exist_ok=True)
+        self.wait_for_updates()
+        saved = []
+        with torch.no_grad():
+            for s in self.layer_states:
+                for p in s.layer.parameters():
+                    saved.append((p, p.data))
+                    p.data = p.data.to(dtype=self.dtype)
+        try:
+            self.base_model.save_pretrained(output_dir)
+        finally:
+            for p, d in saved:
+                p.data = d
+        print(f"Model saved to {output_dir}")
+        return output_dir
+
+    def close(self) -> None:
+        """Finish queued work and stop the worker threads."""
+        try:
+            self.wait_for_updates()
+        finally:
+            self.runtime.shutdown()
+
+    def __del__(self):
+        rt = getattr(self, "runtime", None)
+        if rt is not None:
+            rt.offload_executor.shutdown(wait=False)
+            rt.update_executor.shutdown(wait=False)

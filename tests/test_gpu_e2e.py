@@ -1,0 +1,152 @@
+"""SlideFSDP end to end on a small Llama: staging order, update parity with the
+oracle, and loss parity with a non-offloaded PyTorch bf16 run over 10 steps."""
+
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+V, H, I, L = 1024, 256, 512, 3
+LR, BETAS, EPS, WD = 1e-3, (0.9, 0.999), 1e-8, 0.01
+
+
+def make_model():
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(vocab_size=V, hidden_size=H, intermediate_size=I, num_hidden_layers=L,
+                      num_attention_heads=8, num_key_value_heads=4, max_position_embeddings=512,
+                      rope_theta=500000.0, tie_word_embeddings=False)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(1234)
+    return LlamaForCausalLM(cfg)
+
+
+def units_of(model):
+    m = model.model
+    return [[m.embed_tokens.weight]] + [list(l.parameters()) for l in m.layers] + [[m.norm.weight, model.lm_head.weight]]
+
+
+def batches(n, B=2, S=128):
+    g = torch.Generator().manual_seed(99)
+    return [torch.randint(0, V, (B, S), generator=g) for _ in range(n)]
+
+
+def u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def test_schedule_matches_oracle(dev):
+    from test1_amd import SlideFSDP, SlideFSDPConfig
+
+    sf = SlideFSDP(make_model(), SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD))
+    ids = batches(1)[0].to(dev)
+    sf.runtime.trace = []
+    sf(input_ids=ids, labels=ids)
+    sf.wait_for_updates()
+    assert sf.runtime.trace == oracle.step_schedule(L)
+    sf.close()
+
+
+def test_updates_match_oracle_bit_exact(dev):
+    """Every unit's host update equals the oracle AdamW applied to the same
+    (captured) bf16 grads and fp32 master, for 3 steps."""
+    from test1_amd import SlideFSDP, SlideFSDPConfig
+
+    model = make_model()
+    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS))
+    orc = oracle.LayerAdamOracle(lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
+    ref_units = []
+    for ps in units_of(model):
+        arrs = [p.detach().numpy().copy() for p in ps]
+        ref_units.append(arrs)
+        orc.add_layer(arrs)
+    for ids in batches(3):
+        sf.runtime.capture = {}
+        ids = ids.to(dev)
+        sf(input_ids=ids, labels=ids)
+        sf.wait_for_updates()
+        cap = sf.runtime.capture
+        assert sorted(cap) == list(range(L + 2))
+        for u in range(L + 1, -1, -1):  # update order of the runtime
+            grads, master_before = cap[u]
+            flat_before = np.concatenate([a.reshape(-1) for a in ref_units[u]])
+            assert np.array_equal(master_before.numpy().view(np.uint32), flat_before.view(np.uint32)), f"unit {u}"
+            g = u16(grads)
+            parts, off = [], 0
+            for a in ref_units[u]:
+                parts.append(g[off:off + a.size].reshape(a.shape))
+                off += a.size
+            orc.step_layer(u, parts)
+        for u, ps in enumerate(units_of(model)):
+            for p, a in zip(ps, ref_units[u]):
+                assert np.array_equal(p.detach().numpy().view(np.uint32), a.view(np.uint32)), f"unit {u}"
+    sf.close()
+
+
+def reference_losses(model, steps_ids, dev):
+    """Non-offloaded run: bf16 model on the GPU, same loss as OutputLayer,
+    fp32 masters updated by the oracle AdamW unit by unit (last unit first)."""
+    gm = copy.deepcopy(model).to(dev, torch.bfloat16)
+    units_gpu = units_of(gm)
+    masters = [[p.detach().float().numpy().copy() for p in ps] for ps in units_of(model)]
+    orc = oracle.LayerAdamOracle(lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
+    for arrs in masters:
+        orc.add_layer(arrs)
+    losses, first_grads = [], None
+    for ids in steps_ids:
+        with torch.no_grad():
+            for ps, arrs in zip(units_gpu, masters):
+                for p, a in zip(ps, arrs):
+                    b = oracle.cast_f32_bf16(a)
+                    p.data.copy_(torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).view(p.shape))
+        ids = ids.to(dev)
+        gm.zero_grad(set_to_none=True)
+        hidden = gm.model(input_ids=ids).last_hidden_state
+        logits = gm.lm_head(hidden)
+        loss = torch.nn.functional.cross_entropy(logits[..., :-1, :].reshape(-1, V), ids[..., 1:].reshape(-1))
+        loss.backward()
+        losses.append(loss.item())
+        grads = [[u16(p.grad).reshape(p.shape) for p in ps] for ps in units_gpu]
+        if first_grads is None:
+            first_grads = grads
+        for u in range(len(units_gpu) - 1, -1, -1):
+            orc.step_layer(u, grads[u])
+    return losses, first_grads
+
+
+def test_loss_parity_with_non_offloaded_run(dev):
+    from test1_amd import SlideFSDP, SlideFSDPConfig
+
+    model = make_model()
+    steps = batches(10)
+    ref_losses, ref_grads = reference_losses(model, steps, dev)
+    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS))
+    losses = []
+    for k, ids in enumerate(steps):
+        if k == 0:
+            sf.runtime.capture = {}
+        ids = ids.to(dev)
+        losses.append(sf(input_ids=ids, labels=ids).loss.item())
+        sf.wait_for_updates()
+        if k == 0:
+            cap, sf.runtime.capture = sf.runtime.capture, None
+            for u, ref_u in enumerate(ref_grads):
+                got = u16(cap[u][0]).view(np.int16).view(np.uint16)
+                exp = np.concatenate([g.reshape(-1) for g in ref_u])
+                a = got.view(np.int16).astype(np.int32)
+                # grads of the same bf16 weights on the same kernels: report how
+                # many differ (non-deterministic reductions may flip last bits)
+                gf = torch.from_numpy(got.view(np.int16).copy()).view(torch.bfloat16).float()
+                ef = torch.from_numpy(exp.view(np.int16).copy()).view(torch.bfloat16).float()
+                assert torch.allclose(gf, ef, rtol=2e-2, atol=1e-6), f"unit {u} grads"
+    print("losses", [round(x, 5) for x in losses])
+    print("ref   ", [round(x, 5) for x in ref_losses])
+    for a, b in zip(losses, ref_losses):
+        assert abs(a - b) <= 1e-2 * abs(b), (a, b)
+    assert abs(losses[0] - ref_losses[0]) <= 1e-3 * abs(ref_losses[0])
+    sf.close()

@@ -1,0 +1,134 @@
+"""HIP kernels through the C ABI, bit-exact against the oracle."""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import GOLDEN
+from test1_amd import kernels
+from test1_amd.pinned import pinned_empty
+
+pytestmark = pytest.mark.gpu
+
+
+def bits16(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def rand_f32(n, seed, std=0.02):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(n, generator=g) * std
+
+
+@pytest.mark.parametrize("n", [0, 1, 7, 8, 9, 8191, 8192, 8193, 65536 * 4 + 3, (1 << 20) | 13])
+def test_cast_flat_matches_oracle(dev, n):
+    x = rand_f32(n, n)
+    out = torch.full((n,), 7.0, dtype=torch.bfloat16, device=dev)
+    kernels.cast_f32_bf16_(out, x.to(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(out), oracle.cast_f32_bf16(x.numpy()))
+
+
+def test_cast_golden_and_random_bit_patterns(dev):
+    d = np.load(os.path.join(GOLDEN, "cast_f32_bf16.npz"))
+    rng = np.random.default_rng(0)
+    rnd = rng.integers(0, 1 << 32, 200_003, dtype=np.uint64).astype(np.uint32)  # NaN, inf, denormals included
+    bits = np.concatenate([d["x_bits"], rnd])
+    x = torch.from_numpy(bits.view(np.float32).copy())
+    out = torch.empty(x.numel(), dtype=torch.bfloat16, device=dev)
+    kernels.cast_f32_bf16_(out, x.to(dev))
+    torch.cuda.synchronize()
+    got = bits16(out)
+    assert np.array_equal(got[: d["bf16_bits"].size], d["bf16_bits"])
+    assert np.array_equal(got, oracle.cast_f32_bf16(bits.view(np.float32)))
+
+
+@pytest.mark.parametrize("src_off,dst_off", [(1, 0), (0, 3), (5, 5), (2, 6)])
+def test_cast_unaligned_views(dev, src_off, dst_off):
+    n = 10_007
+    x = rand_f32(n + 16, 5)
+    xs = x.to(dev)
+    out = torch.zeros(n + 16, dtype=torch.bfloat16, device=dev)
+    kernels.cast_f32_bf16_(out[dst_off:dst_off + n], xs[src_off:src_off + n])
+    torch.cuda.synchronize()
+    exp = np.zeros(n + 16, np.uint16)
+    exp[dst_off:dst_off + n] = oracle.cast_f32_bf16(x.numpy()[src_off:src_off + n])
+    assert np.array_equal(bits16(out), exp)
+
+
+def test_cast_full_llama_layer(dev):
+    # one Llama-3-8B decoder layer: 218,112,000 elements, the staged unit size
+    n = 218_112_000
+    x = rand_f32(n, 42)
+    out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    kernels.cast_f32_bf16_(out, x.to(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(out), oracle.cast_f32_bf16(x.numpy()))
+
+
+def test_cast_scatter_segments(dev):
+    # 70 segments (> one launch's 64), ragged sizes, some misaligned, one empty
+    rng = np.random.default_rng(1)
+    sizes = [int(s) for s in rng.integers(0, 20_000, 70)]
+    sizes[3] = 0
+    src = rand_f32(sum(sizes) + 70, 9).to(dev)
+    dst = torch.zeros(sum(sizes) + 200, dtype=torch.bfloat16, device=dev)
+    pairs, so, do, expect = [], 0, 0, np.zeros(dst.numel(), np.uint16)
+    host = src.cpu().numpy()
+    for k, n in enumerate(sizes):
+        so += k % 3          # skew the source alignment
+        do += (k * 5) % 8    # and the destination alignment
+        pairs.append((src[so:so + n], dst[do:do + n]))
+        expect[do:do + n] = oracle.cast_f32_bf16(host[so:so + n])
+        so += n
+        do += n
+    kernels.cast_scatter_f32_bf16(pairs)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(dst), expect)
+
+
+def test_pack_unpack_round_trip(dev):
+    g = torch.Generator().manual_seed(3)
+    sizes = [16_777_216 // 64, 4096, 4096 + 3, 1, 0, 8192 * 4 + 9]
+    parts = [torch.randn(n, generator=g).bfloat16() for n in sizes]
+    dparts = [p.to(dev) for p in parts]
+    packed = torch.empty(sum(sizes) + 5, dtype=torch.bfloat16, device=dev)
+    kernels.pack_b16(dparts, packed)
+    torch.cuda.synchronize()
+    exp = oracle.pack_b16([p.view(torch.int16).numpy() for p in parts])
+    assert np.array_equal(bits16(packed)[: exp.size], exp)
+    outs = [torch.zeros_like(p) for p in dparts]
+    kernels.unpack_b16(packed, outs)
+    torch.cuda.synchronize()
+    for a, b in zip(outs, parts):
+        assert torch.equal(a.cpu().view(torch.int16), b.view(torch.int16))
+
+
+def test_copy_segs_and_fill(dev):
+    a = torch.arange(50_000, dtype=torch.int16, device=dev)
+    b = torch.zeros(60_000, dtype=torch.int16, device=dev)
+    kernels.copy_segs_b16([(a[1:10_001], b[3:10_003]), (a[20_000:20_008], b[40_000:40_008])])
+    kernels.fill_b16_(b[50_001:59_999], 0x1234)
+    torch.cuda.synchronize()
+    exp = np.zeros(60_000, np.int16)
+    exp[3:10_003] = np.arange(1, 10_001)
+    exp[40_000:40_008] = np.arange(20_000, 20_008)
+    exp[50_001:59_999] = 0x1234
+    assert np.array_equal(b.cpu().numpy(), exp)
+
+
+def test_pinned_memcpy_round_trip(dev):
+    n = 3 * (1 << 20) + 7
+    h = pinned_empty(n, torch.float32)
+    assert h.is_pinned()
+    h.copy_(rand_f32(n, 11))
+    d = torch.empty(n, dtype=torch.float32, device=dev)
+    back = pinned_empty(n, torch.float32)
+    s = torch.cuda.Stream()
+    kernels.memcpy_async(d, h, s)
+    kernels.memcpy_async(back, d, s)
+    s.synchronize()
+    assert torch.equal(back.view(torch.int32), h.view(torch.int32))

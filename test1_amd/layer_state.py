@@ -205,7 +205,9 @@ class StreamingRuntime:
         self._trace_lock = threading.Lock()
         self.d2h_timing: Optional[list] = None
         # Test hook: when a dict, each update stores {unit: (host grads, fp32
-        # master before the update)} copies, for checking against the oracle.
+        # master before the update)} and each gradient offload stores
+        # {("device_grads", unit): [param.grad clones]}, for checking the
+        # pack and the update against the oracle.
         self.capture: Optional[dict] = None
 
     def log(self, *event) -> None:
@@ -352,6 +354,9 @@ class LayerRuntimeState(nn.Module):
                 raise RuntimeError(f"unit {self.layer_idx}: grad of {name} is {g.dtype} on {g.device}, "
                                    f"expected {gbuf.dtype} on {gbuf.device}")
             pairs.append((g.detach().contiguous().reshape(-1), gbuf[off:off + size]))
+        if self.runtime.capture is not None:
+            self.runtime.capture[("device_grads", self.layer_idx)] = [
+                None if p.grad is None else p.grad.detach().clone() for p in self._params]
         # One launch gathers every gradient into its offset in the unit's
         # grad buffer; parameters that received no gradient contribute zeros,
         # as the zeroed grad buffer of the reference does (layer_state.py:297).

@@ -191,7 +191,11 @@ class SlidingCheckpoint(saved_tensors_hooks):
                 cur.wait_event(ev)
             result = bufs[self.unpack_counter]
             self.unpack_counter += 1
-            if self.no_mask or self.unpack_counter == len(bufs):
+            # Pop once every prefetched tensor of this layer has been served.
+            # (The reference pops after the first tensor when no_mask is set,
+            # sliding_checkpoint.py:128, which misroutes a layer that saves
+            # more than one tensor; the count is exact in both cases.)
+            if self.unpack_counter == len(bufs):
                 self.fifo.popleft()
             return result
 

@@ -43,7 +43,7 @@ def u16(t):
 def test_schedule_matches_oracle(dev):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
-    sf = SlideFSDP(make_model(), SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD))
+    sf = SlideFSDP(make_model(), SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD), wait_timeout=120)
     ids = batches(1)[0].to(dev)
     sf.runtime.trace = []
     sf(input_ids=ids, labels=ids)
@@ -58,7 +58,7 @@ def test_updates_match_oracle_bit_exact(dev):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model()
-    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS))
+    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS), wait_timeout=120)
     orc = oracle.LayerAdamOracle(lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
     ref_units = []
     for ps in units_of(model):
@@ -71,7 +71,12 @@ def test_updates_match_oracle_bit_exact(dev):
         sf(input_ids=ids, labels=ids)
         sf.wait_for_updates()
         cap = sf.runtime.capture
-        assert sorted(cap) == list(range(L + 2))
+        assert sorted(k for k in cap if isinstance(k, int)) == list(range(L + 2))
+        for u in range(L + 2):
+            # the packed host grads are the device grads, bit for bit, in layout order
+            dev_grads = cap[("device_grads", u)]
+            exp = oracle.pack_b16([u16(g) for g in dev_grads])
+            assert np.array_equal(u16(cap[u][0]), exp), f"unit {u} packed grads"
         for u in range(L + 1, -1, -1):  # update order of the runtime
             grads, master_before = cap[u]
             flat_before = np.concatenate([a.reshape(-1) for a in ref_units[u]])
@@ -125,7 +130,7 @@ def test_loss_parity_with_non_offloaded_run(dev):
     model = make_model()
     steps = batches(10)
     ref_losses, ref_grads = reference_losses(model, steps, dev)
-    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS))
+    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS), wait_timeout=120)
     losses = []
     for k, ids in enumerate(steps):
         if k == 0:
@@ -138,12 +143,15 @@ def test_loss_parity_with_non_offloaded_run(dev):
             for u, ref_u in enumerate(ref_grads):
                 got = u16(cap[u][0]).view(np.int16).view(np.uint16)
                 exp = np.concatenate([g.reshape(-1) for g in ref_u])
-                a = got.view(np.int16).astype(np.int32)
-                # grads of the same bf16 weights on the same kernels: report how
-                # many differ (non-deterministic reductions may flip last bits)
+                # Same bf16 weights through the same kernels; reductions with
+                # atomics (the embedding backward) may differ in the last bits,
+                # so compare in relative L2 and report the bit-exact fraction.
                 gf = torch.from_numpy(got.view(np.int16).copy()).view(torch.bfloat16).float()
                 ef = torch.from_numpy(exp.view(np.int16).copy()).view(torch.bfloat16).float()
-                assert torch.allclose(gf, ef, rtol=2e-2, atol=1e-6), f"unit {u} grads"
+                rel = ((gf - ef).norm() / ef.norm().clamp_min(1e-30)).item()
+                exact = float((got == exp).mean())
+                print(f"unit {u}: grad rel-L2 {rel:.2e}, bit-exact fraction {exact:.4f}")
+                assert rel < 1e-2, f"unit {u} grads"
     print("losses", [round(x, 5) for x in losses])
     print("ref   ", [round(x, 5) for x in ref_losses])
     for a, b in zip(losses, ref_losses):

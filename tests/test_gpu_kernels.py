@@ -74,8 +74,8 @@ def test_cast_scatter_segments(dev):
     rng = np.random.default_rng(1)
     sizes = [int(s) for s in rng.integers(0, 20_000, 70)]
     sizes[3] = 0
-    src = rand_f32(sum(sizes) + 70, 9).to(dev)
-    dst = torch.zeros(sum(sizes) + 200, dtype=torch.bfloat16, device=dev)
+    src = rand_f32(sum(sizes) + 3 * 70, 9).to(dev)
+    dst = torch.zeros(sum(sizes) + 8 * 70, dtype=torch.bfloat16, device=dev)
     pairs, so, do, expect = [], 0, 0, np.zeros(dst.numel(), np.uint16)
     host = src.cpu().numpy()
     for k, n in enumerate(sizes):

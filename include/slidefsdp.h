@@ -84,25 +84,37 @@ int sf_cast_scatter_f32_bf16(const sf_seg* segs, int nsegs,
  * Gradient and activation packing (libsf_hip.so)
  * ------------------------------------------------------------------- */
 
+/* The segment-copy entry points below take max_workgroups: <= 0 launches
+ * one workgroup per 8192-element tile (device-to-device work, all CUs);
+ * a positive value caps the grid, each workgroup then striding over tiles.
+ * A capped grid is meant for a destination in pinned host memory (the
+ * device address from sf_host_device_pointer), where a few dozen
+ * workgroups already saturate the host link and the remaining CUs stay
+ * free for compute. */
+
 /* Gather: for each segment k, copy segs[k].n 16-bit elements from
  * segs[k].src to dst + (sum of the n of segments before k).  segs[k].dst
  * is ignored.  Packs a layer's per-parameter bf16 gradients into one
- * contiguous buffer that a single D2H copy can move; it replaces the
+ * contiguous buffer -- with dst in pinned host memory, straight into the
+ * host staging slot, so the pack and the D2H are one kernel.  Replaces the
  * per-parameter grad views into the shared grad buffer that
- * layer_state.py:250 and :321-322 set up and the D2H at
- * distributed_sync.py:353 reads. */
+ * layer_state.py:250 and :321-322 set up plus the D2H at
+ * distributed_sync.py:353. */
 int sf_pack_b16(const sf_seg* segs, int nsegs, uint16_t* dst,
-                sf_stream_t stream);
+                int max_workgroups, sf_stream_t stream);
 
 /* Scatter, the inverse of sf_pack_b16: for each segment k, copy segs[k].n
  * elements from src + (sum of earlier n) to segs[k].dst.  segs[k].src is
  * ignored.  Restores packed checkpoint tensors (sliding_checkpoint.py:
  * 104-105) when they were packed from non-contiguous sources. */
 int sf_unpack_b16(const uint16_t* src, const sf_seg* segs, int nsegs,
-                  sf_stream_t stream);
+                  int max_workgroups, sf_stream_t stream);
 
-/* General 16-bit segment copy: both addresses taken from each segment. */
-int sf_copy_segs_b16(const sf_seg* segs, int nsegs, sf_stream_t stream);
+/* General 16-bit segment copy: both addresses taken from each segment.
+ * Also packs checkpoint tensors into their pinned host slots
+ * (sliding_checkpoint.py:69-73). */
+int sf_copy_segs_b16(const sf_seg* segs, int nsegs, int max_workgroups,
+                     sf_stream_t stream);
 
 /* dst[i] = value for i < n (16-bit elements), as a kernel rather than a
  * memset node so it is safe inside captured graphs.  Replaces
@@ -133,6 +145,10 @@ int sf_memcpy_async(void* dst, const void* src, size_t bytes, int kind,
  * 480-503). */
 int sf_host_alloc(void** out, size_t bytes);
 int sf_host_free(void* ptr);
+
+/* Device-side address of pinned host memory, for kernels that read or
+ * write host memory directly (hipHostGetDevicePointer). */
+int sf_host_device_pointer(void* host_ptr, void** device_ptr);
 
 /* ---------------------------------------------------------------------
  * Host AdamW (libsf_cpu.so)

@@ -224,7 +224,7 @@ class LayerAdamOracle:
 # Unit schedule of one training step
 # ---------------------------------------------------------------------------
 
-def step_schedule(num_decoders: int, act_offload: bool = True) -> List[Tuple]:
+def step_schedule(num_decoders: int, act_offload: bool = True, first_decoder_first: bool = False) -> List[Tuple]:
     """Expected order of staging events for one training step of a model with
     ``num_decoders`` decoder layers, units numbered 0 (embedding),
     1..L (decoders), L+1 (norm + lm_head).
@@ -246,10 +246,14 @@ def step_schedule(num_decoders: int, act_offload: bool = True) -> List[Tuple]:
     unit's gradients is triggered after all of its gradients exist, not by
     the first parameter's pre-hook (slide_fsdp.py:419-430), which fires
     before the unit's backward is complete; the order of events is the same.
+    ``first_decoder_first`` swaps the two initial loads (an ordering the
+    reference does not use; the set of events is unchanged).
     Parity unpinned beyond this restatement: the reference has no tests.
     """
     L = num_decoders
     out: List[Tuple] = [("h2d", 0, False), ("h2d", 1, False)]
+    if first_decoder_first:
+        out.reverse()
     for i in range(1, L + 1):
         nxt = i + 1
         out.append(("h2d", nxt, nxt == L + 1))

@@ -59,13 +59,14 @@ HIP_SIGNATURES = {
     "sf_abi_version": [],
     "sf_cast_f32_bf16": [_vp, _vp, _sz, _vp],
     "sf_cast_scatter_f32_bf16": [ctypes.POINTER(SfSeg), _i, _vp],
-    "sf_pack_b16": [ctypes.POINTER(SfSeg), _i, _vp, _vp],
-    "sf_unpack_b16": [_vp, ctypes.POINTER(SfSeg), _i, _vp],
-    "sf_copy_segs_b16": [ctypes.POINTER(SfSeg), _i, _vp],
+    "sf_pack_b16": [ctypes.POINTER(SfSeg), _i, _vp, _i, _vp],
+    "sf_unpack_b16": [_vp, ctypes.POINTER(SfSeg), _i, _i, _vp],
+    "sf_copy_segs_b16": [ctypes.POINTER(SfSeg), _i, _i, _vp],
     "sf_fill_b16": [_vp, _sz, ctypes.c_uint16, _vp],
     "sf_memcpy_async": [_vp, _vp, _sz, _i, _vp],
     "sf_host_alloc": [ctypes.POINTER(_vp), _sz],
     "sf_host_free": [_vp],
+    "sf_host_device_pointer": [_vp, ctypes.POINTER(_vp)],
 }
 
 CPU_SIGNATURES = {

@@ -162,36 +162,41 @@ struct OpCopy16 {
 template <typename Op>
 __global__ __launch_bounds__(kThreads) void seg_kernel(const SegTable t) {
     using S = typename Op::S;
-    const uint64_t tile = blockIdx.x;
-    const uint32_t s = find_seg(t, tile);
-    const uint64_t first = (tile - t.tile_start[s]) * kTileElems;  // element offset in segment
-    const uint64_t n = t.n[s];
-    const uint64_t len = (n - first < kTileElems) ? (n - first) : kTileElems;
-    const S* src = reinterpret_cast<const S*>(t.src[s]) + first;
-    uint16_t* dst = reinterpret_cast<uint16_t*>(t.dst[s]) + first;
+    const uint64_t ntiles = t.tile_start[t.nsegs];
+    // Grid-stride over tiles: one workgroup per tile when the grid covers
+    // them all, or a capped grid (e.g. a copy into host memory, which only
+    // needs enough workgroups to keep the host link busy).
+    for (uint64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const uint32_t s = find_seg(t, tile);
+        const uint64_t first = (tile - t.tile_start[s]) * kTileElems;  // element offset in segment
+        const uint64_t n = t.n[s];
+        const uint64_t len = (n - first < kTileElems) ? (n - first) : kTileElems;
+        const S* src = reinterpret_cast<const S*>(t.src[s]) + first;
+        uint16_t* dst = reinterpret_cast<uint16_t*>(t.dst[s]) + first;
 
-    const bool aligned = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) &
-                          (Op::kAlign - 1)) == 0;
-    if (aligned && len == kTileElems) {
-        // Full aligned tile: unpredicated loads, all in flight together.
-        u32x4 v[kUnroll];
+        const bool aligned = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) &
+                              (Op::kAlign - 1)) == 0;
+        if (aligned && len == kTileElems) {
+            // Full aligned tile: unpredicated loads, all in flight together.
+            u32x4 v[kUnroll];
 #pragma unroll
-        for (int k = 0; k < kUnroll; ++k) v[k] = Op::load_convert(src + (k * kThreads + threadIdx.x) * kGroup);
+            for (int k = 0; k < kUnroll; ++k) v[k] = Op::load_convert(src + (k * kThreads + threadIdx.x) * kGroup);
 #pragma unroll
-        for (int k = 0; k < kUnroll; ++k)
-            __builtin_nontemporal_store(v[k], reinterpret_cast<u32x4*>(dst + (k * kThreads + threadIdx.x) * kGroup));
-    } else if (aligned) {
-        // Last tile of a segment: predicated groups, then the < 8 element tail.
-        const uint64_t n8 = len / kGroup;
-        for (int k = 0; k < kUnroll; ++k) {
-            const uint64_t g = k * kThreads + threadIdx.x;
-            if (g < n8) __builtin_nontemporal_store(Op::load_convert(src + g * kGroup),
-                                                    reinterpret_cast<u32x4*>(dst + g * kGroup));
+            for (int k = 0; k < kUnroll; ++k)
+                __builtin_nontemporal_store(v[k], reinterpret_cast<u32x4*>(dst + (k * kThreads + threadIdx.x) * kGroup));
+        } else if (aligned) {
+            // Last tile of a segment: predicated groups, then the < 8 element tail.
+            const uint64_t n8 = len / kGroup;
+            for (int k = 0; k < kUnroll; ++k) {
+                const uint64_t g = k * kThreads + threadIdx.x;
+                if (g < n8) __builtin_nontemporal_store(Op::load_convert(src + g * kGroup),
+                                                        reinterpret_cast<u32x4*>(dst + g * kGroup));
+            }
+            const uint64_t rem = len - n8 * kGroup;
+            if (threadIdx.x < rem) dst[n8 * kGroup + threadIdx.x] = Op::convert1(src[n8 * kGroup + threadIdx.x]);
+        } else {
+            for (uint64_t i = threadIdx.x; i < len; i += kThreads) dst[i] = Op::convert1(src[i]);
         }
-        const uint64_t rem = len - n8 * kGroup;
-        if (threadIdx.x < rem) dst[n8 * kGroup + threadIdx.x] = Op::convert1(src[n8 * kGroup + threadIdx.x]);
-    } else {
-        for (uint64_t i = threadIdx.x; i < len; i += kThreads) dst[i] = Op::convert1(src[i]);
     }
 }
 
@@ -202,7 +207,7 @@ inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 constexpr uint64_t kMaxBlocks = (uint64_t(1) << 31) / kThreads;
 
 template <typename Op>
-int launch_segs(const sf_seg* segs, int nsegs, hipStream_t stream) {
+int launch_segs(const sf_seg* segs, int nsegs, int max_workgroups, hipStream_t stream) {
     if (nsegs < 0 || (nsegs > 0 && segs == nullptr)) return SF_EINVAL;
     // Tables longer than SF_MAX_SEGS are split into several launches.
     for (int base = 0; base < nsegs; base += SF_MAX_SEGS) {
@@ -226,7 +231,9 @@ int launch_segs(const sf_seg* segs, int nsegs, hipStream_t stream) {
         t.tile_start[m] = tiles;
         t.nsegs = m;
         if (tiles > kMaxBlocks) return SF_EINVAL;  // > 17.6e12 elements: not a real layer
-        hipLaunchKernelGGL(seg_kernel<Op>, dim3(uint32_t(tiles)), dim3(kThreads), 0, stream, t);
+        uint64_t grid = tiles;
+        if (max_workgroups > 0 && grid > uint64_t(max_workgroups)) grid = uint64_t(max_workgroups);
+        hipLaunchKernelGGL(seg_kernel<Op>, dim3(uint32_t(grid)), dim3(kThreads), 0, stream, t);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return int(e);
     }
@@ -281,14 +288,14 @@ int sf_cast_f32_bf16(const float* src, uint16_t* dst, size_t n, sf_stream_t stre
 }
 
 int sf_cast_scatter_f32_bf16(const sf_seg* segs, int nsegs, sf_stream_t stream) {
-    return launch_segs<OpCast>(segs, nsegs, reinterpret_cast<hipStream_t>(stream));
+    return launch_segs<OpCast>(segs, nsegs, 0, reinterpret_cast<hipStream_t>(stream));
 }
 
-int sf_copy_segs_b16(const sf_seg* segs, int nsegs, sf_stream_t stream) {
-    return launch_segs<OpCopy16>(segs, nsegs, reinterpret_cast<hipStream_t>(stream));
+int sf_copy_segs_b16(const sf_seg* segs, int nsegs, int max_workgroups, sf_stream_t stream) {
+    return launch_segs<OpCopy16>(segs, nsegs, max_workgroups, reinterpret_cast<hipStream_t>(stream));
 }
 
-int sf_pack_b16(const sf_seg* segs, int nsegs, uint16_t* dst, sf_stream_t stream) {
+int sf_pack_b16(const sf_seg* segs, int nsegs, uint16_t* dst, int max_workgroups, sf_stream_t stream) {
     if (nsegs < 0 || (nsegs > 0 && (segs == nullptr || dst == nullptr))) return SF_EINVAL;
     sf_seg local[SF_MAX_SEGS];
     uint64_t off = 0;
@@ -300,13 +307,14 @@ int sf_pack_b16(const sf_seg* segs, int nsegs, uint16_t* dst, sf_stream_t stream
             local[i].n = segs[base + i].n;
             off += segs[base + i].n;
         }
-        int rc = launch_segs<OpCopy16>(local, cnt, reinterpret_cast<hipStream_t>(stream));
+        int rc = launch_segs<OpCopy16>(local, cnt, max_workgroups, reinterpret_cast<hipStream_t>(stream));
         if (rc != SF_OK) return rc;
     }
     return SF_OK;
 }
 
-int sf_unpack_b16(const uint16_t* src, const sf_seg* segs, int nsegs, sf_stream_t stream) {
+int sf_unpack_b16(const uint16_t* src, const sf_seg* segs, int nsegs, int max_workgroups,
+                  sf_stream_t stream) {
     if (nsegs < 0 || (nsegs > 0 && (segs == nullptr || src == nullptr))) return SF_EINVAL;
     sf_seg local[SF_MAX_SEGS];
     uint64_t off = 0;
@@ -318,7 +326,7 @@ int sf_unpack_b16(const uint16_t* src, const sf_seg* segs, int nsegs, sf_stream_
             local[i].n = segs[base + i].n;
             off += segs[base + i].n;
         }
-        int rc = launch_segs<OpCopy16>(local, cnt, reinterpret_cast<hipStream_t>(stream));
+        int rc = launch_segs<OpCopy16>(local, cnt, max_workgroups, reinterpret_cast<hipStream_t>(stream));
         if (rc != SF_OK) return rc;
     }
     return SF_OK;
@@ -372,6 +380,12 @@ int sf_host_alloc(void** out, size_t bytes) {
 int sf_host_free(void* ptr) {
     if (ptr == nullptr) return SF_OK;
     return int(hipHostFree(ptr));
+}
+
+int sf_host_device_pointer(void* host_ptr, void** device_ptr) {
+    if (host_ptr == nullptr || device_ptr == nullptr) return SF_EINVAL;
+    *device_ptr = nullptr;
+    return int(hipHostGetDevicePointer(device_ptr, host_ptr, 0));
 }
 
 }  // extern "C"

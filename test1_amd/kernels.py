@@ -76,17 +76,35 @@ def cast_scatter_f32_bf16(pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]],
                   "sf_cast_scatter_f32_bf16")
 
 
-def _check_b16(t: torch.Tensor, what: str) -> None:
+def _check_b16(t: torch.Tensor, what: str, host_ok: bool = False) -> None:
     if t.dtype not in _B16:
         raise TypeError(f"{what}: need a 16-bit dtype, got {t.dtype}")
-    _require_cuda(t, what)
+    if host_ok and t.device.type == "cpu":
+        if not t.is_pinned():
+            raise ValueError(f"{what}: a host tensor must be pinned to be written by a kernel")
+    else:
+        _require_cuda(t, what)
     _require_contig(t, what)
 
 
+def device_address(t: torch.Tensor) -> int:
+    """Address at which a kernel reaches ``t``: its data pointer for a GPU
+    tensor, the mapped device address of pinned host memory otherwise."""
+    if t.device.type == "cuda":
+        return t.data_ptr()
+    base = t.untyped_storage().data_ptr()
+    dev = ctypes.c_void_p()
+    _native.check(_native.hip().sf_host_device_pointer(ctypes.c_void_p(base), ctypes.byref(dev)),
+                  "sf_host_device_pointer")
+    return dev.value + (t.data_ptr() - base)
+
+
 def pack_b16(srcs: Sequence[torch.Tensor], dst: torch.Tensor,
-             stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
-    """dst[off_k : off_k + n_k] = srcs[k].flatten(), offsets in order from 0."""
-    _check_b16(dst, "dst")
+             stream: Optional[torch.cuda.Stream] = None, max_workgroups: int = 0) -> torch.Tensor:
+    """dst[off_k : off_k + n_k] = srcs[k].flatten(), offsets in order from 0.
+
+    ``dst`` may be pinned host memory (then pass a small ``max_workgroups``)."""
+    _check_b16(dst, "dst", host_ok=True)
     total = 0
     segs = []
     for k, s in enumerate(srcs):
@@ -96,31 +114,35 @@ def pack_b16(srcs: Sequence[torch.Tensor], dst: torch.Tensor,
     if total > dst.numel():
         raise ValueError(f"pack_b16: {total} elements do not fit in dst of {dst.numel()}")
     arr = _seg_array(segs)
-    _native.check(_native.hip().sf_pack_b16(arr, len(segs), dst.data_ptr(), _stream_ptr(stream)), "sf_pack_b16")
+    _native.check(_native.hip().sf_pack_b16(arr, len(segs), device_address(dst), int(max_workgroups),
+                                            _stream_ptr(stream)), "sf_pack_b16")
     return dst
 
 
 def copy_segs_b16(pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]],
-                  stream: Optional[torch.cuda.Stream] = None) -> None:
-    """For each (src, dst) pair of contiguous 16-bit GPU tensors of equal numel,
-    dst = src, all in one launch."""
+                  stream: Optional[torch.cuda.Stream] = None, max_workgroups: int = 0) -> None:
+    """For each (src, dst) pair of contiguous 16-bit tensors of equal numel,
+    dst = src, all in one launch.  Sources are GPU tensors; destinations are
+    GPU tensors or pinned host tensors."""
     segs = []
     for k, (src, dst) in enumerate(pairs):
         _check_b16(src, f"pair {k} src")
-        _check_b16(dst, f"pair {k} dst")
+        _check_b16(dst, f"pair {k} dst", host_ok=True)
         if src.numel() != dst.numel():
             raise ValueError(f"pair {k}: numel mismatch {src.numel()} vs {dst.numel()}")
-        segs.append((src.data_ptr(), dst.data_ptr(), src.numel()))
+        segs.append((src.data_ptr(), device_address(dst), src.numel()))
     if not segs:
         return
     arr = _seg_array(segs)
-    _native.check(_native.hip().sf_copy_segs_b16(arr, len(segs), _stream_ptr(stream)), "sf_copy_segs_b16")
+    _native.check(_native.hip().sf_copy_segs_b16(arr, len(segs), int(max_workgroups), _stream_ptr(stream)),
+                  "sf_copy_segs_b16")
 
 
 def unpack_b16(src: torch.Tensor, dsts: Sequence[torch.Tensor],
-               stream: Optional[torch.cuda.Stream] = None) -> None:
-    """dsts[k].flatten() = src[off_k : off_k + n_k], the inverse of pack_b16."""
-    _check_b16(src, "src")
+               stream: Optional[torch.cuda.Stream] = None, max_workgroups: int = 0) -> None:
+    """dsts[k].flatten() = src[off_k : off_k + n_k], the inverse of pack_b16.
+    ``src`` may be pinned host memory."""
+    _check_b16(src, "src", host_ok=True)
     total = 0
     segs = []
     for k, d in enumerate(dsts):
@@ -130,8 +152,8 @@ def unpack_b16(src: torch.Tensor, dsts: Sequence[torch.Tensor],
     if total > src.numel():
         raise ValueError(f"unpack_b16: src of {src.numel()} holds fewer than {total} elements")
     arr = _seg_array(segs)
-    _native.check(_native.hip().sf_unpack_b16(src.data_ptr(), arr, len(segs), _stream_ptr(stream)),
-                  "sf_unpack_b16")
+    _native.check(_native.hip().sf_unpack_b16(device_address(src), arr, len(segs), int(max_workgroups),
+                                              _stream_ptr(stream)), "sf_unpack_b16")
 
 
 def fill_b16_(dst: torch.Tensor, value: int = 0, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:

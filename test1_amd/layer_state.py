@@ -94,13 +94,28 @@ class LayerBufferPool:
             return len(self.pool)
 
 
+class _StageTicket:
+    """Chunks of one unit's master in flight through the staging ring."""
+
+    def __init__(self, host: torch.Tensor, chunks: List[Tuple[int, int]]):
+        self.host = host
+        self.chunks = chunks          # (offset, elements) per chunk
+        self.slots: List[int] = []    # staging slot of each issued copy
+        self.copied: List[torch.cuda.Event] = []
+
+
 class H2DStager:
     """Pinned fp32 master -> device bf16 unit, through a device fp32 ring.
 
-    Each chunk: DMA into slot s on ``h2d_stream`` (after the cast that last
-    read slot s), then the cast kernel on ``cast_stream``.  Copies of later
-    chunks and layers keep the host link busy while earlier chunks are cast
-    or while a cast waits for its unit to become free.
+    Two phases, so the host link never waits for a pool unit:
+      ``begin``   issues the DMA copies of the first ``depth`` chunks into
+                  free ring slots on ``h2d_stream`` (each after the cast that
+                  last read its slot) -- no pool unit is needed for this;
+      ``finish``  once the caller holds a unit, casts each chunk into it on
+                  ``cast_stream`` (after the unit's ``ready`` event and the
+                  chunk's copy) and issues the remaining copies as slots free.
+    One unit is staged at a time: ``begin`` takes a lock that ``finish``
+    releases.
     """
 
     def __init__(self, device: torch.device, chunk_elems: int, depth: int,
@@ -116,46 +131,76 @@ class H2DStager:
         self.cast_stream = cast_stream
         self._lock = threading.Lock()
         # Optional instrumentation: when a list, each cast appends
-        # (start_event, end_event, n_elements); each copy appends to copy_timing.
+        # (start_event, end_event, n_elements); each copy appends
+        # (start_event, end_event, bytes) to copy_timing.
         self.cast_timing: Optional[list] = None
         self.copy_timing: Optional[list] = None
 
-    def load(self, host_f32: torch.Tensor, dst_bf16: torch.Tensor,
-             wait_event: Optional[torch.cuda.Event]) -> torch.cuda.Event:
-        n = host_f32.numel()
-        if dst_bf16.numel() < n:
-            raise ValueError("H2DStager.load: destination smaller than source")
-        with self._lock:
+    def _slot(self, s: int, c: int) -> torch.Tensor:
+        return self.buf[s * self.chunk: s * self.chunk + c]
+
+    def _issue_copy(self, t: _StageTicket, j: int) -> None:
+        off, c = t.chunks[j]
+        s = self.next_slot
+        self.next_slot = (s + 1) % self.depth
+        if self.slot_free[s] is not None:
+            self.h2d_stream.wait_event(self.slot_free[s])
+        timing = self.copy_timing is not None
+        if timing:
+            t0 = torch.cuda.Event(enable_timing=True)
+            t0.record(self.h2d_stream)
+        kernels.memcpy_async(self._slot(s, c), t.host[off:off + c], self.h2d_stream)
+        copied = torch.cuda.Event(enable_timing=True) if timing else _new_event()
+        copied.record(self.h2d_stream)
+        if timing:
+            self.copy_timing.append((t0, copied, c * 4))
+        t.slots.append(s)
+        t.copied.append(copied)
+
+    def begin(self, host_f32: torch.Tensor) -> _StageTicket:
+        self._lock.acquire()
+        try:
+            n = host_f32.numel()
+            t = _StageTicket(host_f32, [(off, min(self.chunk, n - off)) for off in range(0, n, self.chunk)])
+            for j in range(min(len(t.chunks), self.depth)):
+                self._issue_copy(t, j)
+            return t
+        except BaseException:
+            self._lock.release()
+            raise
+
+    def finish(self, t: _StageTicket, dst_bf16: torch.Tensor,
+               wait_event: Optional[torch.cuda.Event]) -> torch.cuda.Event:
+        try:
+            if dst_bf16.numel() < t.host.numel():
+                raise ValueError("H2DStager.finish: destination smaller than source")
             if wait_event is not None:
                 self.cast_stream.wait_event(wait_event)
-            for off in range(0, n, self.chunk):
-                c = min(self.chunk, n - off)
-                s = self.next_slot
-                self.next_slot = (s + 1) % self.depth
-                slot = self.buf[s * self.chunk: s * self.chunk + c]
-                if self.slot_free[s] is not None:
-                    self.h2d_stream.wait_event(self.slot_free[s])
-                if self.copy_timing is not None:
-                    t0 = torch.cuda.Event(enable_timing=True)
-                    t0.record(self.h2d_stream)
-                kernels.memcpy_async(slot, host_f32[off:off + c], self.h2d_stream)
-                copied = _new_event() if self.copy_timing is None else torch.cuda.Event(enable_timing=True)
-                copied.record(self.h2d_stream)
-                if self.copy_timing is not None:
-                    self.copy_timing.append((t0, copied, c * 4))
-                self.cast_stream.wait_event(copied)
-                if self.cast_timing is not None:
+            timing = self.cast_timing is not None
+            for j, (off, c) in enumerate(t.chunks):
+                s = t.slots[j]
+                self.cast_stream.wait_event(t.copied[j])
+                if timing:
                     c0 = torch.cuda.Event(enable_timing=True)
                     c0.record(self.cast_stream)
-                kernels.cast_f32_bf16_(dst_bf16[off:off + c], slot, self.cast_stream)
-                freed = _new_event() if self.cast_timing is None else torch.cuda.Event(enable_timing=True)
+                kernels.cast_f32_bf16_(dst_bf16[off:off + c], self._slot(s, c), self.cast_stream)
+                freed = torch.cuda.Event(enable_timing=True) if timing else _new_event()
                 freed.record(self.cast_stream)
-                if self.cast_timing is not None:
+                if timing:
                     self.cast_timing.append((c0, freed, c))
                 self.slot_free[s] = freed
+                if j + self.depth < len(t.chunks):
+                    self._issue_copy(t, j + self.depth)  # reuses slot s, after this cast
             done = _new_event()
             done.record(self.cast_stream)
             return done
+        finally:
+            self._lock.release()
+
+    def load(self, host_f32: torch.Tensor, dst_bf16: torch.Tensor,
+             wait_event: Optional[torch.cuda.Event]) -> torch.cuda.Event:
+        """``begin`` and ``finish`` in one call."""
+        return self.finish(self.begin(host_f32), dst_bf16, wait_event)
 
 
 class GradStagingRing:
@@ -187,8 +232,13 @@ class StreamingRuntime:
     ring, worker threads and the optional event trace."""
 
     def __init__(self, device: torch.device, dtype: torch.dtype, max_param_size: int, pool_size: int,
-                 stage_chunk_elems: int, stage_depth: int, grad_ring_depth: int, wait_timeout: Optional[float]):
+                 stage_chunk_elems: int, stage_depth: int, grad_ring_depth: int, wait_timeout: Optional[float],
+                 d2h_workgroups: int = 64):
         self.device = device
+        # Workgroups of the kernels that write into pinned host memory (grad
+        # and checkpoint offload): enough to keep the host link busy, few
+        # enough to leave the CUs to the layer compute.
+        self.d2h_workgroups = d2h_workgroups
         self.h2d_stream = torch.cuda.Stream(device=device)
         self.cast_stream = torch.cuda.Stream(device=device)
         self.d2h_stream = torch.cuda.Stream(device=device)
@@ -249,9 +299,15 @@ class LayerRuntimeState(nn.Module):
         self._current_gpu_cache: Optional[Dict[str, Any]] = None
         self._post_called = False
         self._bwd_armed = False
+        self._bwd_compute_done = False
+        self._grads_offloaded = False
 
         params = list(self.layer.parameters())
         self.total_size = sum(p.numel() for p in params)
+        # Units whose backward does not read their parameters skip the reload
+        # before their backward (the reference reloads every unit,
+        # slide_fsdp.py:443-444).
+        self.backward_reads_params = not isinstance(self.layer, nn.Embedding)
         self._cpu_params_flat = pinned_empty(self.total_size, torch.float32)
         self._param_maps: "OrderedDict[str, Tuple[int, torch.Size, int]]" = OrderedDict()
         self._param_views: "OrderedDict[str, torch.Tensor]" = OrderedDict()
@@ -299,17 +355,38 @@ class LayerRuntimeState(nn.Module):
         """Start loading this unit; returns once the work is enqueued.
 
         Waits on the host only for this unit's previous update (so the master
-        is current) and for a free pool unit.
+        is current) and then for a free pool unit; the fp32 copies into the
+        staging ring are issued before the pool wait, so the host link keeps
+        streaming while an earlier unit is still busy.
         """
         if self._current_gpu_cache is not None:
             return  # already resident (last decoder / output unit)
         self.wait_for_update()
-        unit = self.buffer_pool.acquire(timeout=self.runtime.wait_timeout)
-        self._h2d_done = self.runtime.stager.load(self._cpu_params_flat, unit["param"], unit["ready"])
+        stager = self.runtime.stager
+        # The backward of an embedding never reads its weights (its gradient
+        # depends only on the indices), so no copy or cast is needed then.
+        ticket = None if (is_backward and not self.backward_reads_params) else stager.begin(self._cpu_params_flat)
+        try:
+            unit = self.buffer_pool.acquire(timeout=self.runtime.wait_timeout)
+        except BaseException:
+            if ticket is not None:
+                stager.finish(ticket, self._dummy_dst(), None)
+            raise
+        if ticket is None:
+            self._h2d_done = unit["ready"]   # keep the release fence of the unit
+        else:
+            self._h2d_done = stager.finish(ticket, unit["param"], unit["ready"])
         unit["ready"] = None
         self._bind_device_views(unit)
         self._current_gpu_cache = unit
+        self._bwd_compute_done = False
+        self._grads_offloaded = False
         self.runtime.log("h2d", self.layer_idx, is_backward)
+
+    def _dummy_dst(self) -> torch.Tensor:
+        # Only used to drain a staging ticket after a failed acquire: casts
+        # into a scratch buffer so the ring's slot events stay consistent.
+        return torch.empty(self.total_size, dtype=torch.bfloat16, device=self.runtime.device)
 
     def wait_for_h2d(self, timeout: Optional[float] = None) -> None:
         """Make the current stream wait for this unit's load (no host block)."""
@@ -325,10 +402,14 @@ class LayerRuntimeState(nn.Module):
         its gradients after its backward (``is_backward=True``).
 
         Forward: the unit becomes reusable once the current stream has passed
-        this point.  Backward: pack the gradients on the current stream, then
-        hand the D2H and update to the worker threads.  ``prev_update`` is
-        accepted for signature compatibility; the two-slot grad ring makes it
-        unnecessary.
+        this point.  Backward: the gradients are handed to the offload thread,
+        which packs them with one kernel straight into a pinned host slot on
+        ``d2h_stream``, and the update is queued behind it.  The pool unit is
+        released separately, by ``mark_backward_compute_done`` and this call
+        together (whichever comes last), because the unit's weights may still
+        be read by backward kernels enqueued after its last gradient.
+        ``prev_update`` is accepted for signature compatibility; the grad ring
+        makes it unnecessary.
         """
         unit = self._current_gpu_cache
         if unit is None:
@@ -343,58 +424,74 @@ class LayerRuntimeState(nn.Module):
             self.buffer_pool.release(unit)
             return
 
-        gbuf = unit["grad"]
-        pairs, missing = [], []
+        grads, missing = [], []
         for (name, (off, shape, size)), p in self._named():
             g = p.grad
             if g is None:
                 missing.append((off, size))
                 continue
-            if g.dtype != gbuf.dtype or g.device != gbuf.device:
+            if g.dtype != unit["param"].dtype or g.device != unit["param"].device:
                 raise RuntimeError(f"unit {self.layer_idx}: grad of {name} is {g.dtype} on {g.device}, "
-                                   f"expected {gbuf.dtype} on {gbuf.device}")
-            pairs.append((g.detach().contiguous().reshape(-1), gbuf[off:off + size]))
+                                   f"expected {unit['param'].dtype} on {unit['param'].device}")
+            grads.append((g.detach().contiguous().reshape(-1), off))
         if self.runtime.capture is not None:
             self.runtime.capture[("device_grads", self.layer_idx)] = [
                 None if p.grad is None else p.grad.detach().clone() for p in self._params]
-        # One launch gathers every gradient into its offset in the unit's
-        # grad buffer; parameters that received no gradient contribute zeros,
-        # as the zeroed grad buffer of the reference does (layer_state.py:297).
-        kernels.copy_segs_b16(pairs, cur)
-        for off, size in missing:
-            kernels.fill_b16_(gbuf[off:off + size], 0, cur)
         grad_ready = _new_event()
         grad_ready.record(cur)
-        # The grads were produced on the current stream and are read there by
-        # the pack kernel; dropping them now lets the allocator reuse them in
-        # stream order.
-        self._bind_host_views()
-        self._current_gpu_cache = None
+        for p in self._params:
+            p.grad = None
         self.update_finished.clear()
         self.runtime.log("d2h", self.layer_idx)
-        self._d2h_future = self.runtime.offload_executor.submit(self._d2h_task, unit, grad_ready)
+        self._d2h_future = self.runtime.offload_executor.submit(self._d2h_task, grads, missing, grad_ready)
+        self._grads_offloaded = True
+        self._maybe_release_after_backward()
 
-    def _d2h_task(self, unit: Dict[str, Any], grad_ready: torch.cuda.Event) -> None:
+    def mark_backward_compute_done(self) -> None:
+        """Every backward kernel that reads this unit's weights has been
+        enqueued on the current stream (called when the gradient has flowed
+        past the unit's first operation)."""
+        if self._current_gpu_cache is None:
+            return
+        self._bwd_compute_done = True
+        self._maybe_release_after_backward()
+
+    def _maybe_release_after_backward(self) -> None:
+        unit = self._current_gpu_cache
+        if unit is None or not (self._bwd_compute_done and self._grads_offloaded):
+            return
+        ev = _new_event()
+        ev.record(torch.cuda.current_stream())
+        unit["ready"] = ev
+        self._bind_host_views()
+        self._current_gpu_cache = None
+        self.buffer_pool.release(unit)
+
+    def _d2h_task(self, grads: List[Tuple[torch.Tensor, int]], missing: List[Tuple[int, int]],
+                  grad_ready: torch.cuda.Event) -> None:
         rt = self.runtime
         slot = rt.grad_ring.acquire(timeout=rt.wait_timeout)
         try:
             host = rt.grad_ring.slots[slot]
             rt.d2h_stream.wait_event(grad_ready)
-            if rt.d2h_timing is not None:
+            timing = rt.d2h_timing is not None
+            if timing:
                 t0 = torch.cuda.Event(enable_timing=True)
                 t0.record(rt.d2h_stream)
-            kernels.memcpy_async(host[:self.total_size], unit["grad"][:self.total_size], rt.d2h_stream)
-            done = _new_event() if rt.d2h_timing is None else torch.cuda.Event(enable_timing=True)
+            kernels.copy_segs_b16([(g, host[off:off + g.numel()]) for g, off in grads], rt.d2h_stream,
+                                  max_workgroups=rt.d2h_workgroups)
+            for g, _ in grads:
+                g.record_stream(rt.d2h_stream)
+            done = torch.cuda.Event(enable_timing=True) if timing else _new_event()
             done.record(rt.d2h_stream)
-            if rt.d2h_timing is not None:
-                rt.d2h_timing.append((t0, done, self.total_size * 2))
+            if timing:
+                rt.d2h_timing.append((t0, done, 2 * sum(g.numel() for g, _ in grads)))
         except BaseException:
             rt.grad_ring.release(slot)
-            self.buffer_pool.release(unit)
+            self.update_finished.set()
             raise
-        unit["ready"] = done
-        self.buffer_pool.release(unit)
-        self._update_future = rt.update_executor.submit(self._do_update, slot, done)
+        del grads
+        self._update_future = rt.update_executor.submit(self._do_update, slot, done, missing)
 
     def wait_for_d2h(self, timeout: Optional[float] = None) -> None:
         """Wait until the gradient offload has been issued (and re-raise its
@@ -411,10 +508,14 @@ class LayerRuntimeState(nn.Module):
             views[p] = host[off:off + size].view(shape)
         return views
 
-    def _do_update(self, slot: int, d2h_done: torch.cuda.Event) -> bool:
+    def _do_update(self, slot: int, d2h_done: torch.cuda.Event, missing: List[Tuple[int, int]]) -> bool:
         rt = self.runtime
         try:
             d2h_done.synchronize()
+            for off, size in missing:
+                # a parameter that received no gradient: zeros, as the zeroed
+                # grad buffer of the reference gives it (layer_state.py:297)
+                rt.grad_ring.slots[slot][off:off + size].zero_()
             if rt.capture is not None:
                 rt.capture[self.layer_idx] = (rt.grad_ring.slots[slot][:self.total_size].clone(),
                                               self._cpu_params_flat.clone())

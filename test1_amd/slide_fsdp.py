@@ -90,14 +90,15 @@ class SlideFSDP(nn.Module):
     Extra keyword arguments (all optional, not in the reference):
       stage_chunk_elems  fp32 elements per H2D staging chunk (default: the
                          largest unit, i.e. one chunk per unit)
-      stage_depth        staging ring depth (default 2)
-      grad_ring_depth    pinned gradient slots (default 2)
+      stage_depth        staging ring depth (default 3: copies may run up to
+                         two units ahead of the unit being cast)
+      grad_ring_depth    pinned gradient slots (default 3)
       wait_timeout       seconds before a host wait raises TimeoutError
                          (default None: wait forever, as the reference)
     """
 
     def __init__(self, model, config: SlideFSDPConfig, *, stage_chunk_elems: Optional[int] = None,
-                 stage_depth: int = 2, grad_ring_depth: int = 2, wait_timeout: Optional[float] = None):
+                 stage_depth: int = 3, grad_ring_depth: int = 3, wait_timeout: Optional[float] = None):
         super().__init__()
         if config.param_transfer_mode != "full":
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
@@ -196,6 +197,7 @@ class SlideFSDP(nn.Module):
             @staticmethod
             def forward(ctx, hidden_states, layer_state, next_layer_state):
                 ctx.set_materialize_grads(False)
+                ctx.layer_state = layer_state
                 if next_layer_state is not None:
                     is_output = next_layer_state.layer_idx == len(sf.layer_states) - 1
                     next_layer_state.to_device_async(is_backward=is_output)
@@ -205,6 +207,10 @@ class SlideFSDP(nn.Module):
 
             @staticmethod
             def backward(ctx, grad_output):
+                # The gradient has flowed past the unit's first operation: all
+                # of its backward kernels, including those reading its
+                # weights, are enqueued.
+                ctx.layer_state.mark_backward_compute_done()
                 return grad_output, None, None
 
         class PostLayerFunction(torch.autograd.Function):
@@ -251,6 +257,10 @@ class SlideFSDP(nn.Module):
         with layer_state._grad_lock:
             layer_state._bwd_armed = True
             layer_state._grads_seen = 0
+        if idx == 0:
+            # the embedding has no PreLayerFunction; its only backward kernel
+            # (the gradient scatter) reads no weights
+            layer_state._bwd_compute_done = True
         if idx - 1 >= 0:
             self.layer_states[idx - 1].to_device_async(is_backward=True)
         layer_state.wait_for_h2d()
@@ -269,6 +279,8 @@ class SlideFSDP(nn.Module):
         for idx, state in enumerate(self.layer_states):
             if state._bwd_armed and state.is_resident():
                 self._on_post_backward(state, idx)
+            if state.is_resident() and state._grads_offloaded:
+                state.mark_backward_compute_done()
 
     # ------------------------------------------------------------------
     def _allocate_activation_tensors(self, batch_size: int, seq_length: int, hidden_size: int) -> None:
@@ -297,9 +309,13 @@ class SlideFSDP(nn.Module):
 
         embed_state = self.layer_states[0]
         next_state = self.layer_states[1] if len(self.layer_states) > 1 else None
-        embed_state.to_device_async(is_backward=False)
+        # The first decoder's master was updated before the embedding's (the
+        # embedding is the last unit of the previous backward), so its load is
+        # issued first and runs while the embedding's update finishes.  The
+        # reference issues the embedding first (slide_fsdp.py:536-541).
         if next_state is not None:
             next_state.to_device_async(is_backward=False)
+        embed_state.to_device_async(is_backward=False)
         embed_state._post_called = False
         embed_state.wait_for_h2d()
         hidden_states = embed_state.layer(input_ids)
@@ -327,7 +343,8 @@ class SlideFSDP(nn.Module):
             if self.config.ac_offload_mode != "none":
                 with SlidingCheckpoint(layer_idx=i + 1, layer_tensors=self.layer_tensors, is_last_layer=is_last_decoder,
                                        no_mask=attention_mask is None, device=str(self.device),
-                                       prefetch_ring=self._act_ring, trace=trace):
+                                       prefetch_ring=self._act_ring, trace=trace,
+                                       max_workgroups=self.runtime.d2h_workgroups):
                     hidden_states = checkpoint(_layer_forward, hidden_states, causal_mask, self.position_embeddings,
                                                layer_state.layer, use_reentrant=False)
             else:

@@ -22,7 +22,11 @@ What is different, and why:
   * prefetch buffers come from a preallocated two-slot device ring
     (``ActivationRing``) when one is given, instead of ``empty_like`` per
     layer;
-  * events are recorded on the current stream rather than the null stream.
+  * events are recorded on the current stream rather than the null stream;
+  * the checkpoint's empty placeholder tensor is not round-tripped through
+    blocking copies;
+  * 16-bit tensors are packed into their slot by a kernel with a capped grid
+    instead of the runtime's full-device copy kernel.
   * NVMe/GPUDirect mode (``gds_offload=True``) is not part of this build.
 """
 
@@ -103,6 +107,7 @@ class SlidingCheckpoint(saved_tensors_hooks):
         stream: Optional[torch.cuda.Stream] = None,
         prefetch_ring: Optional[ActivationRing] = None,
         trace=None,
+        max_workgroups: int = 64,
     ):
         if gds_offload:
             raise NotImplementedError("SlidingCheckpoint: NVMe (GPUDirect Storage) offload is not supported")
@@ -124,9 +129,15 @@ class SlidingCheckpoint(saved_tensors_hooks):
         self.pre_unpack_event = torch.cuda.Event()
         self.post_unpack_event_prefetch = torch.cuda.Event()
         self._trace = trace
+        self.max_workgroups = max_workgroups
 
         def pack_hook(tensor: torch.Tensor) -> Tuple[torch.device, Any]:
-            if tensor.size() == torch.Size([0]) or not pin_memory:
+            if tensor.size() == torch.Size([0]):
+                # The checkpoint's empty placeholder: nothing to copy.  The
+                # reference's `.cpu()` (sliding_checkpoint.py:54-55) is a
+                # blocking copy that stalls the host on every layer.
+                return (tensor.device, torch.empty(tensor.shape, dtype=tensor.dtype))
+            if not pin_memory:
                 return (tensor.device, tensor.cpu())
             if self.is_last_layer:
                 return (tensor.device, tensor)
@@ -149,7 +160,13 @@ class SlidingCheckpoint(saved_tensors_hooks):
             if not src.is_contiguous():
                 with torch.cuda.stream(self.stream):
                     src = src.contiguous()
-            kernels.memcpy_async(slot, src, self.stream)
+            if src.element_size() == 2:
+                # 16-bit tensors are packed by a capped-grid kernel writing
+                # straight into the pinned slot (a few CUs keep the link busy).
+                kernels.copy_segs_b16([(src.view(-1), slot.view(-1))], self.stream,
+                                      max_workgroups=self.max_workgroups)
+            else:
+                kernels.memcpy_async(slot, src, self.stream)
             src.record_stream(self.stream)
             self.pack_counter += 1
             self._counts[(self._key, self.layer_idx)] = self.pack_counter
@@ -157,7 +174,9 @@ class SlidingCheckpoint(saved_tensors_hooks):
 
         def unpack_hook(packed: Tuple[torch.device, Any]) -> torch.Tensor:
             device, tensor = packed
-            if tensor.size() == torch.Size([0]) or not pin_memory:
+            if tensor.size() == torch.Size([0]):
+                return torch.empty(tensor.shape, dtype=tensor.dtype, device=device)
+            if not pin_memory:
                 return tensor.to(device, non_blocking=pin_memory)
             cur = torch.cuda.current_stream()
             if self.unpack_counter == 0:

@@ -48,7 +48,7 @@ def test_schedule_matches_oracle(dev):
     sf.runtime.trace = []
     sf(input_ids=ids, labels=ids)
     sf.wait_for_updates()
-    assert sf.runtime.trace == oracle.step_schedule(L)
+    assert sf.runtime.trace == oracle.step_schedule(L, first_decoder_first=True)
     sf.close()
 
 

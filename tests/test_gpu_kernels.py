@@ -132,3 +132,33 @@ def test_pinned_memcpy_round_trip(dev):
     kernels.memcpy_async(back, d, s)
     s.synchronize()
     assert torch.equal(back.view(torch.int32), h.view(torch.int32))
+
+
+@pytest.mark.parametrize("max_wg", [1, 8, 64, 0])
+def test_pack_into_pinned_host_memory(dev, max_wg):
+    """The grad offload path: one kernel gathers device tensors straight into a
+    pinned host slot, with a capped grid that strides over all tiles."""
+    g = torch.Generator().manual_seed(21)
+    sizes = [8192 * 7 + 3, 5, 0, 4096 * 33, 1]
+    parts = [torch.randn(n, generator=g).bfloat16() for n in sizes]
+    host = pinned_empty(sum(sizes) + 11, torch.bfloat16)
+    host.view(torch.int16).fill_(-1)
+    s = torch.cuda.Stream()
+    kernels.pack_b16([p.to(dev) for p in parts], host, s, max_workgroups=max_wg)
+    s.synchronize()
+    exp = oracle.pack_b16([p.view(torch.int16).numpy() for p in parts])
+    got = host.view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got[: exp.size], exp)
+    assert np.all(got[exp.size:] == 0xFFFF)  # nothing written past the packed range
+
+
+def test_copy_segs_to_pinned_host_offsets(dev):
+    a = torch.arange(100_000, dtype=torch.int16, device=dev)
+    host = pinned_empty(120_000, torch.int16)
+    host.zero_()
+    kernels.copy_segs_b16([(a[:70_001], host[7:70_008]), (a[90_000:], host[110_000:])], max_workgroups=4)
+    torch.cuda.synchronize()
+    exp = np.zeros(120_000, np.int16)
+    exp[7:70_008] = np.arange(70_001)
+    exp[110_000:] = np.arange(90_000, 100_000)
+    assert np.array_equal(host.numpy(), exp)

@@ -88,9 +88,16 @@ def build_model(w: dict, seed: int = 42):
 
 
 def elapsed_stats(records):
-    """(total ms, total bytes or elements) from (start, end, amount) event records."""
-    ms = sum(a.elapsed_time(b) for a, b, _ in records)
-    amt = sum(n for _, _, n in records)
+    """(total ms, total bytes or elements) from (start_event, end_event, amount)
+    records or from (ms, amount) records."""
+    ms = amt = 0.0
+    for r in records:
+        if len(r) == 3:
+            ms += r[0].elapsed_time(r[1])
+            amt += r[2]
+        else:
+            ms += r[0]
+            amt += r[1]
     return ms, amt
 
 
@@ -177,6 +184,9 @@ def main():
     ap.add_argument("--workload", default="llama3-8b", choices=sorted(WORKLOADS))
     ap.add_argument("--layers", type=int, default=0, help="override the number of decoder layers")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--timeline", default="", help="write the host timeline of the timed steps to this file")
+    ap.add_argument("--d2h-engine", default="kernel", choices=("sdma", "kernel"),
+                    help="gradient D2H on SDMA engines or by a capped pack kernel")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs the layer-streaming path on one GPU only; use --gpus 1", file=sys.stderr)
@@ -196,7 +206,7 @@ def main():
     log(f"[bench] model built in {time.time() - t0:.1f}s")
     t0 = time.time()
     cfg = SlideFSDPConfig(device=dev, lr=1e-5, weight_decay=0.01, attention_implementation="sdpa")
-    sf = SlideFSDP(model, cfg)
+    sf = SlideFSDP(model, cfg, d2h_engine=args.d2h_engine)
     log(f"[bench] SlideFSDP ready in {time.time() - t0:.1f}s")
     B, S = w["batch"], w["seq"]
     g = torch.Generator().manual_seed(0)
@@ -211,6 +221,11 @@ def main():
 
     rt = sf.runtime
     rt.stager.cast_timing, rt.stager.copy_timing, rt.d2h_timing = [], [], []
+    if rt.d2h_engine == "sdma":
+        from test1_amd import kernels as _k
+        _k.dma_enable_timing(True)
+    if args.timeline:
+        rt.timeline = []
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     losses = []
@@ -222,6 +237,10 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
     losses = [x.item() for x in losses]
+    if args.timeline:
+        with open(args.timeline, "w") as f:
+            for t, th, what, unit in rt.timeline:
+                f.write(f"{(t - t_start) * 1e3:.3f} {th} {what} {unit}\n")
     log(f"[bench] timed {args.steps} steps in {elapsed:.2f}s, losses {losses}")
 
     cast_ms, cast_elems = elapsed_stats(rt.stager.cast_timing)

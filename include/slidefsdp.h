@@ -37,6 +37,7 @@ typedef void* sf_stream_t;
 #define SF_EDTYPE 9003      /* dtype combination not supported */
 #define SF_ENOOPT 9004      /* unknown optimizer id */
 #define SF_EOVERLAP 9005    /* source and destination ranges overlap */
+#define SF_EDMA_BASE 10000  /* + (hsa_status_t & 0xFFF): a ROCr DMA call failed */
 
 /* Maximum number of segments one segment-table call accepts. */
 #define SF_MAX_SEGS 64
@@ -149,6 +150,45 @@ int sf_host_free(void* ptr);
 /* Device-side address of pinned host memory, for kernels that read or
  * write host memory directly (hipHostGetDevicePointer). */
 int sf_host_device_pointer(void* host_ptr, void** device_ptr);
+
+/* ---------------------------------------------------------------------
+ * SDMA device -> host copies (libsf_hip.so)
+ *
+ * A shader copy into host memory (hipMemcpyAsync's blit, or a pack kernel
+ * with a host destination) slows HBM-bound kernels running beside it; an
+ * SDMA engine does not.  These copies go through the ROCr runtime and are
+ * NOT ordered with HIP streams: the caller must have completed the source
+ * (e.g. synchronised an event on the host) before sf_dma_copy_d2h, and may
+ * read the destination only after sf_dma_wait.  They replace the gradient
+ * D2H of distributed_sync.py:353 (layer_state.py:367-381).
+ * ------------------------------------------------------------------- */
+
+/* Bind to the ROCr agents of HIP device `device` (once per process) and
+ * pick the SDMA engines for device -> host copies: the first two available
+ * engines from index 2 up (HIP's own copies use the first engines, and a
+ * copy queued behind them waits), else the runtime's choice. */
+int sf_dma_init(int device);
+
+/* Override the engines (bit e = SDMA engine e; 0 = runtime's choice). */
+int sf_dma_set_engines(uint32_t engine_mask);
+int sf_dma_get_engines(uint32_t* engine_mask);
+
+/* For each segment, copy segs[k].n BYTES from device address segs[k].src
+ * to pinned host address segs[k].dst.  Segments of 4 MiB or more are split
+ * evenly over the selected engines, others go round-robin.  One completion
+ * handle per issued copy is written to signals (at most max_signals);
+ * *nsignals receives their number. */
+int sf_dma_copy_d2h(const sf_seg* segs, int nsegs, uint64_t* signals,
+                    int max_signals, int* nsignals);
+
+/* Block until every handle completed, then release them.  If start_ns and
+ * end_ns are non-null and timing is enabled, they receive the earliest start
+ * and latest end of the copies (GPU clock, ns). */
+int sf_dma_wait(const uint64_t* signals, int nsignals, uint64_t* start_ns,
+                uint64_t* end_ns);
+
+/* Record start/end times of later copies (1) or stop (0). */
+int sf_dma_enable_timing(int on);
 
 /* ---------------------------------------------------------------------
  * Host AdamW (libsf_cpu.so)

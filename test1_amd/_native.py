@@ -67,6 +67,13 @@ HIP_SIGNATURES = {
     "sf_host_alloc": [ctypes.POINTER(_vp), _sz],
     "sf_host_free": [_vp],
     "sf_host_device_pointer": [_vp, ctypes.POINTER(_vp)],
+    "sf_dma_init": [_i],
+    "sf_dma_set_engines": [ctypes.c_uint32],
+    "sf_dma_get_engines": [ctypes.POINTER(ctypes.c_uint32)],
+    "sf_dma_copy_d2h": [ctypes.POINTER(SfSeg), _i, ctypes.POINTER(ctypes.c_uint64), _i, ctypes.POINTER(_i)],
+    "sf_dma_wait": [ctypes.POINTER(ctypes.c_uint64), _i, ctypes.POINTER(ctypes.c_uint64),
+                    ctypes.POINTER(ctypes.c_uint64)],
+    "sf_dma_enable_timing": [_i],
 }
 
 CPU_SIGNATURES = {

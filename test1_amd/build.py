@@ -46,7 +46,7 @@ def build_hip(verbose: bool = False) -> str:
     tmp = _atomic_out(out)
     _run([HIPCC, f"--offload-arch={OFFLOAD_ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-          "-I", INCLUDE, "-o", tmp, os.path.join(CSRC, "sf_hip.hip")], verbose)
+          "-I", INCLUDE, "-o", tmp, os.path.join(CSRC, "sf_hip.hip"), "-lhsa-runtime64"], verbose)
     os.replace(tmp, out)
     return out
 

@@ -9,6 +9,7 @@ asynchronous on ``stream`` (default: the current stream).
 from __future__ import annotations
 
 import ctypes
+import os
 from typing import Optional, Sequence, Tuple
 
 import torch
@@ -187,3 +188,68 @@ def memcpy_async(dst: torch.Tensor, src: torch.Tensor, stream: Optional[torch.cu
         raise ValueError(f"memcpy_async: unsupported direction {sd} -> {dd}")
     _native.check(_native.hip().sf_memcpy_async(dst.data_ptr(), src.data_ptr(), n, kind, _stream_ptr(stream)),
                   "sf_memcpy_async")
+
+
+# ---------------------------------------------------------------------------
+# SDMA device -> pinned host copies (not stream-ordered; see include/slidefsdp.h)
+# ---------------------------------------------------------------------------
+_dma_ready = set()
+
+
+def dma_init(device: Optional[torch.device] = None) -> None:
+    idx = (device.index if device is not None and device.index is not None else torch.cuda.current_device())
+    if idx in _dma_ready:
+        return
+    _native.check(_native.hip().sf_dma_init(int(idx)), "sf_dma_init")
+    env = os.environ.get("SF_DMA_ENGINES")  # e.g. "2,3"
+    if env not in (None, ""):
+        mask = 0
+        for e in env.split(","):
+            mask |= 1 << int(e)
+        _native.check(_native.hip().sf_dma_set_engines(mask), "sf_dma_set_engines")
+    _dma_ready.add(idx)
+
+
+def dma_engines() -> list:
+    """SDMA engines used for device -> host copies ([] : runtime's choice)."""
+    m = ctypes.c_uint32(0)
+    _native.check(_native.hip().sf_dma_get_engines(ctypes.byref(m)), "sf_dma_get_engines")
+    return [e for e in range(16) if m.value >> e & 1]
+
+
+def dma_enable_timing(on: bool) -> None:
+    _native.check(_native.hip().sf_dma_enable_timing(1 if on else 0), "sf_dma_enable_timing")
+
+
+def dma_copy_d2h(pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]]):
+    """Start SDMA copies of each contiguous GPU ``src`` into the pinned host
+    ``dst`` of equal byte size.  The sources must already be complete on the
+    device.  Returns a handle for ``dma_wait``; keep the tensors alive until
+    then."""
+    segs = []
+    for k, (src, dst) in enumerate(pairs):
+        _require_cuda(src, f"pair {k} src")
+        _require_contig(src, f"pair {k} src")
+        _require_contig(dst, f"pair {k} dst")
+        if dst.device.type != "cpu" or not dst.is_pinned():
+            raise ValueError(f"pair {k}: dst must be a pinned host tensor")
+        nb = src.numel() * src.element_size()
+        if nb != dst.numel() * dst.element_size():
+            raise ValueError(f"pair {k}: byte size mismatch")
+        segs.append((src.data_ptr(), dst.data_ptr(), nb))
+    arr = _seg_array(segs)
+    cap = 16 * max(1, len(segs))
+    handles = (ctypes.c_uint64 * cap)()
+    count = ctypes.c_int(0)
+    _native.check(_native.hip().sf_dma_copy_d2h(arr, len(segs), handles, cap, ctypes.byref(count)),
+                  "sf_dma_copy_d2h")
+    return (handles, count.value)
+
+
+def dma_wait(handle) -> Tuple[int, int]:
+    """Wait for the copies of ``handle``; returns (start_ns, end_ns) when timing
+    is enabled, else (0, 0)."""
+    handles, n = handle
+    t0, t1 = ctypes.c_uint64(0), ctypes.c_uint64(0)
+    _native.check(_native.hip().sf_dma_wait(handles, n, ctypes.byref(t0), ctypes.byref(t1)), "sf_dma_wait")
+    return t0.value, t1.value

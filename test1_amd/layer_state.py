@@ -135,6 +135,17 @@ class H2DStager:
         # (start_event, end_event, bytes) to copy_timing.
         self.cast_timing: Optional[list] = None
         self.copy_timing: Optional[list] = None
+        # Completion event of the last cast issued (see fence_after_casts).
+        self.last_cast_done: Optional[torch.cuda.Event] = None
+
+    def fence_after_casts(self, stream: torch.cuda.Stream) -> None:
+        """Make ``stream`` wait for every cast issued so far.  Kernels that write
+        into host memory are ordered behind the casts this way: a PCIe-writing
+        kernel running beside the HBM-bound cast slows it severalfold, even on
+        disjoint CUs, while delaying the writer by one cast costs nothing."""
+        ev = self.last_cast_done
+        if ev is not None:
+            stream.wait_event(ev)
 
     def _slot(self, s: int, c: int) -> torch.Tensor:
         return self.buf[s * self.chunk: s * self.chunk + c]
@@ -193,6 +204,7 @@ class H2DStager:
                     self._issue_copy(t, j + self.depth)  # reuses slot s, after this cast
             done = _new_event()
             done.record(self.cast_stream)
+            self.last_cast_done = done
             return done
         finally:
             self._lock.release()
@@ -233,11 +245,22 @@ class StreamingRuntime:
 
     def __init__(self, device: torch.device, dtype: torch.dtype, max_param_size: int, pool_size: int,
                  stage_chunk_elems: int, stage_depth: int, grad_ring_depth: int, wait_timeout: Optional[float],
-                 d2h_workgroups: int = 64):
+                 d2h_workgroups: int = 8, d2h_engine: str = "kernel"):
+        if d2h_engine not in ("sdma", "kernel"):
+            raise ValueError("d2h_engine must be 'sdma' or 'kernel'")
         self.device = device
+        # Gradient D2H: "kernel" (default) packs them with a capped-grid kernel
+        # writing into host memory, ~49 GB/s while the link is busy the other
+        # way; "sdma" hands them to SDMA engines through ROCr (no shader
+        # traffic, but engines shared with HIP's own copies left it at
+        # 14 GB/s in the training step).
+        self.d2h_engine = d2h_engine
+        if d2h_engine == "sdma":
+            kernels.dma_init(device)
         # Workgroups of the kernels that write into pinned host memory (grad
-        # and checkpoint offload): enough to keep the host link busy, few
-        # enough to leave the CUs to the layer compute.
+        # and checkpoint offload): 8 move ~49 GB/s while the link is busy the
+        # other way; more do not move more, and slow HBM-bound kernels beside
+        # them (the staging cast: 1.75x with 8, 10x with 64).
         self.d2h_workgroups = d2h_workgroups
         self.h2d_stream = torch.cuda.Stream(device=device)
         self.cast_stream = torch.cuda.Stream(device=device)
@@ -253,6 +276,8 @@ class StreamingRuntime:
         self.wait_timeout = wait_timeout
         self.trace: Optional[List[Tuple]] = None
         self._trace_lock = threading.Lock()
+        # Optional host timeline: (perf_counter, thread name, event, unit).
+        self.timeline: Optional[list] = None
         self.d2h_timing: Optional[list] = None
         # Test hook: when a dict, each update stores {unit: (host grads, fp32
         # master before the update)} and each gradient offload stores
@@ -264,6 +289,10 @@ class StreamingRuntime:
         if self.trace is not None:
             with self._trace_lock:
                 self.trace.append(tuple(event))
+
+    def mark(self, what: str, unit: int) -> None:
+        if self.timeline is not None:
+            self.timeline.append((time.perf_counter(), threading.current_thread().name, what, unit))
 
     def shutdown(self) -> None:
         self.offload_executor.shutdown(wait=True)
@@ -382,6 +411,7 @@ class LayerRuntimeState(nn.Module):
         self._bwd_compute_done = False
         self._grads_offloaded = False
         self.runtime.log("h2d", self.layer_idx, is_backward)
+        self.runtime.mark("h2d_issued", self.layer_idx)
 
     def _dummy_dst(self) -> torch.Tensor:
         # Only used to drain a staging ticket after a failed acquire: casts
@@ -439,11 +469,16 @@ class LayerRuntimeState(nn.Module):
                 None if p.grad is None else p.grad.detach().clone() for p in self._params]
         grad_ready = _new_event()
         grad_ready.record(cur)
+        # The cast issued last before these gradients existed (the next unit's
+        # load); the pack is ordered behind it, not behind later ones.
+        cast_fence = self.runtime.stager.last_cast_done
         for p in self._params:
             p.grad = None
         self.update_finished.clear()
         self.runtime.log("d2h", self.layer_idx)
-        self._d2h_future = self.runtime.offload_executor.submit(self._d2h_task, grads, missing, grad_ready)
+        self.runtime.mark("post_backward", self.layer_idx)
+        self._d2h_future = self.runtime.offload_executor.submit(self._d2h_task, grads, missing, grad_ready,
+                                                                cast_fence)
         self._grads_offloaded = True
         self._maybe_release_after_backward()
 
@@ -468,30 +503,49 @@ class LayerRuntimeState(nn.Module):
         self.buffer_pool.release(unit)
 
     def _d2h_task(self, grads: List[Tuple[torch.Tensor, int]], missing: List[Tuple[int, int]],
-                  grad_ready: torch.cuda.Event) -> None:
+                  grad_ready: torch.cuda.Event, cast_fence: Optional[torch.cuda.Event] = None) -> None:
         rt = self.runtime
+        rt.mark("d2h_task", self.layer_idx)
         slot = rt.grad_ring.acquire(timeout=rt.wait_timeout)
+        rt.mark("slot", self.layer_idx)
         try:
             host = rt.grad_ring.slots[slot]
-            rt.d2h_stream.wait_event(grad_ready)
-            timing = rt.d2h_timing is not None
-            if timing:
-                t0 = torch.cuda.Event(enable_timing=True)
-                t0.record(rt.d2h_stream)
-            kernels.copy_segs_b16([(g, host[off:off + g.numel()]) for g, off in grads], rt.d2h_stream,
-                                  max_workgroups=rt.d2h_workgroups)
-            for g, _ in grads:
-                g.record_stream(rt.d2h_stream)
-            done = torch.cuda.Event(enable_timing=True) if timing else _new_event()
-            done.record(rt.d2h_stream)
-            if timing:
-                rt.d2h_timing.append((t0, done, 2 * sum(g.numel() for g, _ in grads)))
+            pairs = [(g, host[off:off + g.numel()]) for g, off in grads]
+            if rt.d2h_engine == "sdma":
+                # The gradients must be complete before an SDMA engine reads
+                # them (the copy is not stream-ordered): wait here, on this
+                # worker thread, then hand the copy to the engine.
+                grad_ready.synchronize()
+                rt.mark("grad_ready", self.layer_idx)
+                handle = kernels.dma_copy_d2h(pairs)
+                rt.mark("dma_issued", self.layer_idx)
+                done = None
+            else:
+                rt.d2h_stream.wait_event(grad_ready)
+                if cast_fence is not None:
+                    rt.d2h_stream.wait_event(cast_fence)
+                timing = rt.d2h_timing is not None
+                if timing:
+                    t0 = torch.cuda.Event(enable_timing=True)
+                    t0.record(rt.d2h_stream)
+                kernels.copy_segs_b16(pairs, rt.d2h_stream, max_workgroups=rt.d2h_workgroups)
+                for g, _ in grads:
+                    g.record_stream(rt.d2h_stream)
+                done = torch.cuda.Event(enable_timing=True) if timing else _new_event()
+                done.record(rt.d2h_stream)
+                if timing:
+                    rt.d2h_timing.append((t0, done, 2 * sum(g.numel() for g, _ in grads)))
+                handle = None
         except BaseException:
             rt.grad_ring.release(slot)
             self.update_finished.set()
             raise
-        del grads
-        self._update_future = rt.update_executor.submit(self._do_update, slot, done, missing)
+        nbytes = 2 * sum(g.numel() for g, _ in grads)
+        # With SDMA the gradient tensors stay referenced until the copy is
+        # waited for; the caching allocator cannot hand them out before then.
+        keep = grads if handle is not None else None
+        del grads, pairs
+        self._update_future = rt.update_executor.submit(self._do_update, slot, done, missing, handle, keep, nbytes)
 
     def wait_for_d2h(self, timeout: Optional[float] = None) -> None:
         """Wait until the gradient offload has been issued (and re-raise its
@@ -502,16 +556,28 @@ class LayerRuntimeState(nn.Module):
             f.result(timeout=timeout)
 
     # ------------------------------------------------------------------
+    def _master_views(self) -> Dict[nn.Parameter, torch.Tensor]:
+        return {p: self._param_views[name] for (name, _), p in self._named()}
+
     def _grad_views(self, host: torch.Tensor) -> Dict[nn.Parameter, torch.Tensor]:
         views = {}
         for (name, (off, shape, size)), p in self._named():
             views[p] = host[off:off + size].view(shape)
         return views
 
-    def _do_update(self, slot: int, d2h_done: torch.cuda.Event, missing: List[Tuple[int, int]]) -> bool:
+    def _do_update(self, slot: int, d2h_done: Optional[torch.cuda.Event], missing: List[Tuple[int, int]],
+                   dma_handle=None, keep=None, nbytes: int = 0) -> bool:
         rt = self.runtime
         try:
-            d2h_done.synchronize()
+            rt.mark("update_start", self.layer_idx)
+            if dma_handle is not None:
+                t0, t1 = kernels.dma_wait(dma_handle)
+                rt.mark("dma_done", self.layer_idx)
+                del keep
+                if rt.d2h_timing is not None and t1 > t0:
+                    rt.d2h_timing.append(((t1 - t0) * 1e-6, nbytes))
+            else:
+                d2h_done.synchronize()
             for off, size in missing:
                 # a parameter that received no gradient: zeros, as the zeroed
                 # grad buffer of the reference gives it (layer_state.py:297)
@@ -521,7 +587,12 @@ class LayerRuntimeState(nn.Module):
                                               self._cpu_params_flat.clone())
             with self.update_lock:
                 if self.layer_optimizer is not None:
-                    self.layer_optimizer.step_with_grad_views(self.layer_idx, self._grad_views(rt.grad_ring.slots[slot]))
+                    # The fp32 masters are passed explicitly: this thread never
+                    # reads param.data, which the autograd thread may be
+                    # rebinding at the same time.
+                    self.layer_optimizer.step_with_grad_views(self.layer_idx, self._grad_views(rt.grad_ring.slots[slot]),
+                                                              param_views=self._master_views())
+            rt.mark("adam_done", self.layer_idx)
         finally:
             rt.grad_ring.release(slot)
             self.update_finished.set()

@@ -126,15 +126,17 @@ class LayerAdam:
             return [self._group(layer_idx)]
         return list(self.param_groups)
 
-    def _update_param(self, group: dict, p: torch.Tensor, grad: torch.Tensor) -> None:
-        if p.device.type != "cpu":
-            raise RuntimeError(f"LayerAdam: unsupported device type {p.device.type}")
-        if p.data.numel() != grad.numel():
+    def _update_param(self, group: dict, p: torch.Tensor, grad: torch.Tensor,
+                      data: Optional[torch.Tensor] = None) -> None:
+        data = p.data if data is None else data
+        if data.device.type != "cpu":
+            raise RuntimeError(f"LayerAdam: unsupported device type {data.device.type}")
+        if data.numel() != grad.numel():
             raise ValueError("LayerAdam: parameter and gradient sizes differ")
         beta1, beta2 = group["betas"]
         st = self.state[p]
         self.cpu_adam.adam_update(self.optimizer_id, group["step"], group["lr"], beta1, beta2, group["eps"],
-                                  group["weight_decay"], group["bias_correction"], p.data, grad,
+                                  group["weight_decay"], group["bias_correction"], data, grad,
                                   st["exp_avg"], st["exp_avg_sq"])
 
     @torch.no_grad()
@@ -154,9 +156,14 @@ class LayerAdam:
 
     @torch.no_grad()
     def step_with_grad_views(self, layer_idx: Optional[int] = None,
-                             grad_views: Optional[Dict[torch.nn.Parameter, torch.Tensor]] = None, closure=None):
+                             grad_views: Optional[Dict[torch.nn.Parameter, torch.Tensor]] = None, closure=None,
+                             param_views: Optional[Dict[torch.nn.Parameter, torch.Tensor]] = None):
         """Update one unit from per-parameter grad views into a host staging
-        buffer (reference layer_adam.py:358-425).  bf16 views are read in place."""
+        buffer (reference layer_adam.py:358-425).  bf16 views are read in place.
+
+        ``param_views`` (not in the reference) names the fp32 host tensors to
+        update per parameter; without it ``p.data`` is updated, which must then
+        be the host master, as in the reference."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -168,7 +175,7 @@ class LayerAdam:
                 if grad is None:
                     print(f"Warning: no gradient view for a parameter of shape {tuple(p.shape)}; skipped")
                     continue
-                self._update_param(group, p, grad)
+                self._update_param(group, p, grad, None if param_views is None else param_views[p])
         return loss
 
     def update_learning_rate(self, new_lr):

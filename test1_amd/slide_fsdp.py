@@ -84,6 +84,22 @@ def _cpu_count() -> int:
         return os.cpu_count() or 1
 
 
+def adam_threads() -> int:
+    """Threads of the host AdamW: ``SF_ADAM_THREADS`` if set, else the host's
+    cores (capped by ``OMP_NUM_THREADS``) minus two.  The two cores left over
+    keep the threads that feed the GPU (the training loop / autograd thread
+    and the offload thread) responsive while an update saturates the rest;
+    the reference reserves cores the same way with numa_launch.sh:255-266."""
+    env = int(os.environ.get("SF_ADAM_THREADS", "0") or 0)
+    if env > 0:
+        return env
+    n = _cpu_count()
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    if omp > 0:
+        n = min(n, omp)
+    return max(1, n - 2)
+
+
 class SlideFSDP(nn.Module):
     """Layer-streaming trainer (reference slide_fsdp.py:116-211).
 
@@ -95,10 +111,13 @@ class SlideFSDP(nn.Module):
       grad_ring_depth    pinned gradient slots (default 3)
       wait_timeout       seconds before a host wait raises TimeoutError
                          (default None: wait forever, as the reference)
+      d2h_engine         "kernel" (default): gradient D2H by a capped-grid pack
+                         kernel into host memory; "sdma": on SDMA engines
     """
 
     def __init__(self, model, config: SlideFSDPConfig, *, stage_chunk_elems: Optional[int] = None,
-                 stage_depth: int = 3, grad_ring_depth: int = 3, wait_timeout: Optional[float] = None):
+                 stage_depth: int = 3, grad_ring_depth: int = 3, wait_timeout: Optional[float] = None,
+                 d2h_engine: str = "kernel"):
         super().__init__()
         if config.param_transfer_mode != "full":
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
@@ -127,13 +146,17 @@ class SlideFSDP(nn.Module):
 
         chunk = int(stage_chunk_elems) if stage_chunk_elems else self.max_param_size
         self.runtime = StreamingRuntime(self.device, self.dtype, self.max_param_size, config.gpu_buffer_pool_size,
-                                        chunk, stage_depth, grad_ring_depth, wait_timeout)
+                                        chunk, stage_depth, grad_ring_depth, wait_timeout, d2h_engine=d2h_engine)
         self.buffer_pool = self.runtime.pool
         self.layer_optimizer = self._create_optimizer(config)
         self.layer_states: List[LayerRuntimeState] = []
         self._create_layer_states()
         self._setup_autograd_functions()
 
+        # The recompute must replay the forward's random numbers only if a
+        # decoder layer draws any (dropout in training); Llama-family layers
+        # draw none, and then the checkpoint skips stashing the RNG state.
+        self._layer_uses_rng = self._decoders_use_rng()
         self.layer_tensors: Optional[List[List[torch.Tensor]]] = None
         self.position_embeddings = None
         self._act_ring = ActivationRing(self.device)
@@ -159,6 +182,13 @@ class SlideFSDP(nn.Module):
         self.output_layer = OutputLayer(norm=decoder.norm, lm_head=lm_head, hidden_size=model.config.hidden_size)
         self.all_layers = [self.embed_tokens] + list(self.decoder_layers) + [self.output_layer]
 
+    def _decoders_use_rng(self) -> bool:
+        cfg = self.model_config
+        for key in ("attention_dropout", "hidden_dropout", "resid_pdrop", "attn_pdrop", "dropout"):
+            if float(getattr(cfg, key, 0.0) or 0.0) > 0.0:
+                return True
+        return any(isinstance(m, nn.Dropout) and m.p > 0 for layer in self.decoder_layers for m in layer.modules())
+
     def _calculate_max_param_size(self) -> int:
         return max(sum(p.numel() for p in layer.parameters()) for layer in self.all_layers)
 
@@ -168,10 +198,7 @@ class SlideFSDP(nn.Module):
                         fp32_optimizer_state=True, num_layer=len(self.all_layers),
                         nvme_offload_fraction=config.optimizer_nvme_offload_fraction,
                         offload_dir=config.optimizer_offload_dir, prefetch=True)
-        threads = int(os.environ.get("SF_ADAM_THREADS", "0") or 0)
-        if threads <= 0:
-            threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or _cpu_count()
-        opt.cpu_adam.set_num_threads(threads)
+        opt.cpu_adam.set_num_threads(adam_threads())
         return opt
 
     def _create_layer_states(self) -> None:
@@ -340,16 +367,20 @@ class SlideFSDP(nn.Module):
                 return self._first(layer(h, attention_mask=mask, position_embeddings=pos,
                                          output_attentions=False, use_cache=False))
 
+            ckpt_kw = dict(use_reentrant=False, preserve_rng_state=self._layer_uses_rng)
             if self.config.ac_offload_mode != "none":
                 with SlidingCheckpoint(layer_idx=i + 1, layer_tensors=self.layer_tensors, is_last_layer=is_last_decoder,
                                        no_mask=attention_mask is None, device=str(self.device),
                                        prefetch_ring=self._act_ring, trace=trace,
-                                       max_workgroups=self.runtime.d2h_workgroups):
+                                       max_workgroups=self.runtime.d2h_workgroups,
+                                       stream=self.runtime.d2h_stream,
+                                       prefetch_stream=self.runtime.h2d_stream,
+                                       pack_fence=self.runtime.stager.fence_after_casts):
                     hidden_states = checkpoint(_layer_forward, hidden_states, causal_mask, self.position_embeddings,
-                                               layer_state.layer, use_reentrant=False)
+                                               layer_state.layer, **ckpt_kw)
             else:
                 hidden_states = checkpoint(_layer_forward, hidden_states, causal_mask, self.position_embeddings,
-                                           layer_state.layer, use_reentrant=False)
+                                           layer_state.layer, **ckpt_kw)
             hidden_states = self._PostLayerFunction.apply(hidden_states, layer_state, is_last_decoder)
 
         output_state = self.layer_states[-1]

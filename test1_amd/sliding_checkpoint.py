@@ -107,7 +107,9 @@ class SlidingCheckpoint(saved_tensors_hooks):
         stream: Optional[torch.cuda.Stream] = None,
         prefetch_ring: Optional[ActivationRing] = None,
         trace=None,
-        max_workgroups: int = 64,
+        max_workgroups: int = 8,
+        prefetch_stream: Optional[torch.cuda.Stream] = None,
+        pack_fence=None,
     ):
         if gds_offload:
             raise NotImplementedError("SlidingCheckpoint: NVMe (GPUDirect Storage) offload is not supported")
@@ -116,6 +118,10 @@ class SlidingCheckpoint(saved_tensors_hooks):
         self.layer_idx = layer_idx - 1  # decoder index; units count the embedding as 0
         self.device = device
         self.stream = stream or offload_stream(device)
+        # Stream of the backward prefetch (host -> device); the offload stream
+        # unless given.  SlideFSDP puts the prefetch on its parameter H2D
+        # stream, in FIFO order behind the parameter load of the same layer.
+        self.prefetch_stream = prefetch_stream or self.stream
         self.is_last_layer = is_last_layer
         self.no_mask = no_mask
         self.layer_tensors = layer_tensors
@@ -130,6 +136,9 @@ class SlidingCheckpoint(saved_tensors_hooks):
         self.post_unpack_event_prefetch = torch.cuda.Event()
         self._trace = trace
         self.max_workgroups = max_workgroups
+        # Optional callable(stream): orders the host-writing pack behind other
+        # work (SlideFSDP passes its stager's cast fence).
+        self.pack_fence = pack_fence
 
         def pack_hook(tensor: torch.Tensor) -> Tuple[torch.device, Any]:
             if tensor.size() == torch.Size([0]):
@@ -154,6 +163,8 @@ class SlidingCheckpoint(saved_tensors_hooks):
             if self.pack_counter == 0:
                 self.pre_pack_event.record(cur)
                 self.stream.wait_event(self.pre_pack_event)
+                if self.pack_fence is not None:
+                    self.pack_fence(self.stream)
                 if self._trace is not None:
                     self._trace("act_d2h", self.layer_idx + 1)
             src = tensor.detach()
@@ -188,13 +199,14 @@ class SlidingCheckpoint(saved_tensors_hooks):
                         bufs = self.ring.buffers_like(host)
                     else:
                         bufs = [torch.empty(t.shape, dtype=t.dtype, device=self.device) for t in host]
-                    self.stream.wait_event(self.pre_unpack_event)
+                    ps = self.prefetch_stream
+                    ps.wait_event(self.pre_unpack_event)
                     for h, d in zip(host, bufs):
-                        kernels.memcpy_async(d, h, self.stream)
+                        kernels.memcpy_async(d, h, ps)
                         if self.ring is None:
-                            d.record_stream(self.stream)
+                            d.record_stream(ps)
                     ev = torch.cuda.Event()
-                    ev.record(self.stream)
+                    ev.record(ps)
                     self.fifo.append((bufs, ev))
                     if self._trace is not None:
                         self._trace("act_h2d", nxt + 1)

@@ -162,3 +162,21 @@ def test_copy_segs_to_pinned_host_offsets(dev):
     exp[7:70_008] = np.arange(70_001)
     exp[110_000:] = np.arange(90_000, 100_000)
     assert np.array_equal(host.numpy(), exp)
+
+
+def test_sdma_copy_d2h(dev):
+    """Device -> pinned host over an SDMA engine, several segments, bit-exact."""
+    kernels.dma_init(dev)
+    g = torch.Generator().manual_seed(5)
+    parts = [torch.randn(n, generator=g).bfloat16() for n in (1 << 20, 7, 4096 * 3 + 1)]
+    dparts = [p.to(dev) for p in parts]
+    host = pinned_empty(sum(p.numel() for p in parts), torch.bfloat16)
+    torch.cuda.synchronize()
+    pairs, off = [], 0
+    for p in dparts:
+        pairs.append((p, host[off:off + p.numel()]))
+        off += p.numel()
+    h = kernels.dma_copy_d2h(pairs)
+    kernels.dma_wait(h)
+    exp = oracle.pack_b16([p.view(torch.int16).numpy() for p in parts])
+    assert np.array_equal(host.view(torch.int16).numpy().view(np.uint16), exp)

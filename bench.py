@@ -87,6 +87,20 @@ def build_model(w: dict, seed: int = 42):
     return model
 
 
+def traffic_factor():
+    """HBM bytes moved per algorithmic byte of the staging cast, from the
+    FETCH_SIZE / WRITE_SIZE counter runs summarised under profiles/ (None if
+    that summary is absent)."""
+    import re
+
+    path = os.path.join(ROOT, "profiles", "cast_flat_kernel__pmc_llama3_8b_layer.md")
+    try:
+        m = re.search(r"traffic_per_algorithmic_byte:\s*([0-9.]+)", open(path).read())
+    except OSError:
+        return None
+    return float(m.group(1)) if m else None
+
+
 def elapsed_stats(records):
     """(total ms, total bytes or elements) from (start_event, end_event, amount)
     records or from (ms, amount) records."""
@@ -286,7 +300,10 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": cast_gbs / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": (None if traffic_factor() is None or not ncast
+                        else traffic_factor() * cast_bytes / ncast),
+            "traffic_source": "profiles/cast_flat_kernel__pmc_llama3_8b_layer.md (FETCH_SIZE, WRITE_SIZE "
+                              "scaled by a plain copy of known size)",
             "launches": ncast,
             "avg_launch_ms": cast_ms / ncast if ncast else None,
             "algorithmic_bytes_per_launch": cast_bytes / ncast if ncast else None,

@@ -1,0 +1,76 @@
+"""Microbenchmark of the staging kernels at one unit's size.
+
+    python -m test1_amd.kernel_bench [--elements N] [--reps R]
+
+Times, with HIP events on the stream each runs on:
+  cast      sf_cast_f32_bf16 over N fp32 elements (6 B per element of HBM)
+  copy      a plain device copy of N/2 fp32 elements (8 B per element),
+            the reference point for hardware counters (FETCH_SIZE and
+            WRITE_SIZE are scaled by what they read for it)
+  pack_d2h  sf_pack_b16 of N/2 bf16 elements into pinned host memory with
+            the offload path's 8-workgroup grid (host link)
+  h2d       one DMA copy of N fp32 elements from pinned host memory
+Default N is one Llama-3-8B decoder layer (218,112,000 parameters).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+
+import torch
+
+from . import kernels
+from .pinned import pinned_empty
+
+HBM_PEAK_GBS = 8000.0
+
+
+def _time(fn, stream, reps):
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        fn()
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--elements", type=int, default=218_112_000)
+    ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    args = ap.parse_args(argv)
+    n, reps = args.elements, args.reps
+    dev = torch.device("cuda", 0)
+    s = torch.cuda.current_stream()
+    src = torch.randn(n, device=dev) * 0.02
+    dst = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    half = n // 2
+    cp_src = torch.ones(half, dtype=torch.float32, device=dev)
+    cp_dst = torch.empty_like(cp_src)
+    g = torch.ones(half, dtype=torch.bfloat16, device=dev)
+    host_g = pinned_empty(half, torch.bfloat16)
+    host_w = pinned_empty(n, torch.float32)
+    host_w.fill_(0.5)
+    dev_w = torch.empty(n, dtype=torch.float32, device=dev)
+    for _ in range(args.warmup):
+        kernels.cast_f32_bf16_(dst, src, s)
+        cp_dst.copy_(cp_src)
+    torch.cuda.synchronize()
+    res = {}
+    ms = _time(lambda: kernels.cast_f32_bf16_(dst, src, s), s, reps)
+    res["cast"] = {"ms": ms, "GB/s": 6 * n / ms / 1e6, "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS,
+                   "algorithmic_bytes": 6 * n}
+    ms = _time(lambda: cp_dst.copy_(cp_src), s, reps)
+    res["copy"] = {"ms": ms, "GB/s": 8 * half / ms / 1e6, "bytes_read": 4 * half, "bytes_written": 4 * half}
+    ms = _time(lambda: kernels.pack_b16([g], host_g, s, max_workgroups=8), s, max(1, reps // 4))
+    res["pack_d2h"] = {"ms": ms, "GB/s": 2 * half / ms / 1e6}
+    ms = _time(lambda: kernels.memcpy_async(dev_w, host_w, s), s, max(1, reps // 4))
+    res["h2d"] = {"ms": ms, "GB/s": 4 * n / ms / 1e6}
+    print(json.dumps({"elements": n, "reps": reps, **res}), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -201,6 +201,8 @@ def main():
     ap.add_argument("--timeline", default="", help="write the host timeline of the timed steps to this file")
     ap.add_argument("--d2h-engine", default="kernel", choices=("sdma", "kernel"),
                     help="gradient D2H on SDMA engines or by a capped pack kernel")
+    ap.add_argument("--h2d-format", default="fp32", choices=("fp32", "bf16"),
+                    help="parameter H2D as fp32 masters + GPU cast, or as the host optimizer's bf16 copy")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs the layer-streaming path on one GPU only; use --gpus 1", file=sys.stderr)
@@ -220,7 +222,7 @@ def main():
     log(f"[bench] model built in {time.time() - t0:.1f}s")
     t0 = time.time()
     cfg = SlideFSDPConfig(device=dev, lr=1e-5, weight_decay=0.01, attention_implementation="sdpa")
-    sf = SlideFSDP(model, cfg, d2h_engine=args.d2h_engine)
+    sf = SlideFSDP(model, cfg, d2h_engine=args.d2h_engine, h2d_format=args.h2d_format)
     log(f"[bench] SlideFSDP ready in {time.time() - t0:.1f}s")
     B, S = w["batch"], w["seq"]
     g = torch.Generator().manual_seed(0)

@@ -219,6 +219,19 @@ int sf_cpu_adam_step(float* params, const void* grads, int g_dtype,
                      float* exp_avg, float* exp_avg_sq, size_t n,
                      const sf_adam_hparams* hp);
 
+/* sf_cpu_adam_step, also writing params_bf16[i] = rne_bf16(params[i]) after
+ * the update (same rounding and NaN rule as sf_cast_f32_bf16).  Feeds the
+ * optional bf16 host-to-device mode: the host keeps a bf16 copy of every
+ * master current, so only 2 bytes per parameter cross the host link, as in
+ * the reference (layer_state.py:301 casts on the host before the H2D). */
+int sf_cpu_adam_step_cast(float* params, const void* grads, int g_dtype,
+                          float* exp_avg, float* exp_avg_sq,
+                          uint16_t* params_bf16, size_t n,
+                          const sf_adam_hparams* hp);
+
+/* Host fp32 -> bf16 cast with the same rounding (OpenMP + AVX-512). */
+int sf_cpu_cast_f32_bf16(const float* src, uint16_t* dst, size_t n);
+
 /* Stateful interface with the reference's pybind11 `cpu_adam` module
  * semantics (optimizer/layer_adam/csrc/cpu_adam.cpp:8-13):
  *   create_adam  -> sf_adam_create   (cpu_adam_impl.cpp:89-127)
@@ -235,6 +248,14 @@ int sf_adam_update(int optimizer_id, size_t step, float lr, float beta1,
                    int bias_correction, float* params, const void* grads,
                    int g_dtype, float* exp_avg, float* exp_avg_sq, size_t n);
 int sf_adam_destroy(int optimizer_id);
+
+/* sf_adam_update that also writes the bf16 copy of the updated params
+ * (params_bf16 may be NULL). */
+int sf_adam_update_cast(int optimizer_id, size_t step, float lr, float beta1,
+                        float beta2, float eps, float weight_decay,
+                        int bias_correction, float* params, const void* grads,
+                        int g_dtype, float* exp_avg, float* exp_avg_sq,
+                        uint16_t* params_bf16, size_t n);
 
 /* OpenMP team size used by the host AdamW (<= 0: library default). */
 int sf_cpu_set_threads(int nthreads);

@@ -83,6 +83,9 @@ CPU_SIGNATURES = {
     "sf_adam_create": [_i, _f, _f, _f, _f, _f, _i, _i],
     "sf_adam_update": [_i, _sz, _f, _f, _f, _f, _f, _i, _vp, _vp, _i, _vp, _vp, _sz],
     "sf_adam_destroy": [_i],
+    "sf_adam_update_cast": [_i, _sz, _f, _f, _f, _f, _f, _i, _vp, _vp, _i, _vp, _vp, _vp, _sz],
+    "sf_cpu_adam_step_cast": [_vp, _vp, _i, _vp, _vp, _vp, _sz, ctypes.POINTER(SfAdamHparams)],
+    "sf_cpu_cast_f32_bf16": [_vp, _vp, _sz],
     "sf_cpu_set_threads": [_i],
     "sf_cpu_has_avx512": [],
 }

@@ -1,9 +1,10 @@
 // Host AdamW for LayerAdam: fp32 params and moments, fp32 or bf16 grads.
 //
 // The update is bound by host DRAM bandwidth (26 bytes per element with bf16
-// grads: read p, g, m, v and write p, m, v), so the kernel is a single
-// streaming pass with 512-bit loads/stores, split over an OpenMP team in
-// contiguous 128-element-aligned ranges.  Reading bf16 grads directly
+// grads: read p, g, m, v and write p, m, v; 28 when it also writes the bf16
+// copy of p that bf16 H2D streams), so the kernel is a single streaming pass
+// with 512-bit loads/stores over 32K-element chunks that an OpenMP team takes
+// dynamically.  Reading bf16 grads directly
 // removes the `grad.float()` temporary of the reference
 // (optimizer/layer_adam/layer_adam.py:404): bf16 -> fp32 widening is a
 // 16-bit left shift and exact, so the update is identical.
@@ -58,6 +59,15 @@ Scalars make_scalars(const sf_adam_hparams& h) {
     return c;
 }
 
+// fp32 -> bf16, round to nearest even on the bit pattern, NaN -> 0xFFFF: the
+// arithmetic of the device staging cast (and of torch's vectorised CPU cast).
+inline uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0xFFFFu;
+    return uint16_t((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
 inline float bf16_to_f32(uint16_t b) {
     uint32_t u = uint32_t(b) << 16;
     float f;
@@ -102,25 +112,45 @@ inline float load_grad(const void* g, size_t i) {
 
 template <int GDT>
 void adam_range_scalar(float* p, const void* g, float* m, float* v, size_t b, size_t e,
-                       const Scalars& c) {
-    for (size_t i = b; i < e; ++i) adam_one(p[i], load_grad<GDT>(g, i), m[i], v[i], c);
+                       const Scalars& c, uint16_t* pb) {
+    for (size_t i = b; i < e; ++i) {
+        adam_one(p[i], load_grad<GDT>(g, i), m[i], v[i], c);
+        if (pb) pb[i] = f32_to_bf16_rne(p[i]);
+    }
 }
 
 template <int GDT>
 void adam_range_tail(float* p, const void* g, float* m, float* v, size_t b, size_t e,
-                     const Scalars& c) {
-    for (size_t i = b; i < e; ++i) adam_one_tail(p[i], load_grad<GDT>(g, i), m[i], v[i], c);
+                     const Scalars& c, uint16_t* pb) {
+    for (size_t i = b; i < e; ++i) {
+        adam_one_tail(p[i], load_grad<GDT>(g, i), m[i], v[i], c);
+        if (pb) pb[i] = f32_to_bf16_rne(p[i]);
+    }
+}
+
+// 16 fp32 -> 16 bf16 (RNE, NaN -> 0xFFFF), integer arithmetic in 512-bit lanes.
+__attribute__((target("avx512f,avx512bw"))) inline __m256i rne16(__m512 x) {
+    const __m512i u = _mm512_castps_si512(x);
+    const __m512i lsb = _mm512_and_si512(_mm512_srli_epi32(u, 16), _mm512_set1_epi32(1));
+    const __m512i r = _mm512_srli_epi32(_mm512_add_epi32(_mm512_add_epi32(u, _mm512_set1_epi32(0x7FFF)), lsb), 16);
+    const __mmask16 nan = _mm512_cmpgt_epu32_mask(_mm512_and_si512(u, _mm512_set1_epi32(0x7FFFFFFF)),
+                                                  _mm512_set1_epi32(0x7F800000));
+    const __m512i out = _mm512_mask_mov_epi32(r, nan, _mm512_set1_epi32(0xFFFF));
+    return _mm512_cvtepi32_epi16(out);
 }
 
 template <int GDT>
-__attribute__((target("avx512f"))) void adam_range_avx512(float* p, const void* g, float* m,
-                                                           float* v, size_t b, size_t e,
-                                                           const Scalars& c) {
+__attribute__((target("avx512f,avx512bw"))) void adam_range_avx512(float* p, const void* g, float* m,
+                                                                    float* v, size_t b, size_t e,
+                                                                    const Scalars& c, uint16_t* pb) {
     const __m512 b1 = _mm512_set1_ps(c.b1), b2 = _mm512_set1_ps(c.b2);
     const __m512 b1m1 = _mm512_set1_ps(c.b1m1), b2m1 = _mm512_set1_ps(c.b2m1);
     const __m512 eps = _mm512_set1_ps(c.eps), bc2 = _mm512_set1_ps(c.bc2);
     const __m512 ss = _mm512_set1_ps(c.step_size), dec = _mm512_set1_ps(c.decay);
     const bool l2 = c.use_decay && !c.adamw, dw = c.use_decay && c.adamw;
+    // The bf16 copy is only read later by a DMA engine: stream it past the
+    // caches (no read-for-ownership) when the 32-byte stores are aligned.
+    const bool pb_nt = pb && (reinterpret_cast<uintptr_t>(pb + b) & 31) == 0;
     size_t i = b;
     for (; i + 16 <= e; i += 16) {
         __m512 gv;
@@ -147,38 +177,52 @@ __attribute__((target("avx512f"))) void adam_range_avx512(float* p, const void* 
         _mm512_storeu_ps(p + i, pv);
         _mm512_storeu_ps(m + i, mv);
         _mm512_storeu_ps(v + i, vv);
+        if (pb_nt) _mm256_stream_si256(reinterpret_cast<__m256i*>(pb + i), rne16(pv));
+        else if (pb) _mm256_storeu_si256(reinterpret_cast<__m256i*>(pb + i), rne16(pv));
     }
-    adam_range_scalar<GDT>(p, g, m, v, i, e, c);
+    if (pb_nt) _mm_sfence();
+    adam_range_scalar<GDT>(p, g, m, v, i, e, c, pb);
 }
 
 bool host_has_avx512() {
-    static const bool has = __builtin_cpu_supports("avx512f");
+    static const bool has = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw");
     return has;
 }
 
 int g_threads = 0;  // <= 0: OpenMP default
 
+__attribute__((target("avx512f,avx512bw"))) void cast_range_avx512(const float* src, uint16_t* dst,
+                                                                    size_t b, size_t e) {
+    size_t i = b;
+    for (; i + 16 <= e; i += 16) _mm256_storeu_si256(reinterpret_cast<__m256i*>(dst + i), rne16(_mm512_loadu_ps(src + i)));
+    for (; i < e; ++i) dst[i] = f32_to_bf16_rne(src[i]);
+}
+
 template <int GDT>
-void adam_parallel(float* p, const void* g, float* m, float* v, size_t n, const Scalars& c) {
+void adam_parallel(float* p, const void* g, float* m, float* v, size_t n, const Scalars& c,
+                   uint16_t* pb) {
     const bool avx = host_has_avx512();
     const size_t n_main = n & ~size_t(15);  // elements before the reference's scalar tail
     int nt = g_threads > 0 ? g_threads : omp_get_max_threads();
     // Small updates do not pay for a team: ~1 MiB of traffic per thread minimum.
     const size_t min_per_thread = size_t(1) << 16;
     if (size_t(nt) * min_per_thread > n) nt = int(n / min_per_thread) > 0 ? int(n / min_per_thread) : 1;
-#pragma omp parallel num_threads(nt)
-    {
-        const int t = omp_get_thread_num(), T = omp_get_num_threads();
-        // Contiguous ranges aligned to 128 elements (512 bytes of fp32).
-        const size_t blocks = (n + 127) / 128;
-        const size_t b = std::min(n, (blocks * size_t(t) / size_t(T)) * 128);
-        const size_t e = std::min(n, (blocks * size_t(t + 1) / size_t(T)) * 128);
+    // Chunks of 32K elements (~0.9 MB of traffic) handed out dynamically: a
+    // thread that the OS preempts (the host also feeds the GPU) takes fewer
+    // chunks instead of stalling the whole update.  Each element's result
+    // depends only on its position, so the partition does not change bits.
+    const size_t chunk = size_t(1) << 15;
+    const long nchunks = long((n + chunk - 1) / chunk);
+#pragma omp parallel for num_threads(nt) schedule(dynamic, 1)
+    for (long k = 0; k < nchunks; ++k) {
+        const size_t b = size_t(k) * chunk;
+        const size_t e = std::min(n, b + chunk);
         const size_t em = std::min(e, n_main);
         if (b < em) {
-            if (avx) adam_range_avx512<GDT>(p, g, m, v, b, em, c);
-            else adam_range_scalar<GDT>(p, g, m, v, b, em, c);
+            if (avx) adam_range_avx512<GDT>(p, g, m, v, b, em, c, pb);
+            else adam_range_scalar<GDT>(p, g, m, v, b, em, c, pb);
         }
-        if (std::max(b, n_main) < e) adam_range_tail<GDT>(p, g, m, v, std::max(b, n_main), e, c);
+        if (std::max(b, n_main) < e) adam_range_tail<GDT>(p, g, m, v, std::max(b, n_main), e, c, pb);
     }
 }
 
@@ -247,15 +291,39 @@ int sf_cpu_set_threads(int nthreads) {
 
 int sf_cpu_has_avx512(void) { return host_has_avx512() ? 1 : 0; }
 
-int sf_cpu_adam_step(float* params, const void* grads, int g_dtype, float* exp_avg,
-                     float* exp_avg_sq, size_t n, const sf_adam_hparams* hp) {
+int sf_cpu_adam_step_cast(float* params, const void* grads, int g_dtype, float* exp_avg,
+                          float* exp_avg_sq, uint16_t* params_bf16, size_t n, const sf_adam_hparams* hp) {
     if (n == 0) return SF_OK;
     if (!params || !grads || !exp_avg || !exp_avg_sq || !hp) return SF_EINVAL;
     const Scalars c = make_scalars(*hp);
     switch (g_dtype) {
-        case SF_DTYPE_F32: adam_parallel<SF_DTYPE_F32>(params, grads, exp_avg, exp_avg_sq, n, c); break;
-        case SF_DTYPE_BF16: adam_parallel<SF_DTYPE_BF16>(params, grads, exp_avg, exp_avg_sq, n, c); break;
+        case SF_DTYPE_F32: adam_parallel<SF_DTYPE_F32>(params, grads, exp_avg, exp_avg_sq, n, c, params_bf16); break;
+        case SF_DTYPE_BF16: adam_parallel<SF_DTYPE_BF16>(params, grads, exp_avg, exp_avg_sq, n, c, params_bf16); break;
         default: return SF_EDTYPE;
+    }
+    return SF_OK;
+}
+
+int sf_cpu_adam_step(float* params, const void* grads, int g_dtype, float* exp_avg,
+                     float* exp_avg_sq, size_t n, const sf_adam_hparams* hp) {
+    return sf_cpu_adam_step_cast(params, grads, g_dtype, exp_avg, exp_avg_sq, nullptr, n, hp);
+}
+
+int sf_cpu_cast_f32_bf16(const float* src, uint16_t* dst, size_t n) {
+    if (n == 0) return SF_OK;
+    if (!src || !dst) return SF_EINVAL;
+    const bool avx = host_has_avx512();
+    int nt = g_threads > 0 ? g_threads : omp_get_max_threads();
+    const size_t min_per_thread = size_t(1) << 18;
+    if (size_t(nt) * min_per_thread > n) nt = int(n / min_per_thread) > 0 ? int(n / min_per_thread) : 1;
+#pragma omp parallel num_threads(nt)
+    {
+        const int t = omp_get_thread_num(), T = omp_get_num_threads();
+        const size_t blocks = (n + 127) / 128;
+        const size_t b = std::min(n, (blocks * size_t(t) / size_t(T)) * 128);
+        const size_t e = std::min(n, (blocks * size_t(t + 1) / size_t(T)) * 128);
+        if (avx) cast_range_avx512(src, dst, b, e);
+        else for (size_t i = b; i < e; ++i) dst[i] = f32_to_bf16_rne(src[i]);
     }
     return SF_OK;
 }
@@ -283,9 +351,20 @@ int sf_adam_create(int optimizer_id, float alpha, float beta1, float beta2, floa
     return SF_OK;
 }
 
+int sf_adam_update_cast(int optimizer_id, size_t step, float lr, float beta1, float beta2, float eps,
+                        float weight_decay, int bias_correction, float* params, const void* grads,
+                        int g_dtype, float* exp_avg, float* exp_avg_sq, uint16_t* params_bf16, size_t n);
+
 int sf_adam_update(int optimizer_id, size_t step, float lr, float beta1, float beta2, float eps,
                    float weight_decay, int bias_correction, float* params, const void* grads,
                    int g_dtype, float* exp_avg, float* exp_avg_sq, size_t n) {
+    return sf_adam_update_cast(optimizer_id, step, lr, beta1, beta2, eps, weight_decay, bias_correction,
+                               params, grads, g_dtype, exp_avg, exp_avg_sq, nullptr, n);
+}
+
+int sf_adam_update_cast(int optimizer_id, size_t step, float lr, float beta1, float beta2, float eps,
+                        float weight_decay, int bias_correction, float* params, const void* grads,
+                        int g_dtype, float* exp_avg, float* exp_avg_sq, uint16_t* params_bf16, size_t n) {
     std::shared_ptr<AdamState> st = find_state(optimizer_id);
     if (!st) return SF_ENOOPT;
     if (g_dtype != SF_DTYPE_F32 && g_dtype != SF_DTYPE_BF16) return SF_EDTYPE;
@@ -314,7 +393,7 @@ int sf_adam_update(int optimizer_id, size_t step, float lr, float beta1, float b
         hp.bias_correction2 = bc2;
         hp.adamw_mode = st->adamw ? 1 : 0;
     }
-    return sf_cpu_adam_step(params, grads, g_dtype, exp_avg, exp_avg_sq, n, &hp);
+    return sf_cpu_adam_step_cast(params, grads, g_dtype, exp_avg, exp_avg_sq, params_bf16, n, &hp);
 }
 
 int sf_adam_destroy(int optimizer_id) {

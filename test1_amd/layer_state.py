@@ -45,6 +45,7 @@ import torch
 import torch.nn as nn
 
 from . import kernels
+from .optimizer import cpu_adam as _cpu_adam
 from .pinned import pinned_empty
 
 
@@ -215,6 +216,44 @@ class H2DStager:
         return self.finish(self.begin(host_f32), dst_bf16, wait_event)
 
 
+class BF16Loader:
+    """Pinned bf16 host copy -> device bf16 unit: one DMA per unit, no cast.
+
+    Used when the host optimizer keeps a bf16 copy of every master current
+    (it writes it in the same pass as the update), so two bytes per parameter
+    cross the host link -- the reference's link format (layer_state.py:299-314)
+    without its host cast on the load path.  Offers the stager's fence
+    interface; there are no casts to fence behind.
+    """
+
+    def __init__(self, h2d_stream: torch.cuda.Stream):
+        self.h2d_stream = h2d_stream
+        self.last_cast_done: Optional[torch.cuda.Event] = None
+        self.cast_timing: Optional[list] = None
+        self.copy_timing: Optional[list] = None
+
+    def fence_after_casts(self, stream: torch.cuda.Stream) -> None:
+        return None
+
+    def load(self, host_bf16: torch.Tensor, dst_bf16: torch.Tensor,
+             wait_event: Optional[torch.cuda.Event]) -> torch.cuda.Event:
+        n = host_bf16.numel()
+        if dst_bf16.numel() < n:
+            raise ValueError("BF16Loader.load: destination smaller than source")
+        if wait_event is not None:
+            self.h2d_stream.wait_event(wait_event)
+        timing = self.copy_timing is not None
+        if timing:
+            t0 = torch.cuda.Event(enable_timing=True)
+            t0.record(self.h2d_stream)
+        kernels.memcpy_async(dst_bf16[:n], host_bf16, self.h2d_stream)
+        done = torch.cuda.Event(enable_timing=True) if timing else _new_event()
+        done.record(self.h2d_stream)
+        if timing:
+            self.copy_timing.append((t0, done, n * 2))
+        return done
+
+
 class GradStagingRing:
     """``depth`` pinned bf16 host slots of ``max_elems`` for gradient D2H.
 
@@ -245,10 +284,18 @@ class StreamingRuntime:
 
     def __init__(self, device: torch.device, dtype: torch.dtype, max_param_size: int, pool_size: int,
                  stage_chunk_elems: int, stage_depth: int, grad_ring_depth: int, wait_timeout: Optional[float],
-                 d2h_workgroups: int = 8, d2h_engine: str = "kernel"):
+                 d2h_workgroups: int = 8, d2h_engine: str = "kernel", h2d_format: str = "fp32"):
         if d2h_engine not in ("sdma", "kernel"):
             raise ValueError("d2h_engine must be 'sdma' or 'kernel'")
+        if h2d_format not in ("fp32", "bf16"):
+            raise ValueError("h2d_format must be 'fp32' or 'bf16'")
+        if h2d_format == "bf16" and dtype != torch.bfloat16:
+            raise ValueError("h2d_format='bf16' needs bf16 units")
         self.device = device
+        # Parameter H2D: "fp32" (default) copies the fp32 masters and casts
+        # them on the GPU; "bf16" copies a bf16 host copy that the optimizer
+        # keeps current, half the bytes on the host link.
+        self.h2d_format = h2d_format
         # Gradient D2H: "kernel" (default) packs them with a capped-grid kernel
         # writing into host memory, ~49 GB/s while the link is busy the other
         # way; "sdma" hands them to SDMA engines through ROCr (no shader
@@ -266,7 +313,10 @@ class StreamingRuntime:
         self.cast_stream = torch.cuda.Stream(device=device)
         self.d2h_stream = torch.cuda.Stream(device=device)
         self.pool = LayerBufferPool(max_param_size, dtype, device, pool_size)
-        self.stager = H2DStager(device, stage_chunk_elems, stage_depth, self.h2d_stream, self.cast_stream)
+        if h2d_format == "bf16":
+            self.stager = BF16Loader(self.h2d_stream)
+        else:
+            self.stager = H2DStager(device, stage_chunk_elems, stage_depth, self.h2d_stream, self.cast_stream)
         self.grad_ring = GradStagingRing(grad_ring_depth, max_param_size, dtype)
         # One thread issues gradient offloads (it may wait for a free host
         # slot); one thread runs the host optimizer, as the reference's
@@ -342,6 +392,11 @@ class LayerRuntimeState(nn.Module):
         self._param_views: "OrderedDict[str, torch.Tensor]" = OrderedDict()
         self._params: List[nn.Parameter] = []
         self._init_param_views()
+        # bf16 H2D: a pinned bf16 copy of the master, rewritten by every update.
+        self._cpu_params_bf16: Optional[torch.Tensor] = None
+        if runtime.h2d_format == "bf16":
+            self._cpu_params_bf16 = pinned_empty(self.total_size, torch.bfloat16)
+            self.refresh_host_copy()
         self._grad_params = [p for p in self._params if p.requires_grad]
         self._grads_seen = 0
         self._grad_lock = threading.Lock()
@@ -367,6 +422,12 @@ class LayerRuntimeState(nn.Module):
 
     def _named(self):
         return zip(self._param_maps.items(), self._params)
+
+    def refresh_host_copy(self) -> None:
+        """Recompute the bf16 host copy from the fp32 master (bf16 H2D only).
+        Updates keep it current; call this after writing the master directly."""
+        if self._cpu_params_bf16 is not None and self.total_size:
+            _cpu_adam.cast_f32_bf16(self._cpu_params_flat, self._cpu_params_bf16)
 
     def _bind_device_views(self, unit: Dict[str, Any]) -> None:
         buf = unit["param"]
@@ -394,7 +455,13 @@ class LayerRuntimeState(nn.Module):
         stager = self.runtime.stager
         # The backward of an embedding never reads its weights (its gradient
         # depends only on the indices), so no copy or cast is needed then.
-        ticket = None if (is_backward and not self.backward_reads_params) else stager.begin(self._cpu_params_flat)
+        skip = is_backward and not self.backward_reads_params
+        if self._cpu_params_bf16 is not None:
+            unit = self.buffer_pool.acquire(timeout=self.runtime.wait_timeout)
+            self._h2d_done = unit["ready"] if skip else stager.load(self._cpu_params_bf16, unit["param"], unit["ready"])
+            self._bind_unit(unit, is_backward)
+            return
+        ticket = None if skip else stager.begin(self._cpu_params_flat)
         try:
             unit = self.buffer_pool.acquire(timeout=self.runtime.wait_timeout)
         except BaseException:
@@ -405,6 +472,9 @@ class LayerRuntimeState(nn.Module):
             self._h2d_done = unit["ready"]   # keep the release fence of the unit
         else:
             self._h2d_done = stager.finish(ticket, unit["param"], unit["ready"])
+        self._bind_unit(unit, is_backward)
+
+    def _bind_unit(self, unit: Dict[str, Any], is_backward: bool) -> None:
         unit["ready"] = None
         self._bind_device_views(unit)
         self._current_gpu_cache = unit
@@ -559,6 +629,11 @@ class LayerRuntimeState(nn.Module):
     def _master_views(self) -> Dict[nn.Parameter, torch.Tensor]:
         return {p: self._param_views[name] for (name, _), p in self._named()}
 
+    def _bf16_views(self) -> Optional[Dict[nn.Parameter, torch.Tensor]]:
+        if self._cpu_params_bf16 is None:
+            return None
+        return self._grad_views(self._cpu_params_bf16)
+
     def _grad_views(self, host: torch.Tensor) -> Dict[nn.Parameter, torch.Tensor]:
         views = {}
         for (name, (off, shape, size)), p in self._named():
@@ -591,7 +666,8 @@ class LayerRuntimeState(nn.Module):
                     # reads param.data, which the autograd thread may be
                     # rebinding at the same time.
                     self.layer_optimizer.step_with_grad_views(self.layer_idx, self._grad_views(rt.grad_ring.slots[slot]),
-                                                              param_views=self._master_views())
+                                                              param_views=self._master_views(),
+                                                              bf16_views=self._bf16_views())
             rt.mark("adam_done", self.layer_idx)
         finally:
             rt.grad_ring.release(slot)

@@ -22,6 +22,7 @@ RuntimeError instead of dereferencing a null pointer (cpu_adam_impl.cpp:229-231)
 from __future__ import annotations
 
 import ctypes
+from typing import Optional
 
 import torch
 
@@ -59,7 +60,11 @@ def _grad_dtype_code(g: torch.Tensor) -> int:
 
 def adam_update(optimizer_id: int, step: int, lr: float, beta1: float, beta2: float, eps: float,
                 weight_decay: float, bias_correction: bool, params: torch.Tensor, grads: torch.Tensor,
-                exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor) -> int:
+                exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor,
+                params_bf16: Optional[torch.Tensor] = None) -> int:
+    """The reference's ``adam_update``.  ``params_bf16`` (not in the
+    reference): a contiguous bf16 CPU tensor of the params' size that receives
+    the round-to-nearest-even bf16 of every updated param in the same pass."""
     if params.dtype != torch.float32 or exp_avg.dtype != torch.float32 or exp_avg_sq.dtype != torch.float32:
         raise RuntimeError(
             f"Adam optimizer with param type {params.dtype} and state type {exp_avg.dtype} "
@@ -79,10 +84,29 @@ def adam_update(optimizer_id: int, step: int, lr: float, beta1: float, beta2: fl
         raise ValueError("adam_update: params, grads and moments must have the same numel")
     if not grads.is_contiguous():
         grads = grads.contiguous()
-    _check(_lib().sf_adam_update(int(optimizer_id), int(step), lr, beta1, beta2, eps, weight_decay,
-                                 1 if bias_correction else 0, params.data_ptr(), grads.data_ptr(), gcode,
-                                 exp_avg.data_ptr(), exp_avg_sq.data_ptr(), n), "adam_update")
+    pb = None
+    if params_bf16 is not None:
+        if (params_bf16.dtype != torch.bfloat16 or params_bf16.device.type != "cpu"
+                or not params_bf16.is_contiguous() or params_bf16.numel() != n):
+            raise ValueError("adam_update: params_bf16 must be a contiguous bf16 CPU tensor of the params' size")
+        pb = params_bf16.data_ptr()
+    _check(_lib().sf_adam_update_cast(int(optimizer_id), int(step), lr, beta1, beta2, eps, weight_decay,
+                                      1 if bias_correction else 0, params.data_ptr(), grads.data_ptr(), gcode,
+                                      exp_avg.data_ptr(), exp_avg_sq.data_ptr(), pb, n), "adam_update")
     return 0
+
+
+def cast_f32_bf16(src: torch.Tensor, dst: torch.Tensor) -> torch.Tensor:
+    """``dst`` = round-to-nearest-even bf16 of ``src`` (NaN -> 0xFFFF), on the
+    host AdamW's threads.  Both contiguous CPU tensors of the same size."""
+    if src.dtype != torch.float32 or dst.dtype != torch.bfloat16:
+        raise TypeError("cast_f32_bf16: expects fp32 src and bf16 dst")
+    if src.device.type != "cpu" or dst.device.type != "cpu":
+        raise RuntimeError("cast_f32_bf16: CPU tensors only")
+    if not (src.is_contiguous() and dst.is_contiguous()) or src.numel() != dst.numel():
+        raise ValueError("cast_f32_bf16: contiguous tensors of the same size")
+    _check(_lib().sf_cpu_cast_f32_bf16(src.data_ptr(), dst.data_ptr(), src.numel()), "sf_cpu_cast_f32_bf16")
+    return dst
 
 
 def set_num_threads(n: int) -> None:

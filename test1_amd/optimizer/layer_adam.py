@@ -127,7 +127,7 @@ class LayerAdam:
         return list(self.param_groups)
 
     def _update_param(self, group: dict, p: torch.Tensor, grad: torch.Tensor,
-                      data: Optional[torch.Tensor] = None) -> None:
+                      data: Optional[torch.Tensor] = None, data_bf16: Optional[torch.Tensor] = None) -> None:
         data = p.data if data is None else data
         if data.device.type != "cpu":
             raise RuntimeError(f"LayerAdam: unsupported device type {data.device.type}")
@@ -137,7 +137,7 @@ class LayerAdam:
         st = self.state[p]
         self.cpu_adam.adam_update(self.optimizer_id, group["step"], group["lr"], beta1, beta2, group["eps"],
                                   group["weight_decay"], group["bias_correction"], data, grad,
-                                  st["exp_avg"], st["exp_avg_sq"])
+                                  st["exp_avg"], st["exp_avg_sq"], params_bf16=data_bf16)
 
     @torch.no_grad()
     def step(self, layer_idx: Optional[int] = None, closure=None):
@@ -157,13 +157,16 @@ class LayerAdam:
     @torch.no_grad()
     def step_with_grad_views(self, layer_idx: Optional[int] = None,
                              grad_views: Optional[Dict[torch.nn.Parameter, torch.Tensor]] = None, closure=None,
-                             param_views: Optional[Dict[torch.nn.Parameter, torch.Tensor]] = None):
+                             param_views: Optional[Dict[torch.nn.Parameter, torch.Tensor]] = None,
+                             bf16_views: Optional[Dict[torch.nn.Parameter, torch.Tensor]] = None):
         """Update one unit from per-parameter grad views into a host staging
         buffer (reference layer_adam.py:358-425).  bf16 views are read in place.
 
         ``param_views`` (not in the reference) names the fp32 host tensors to
         update per parameter; without it ``p.data`` is updated, which must then
-        be the host master, as in the reference."""
+        be the host master, as in the reference.  ``bf16_views`` (not in the
+        reference) names bf16 host tensors that receive the rounded params in
+        the same pass."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -175,7 +178,8 @@ class LayerAdam:
                 if grad is None:
                     print(f"Warning: no gradient view for a parameter of shape {tuple(p.shape)}; skipped")
                     continue
-                self._update_param(group, p, grad, None if param_views is None else param_views[p])
+                self._update_param(group, p, grad, None if param_views is None else param_views[p],
+                                   None if bf16_views is None else bf16_views[p])
         return loss
 
     def update_learning_rate(self, new_lr):

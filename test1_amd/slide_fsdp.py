@@ -113,11 +113,16 @@ class SlideFSDP(nn.Module):
                          (default None: wait forever, as the reference)
       d2h_engine         "kernel" (default): gradient D2H by a capped-grid pack
                          kernel into host memory; "sdma": on SDMA engines
+      h2d_format         "fp32" (default): the fp32 masters cross the host
+                         link and are cast to bf16 on the GPU; "bf16": the
+                         host optimizer keeps a bf16 copy of every master
+                         (written in its update pass) and that crosses the
+                         link, half the bytes.  Both stage the same bits.
     """
 
     def __init__(self, model, config: SlideFSDPConfig, *, stage_chunk_elems: Optional[int] = None,
                  stage_depth: int = 3, grad_ring_depth: int = 3, wait_timeout: Optional[float] = None,
-                 d2h_engine: str = "kernel"):
+                 d2h_engine: str = "kernel", h2d_format: str = "fp32"):
         super().__init__()
         if config.param_transfer_mode != "full":
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
@@ -146,7 +151,8 @@ class SlideFSDP(nn.Module):
 
         chunk = int(stage_chunk_elems) if stage_chunk_elems else self.max_param_size
         self.runtime = StreamingRuntime(self.device, self.dtype, self.max_param_size, config.gpu_buffer_pool_size,
-                                        chunk, stage_depth, grad_ring_depth, wait_timeout, d2h_engine=d2h_engine)
+                                        chunk, stage_depth, grad_ring_depth, wait_timeout, d2h_engine=d2h_engine,
+                                        h2d_format=h2d_format)
         self.buffer_pool = self.runtime.pool
         self.layer_optimizer = self._create_optimizer(config)
         self.layer_states: List[LayerRuntimeState] = []
@@ -396,6 +402,14 @@ class SlideFSDP(nn.Module):
         """Block until every queued host update has finished."""
         for s in self.layer_states:
             s.wait_for_update()
+
+    def refresh_host_copies(self) -> None:
+        """With h2d_format='bf16': recompute every unit's bf16 host copy from
+        its fp32 master, after the masters were written outside the optimizer
+        (a loaded checkpoint).  A no-op with fp32 H2D."""
+        self.wait_for_updates()
+        for s in self.layer_states:
+            s.refresh_host_copy()
 
     def update_learning_rate(self, new_lr: float) -> None:
         if self.layer_optimizer is not None:

@@ -133,3 +133,45 @@ def test_layer_adam_matches_compiled_reference_driven_identically():
     for u, ru in zip(params, rparams):
         for p, rp in zip(u, ru):
             assert torch.equal(p.detach().view(torch.int32), rp.view(torch.int32))
+
+
+def test_adam_update_writes_rounded_bf16_copy():
+    # The fused bf16 output leaves p/m/v unchanged and equals the cast of the
+    # updated params; ragged tail (n % 16 != 0) and one non-finite value.
+    rng = np.random.default_rng(2)
+    n = 2_000_003
+    p0 = torch.from_numpy((rng.standard_normal(n) * 0.02).astype(np.float32))
+    g = torch.from_numpy((rng.standard_normal(n) * 1e-3).astype(np.float32)).bfloat16()
+    g[n - 2] = float("nan")
+    runs = []
+    for with_copy in (False, True):
+        p, m, v = p0.clone(), torch.zeros(n), torch.zeros(n)
+        pb = torch.empty(n, dtype=torch.bfloat16) if with_copy else None
+        cpu_adam.create_adam(70, 1e-5, 0.9, 0.999, 1e-8, 0.01, True)
+        for step in (1, 2):
+            cpu_adam.adam_update(70, step, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, p, g, m, v, params_bf16=pb)
+        cpu_adam.destroy_adam(70)
+        runs.append((p, m, v, pb))
+    for a, b in zip(runs[0][:3], runs[1][:3]):
+        assert np.array_equal(a.numpy().view(np.uint32), b.numpy().view(np.uint32))
+    p, pb = runs[1][0], runs[1][3]
+    assert np.isnan(p[n - 2].item())
+    assert np.array_equal(pb.view(torch.int16).numpy().view(np.uint16), oracle.cast_f32_bf16(p.numpy()))
+
+
+def test_host_cast_matches_golden():
+    d = np.load(os.path.join(GOLDEN, "cast_f32_bf16.npz"))
+    x = torch.from_numpy(d["x_bits"].view(np.float32).copy())
+    out = torch.empty(x.numel(), dtype=torch.bfloat16)
+    cpu_adam.cast_f32_bf16(x, out)
+    assert np.array_equal(out.view(torch.int16).numpy().view(np.uint16), d["bf16_bits"])
+    with pytest.raises(ValueError, match="same size"):
+        cpu_adam.cast_f32_bf16(x, out[:-1])
+    with pytest.raises(ValueError, match="params_bf16"):
+        cpu_adam.create_adam(71, 1e-3)
+        try:
+            q = torch.zeros(8)
+            cpu_adam.adam_update(71, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, True, q, q.clone(), q.clone(), q.clone(),
+                                 params_bf16=torch.empty(8))
+        finally:
+            cpu_adam.destroy_adam(71)

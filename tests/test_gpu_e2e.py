@@ -52,13 +52,17 @@ def test_schedule_matches_oracle(dev):
     sf.close()
 
 
-def test_updates_match_oracle_bit_exact(dev):
+@pytest.mark.parametrize("h2d_format", ["fp32", "bf16"])
+def test_updates_match_oracle_bit_exact(dev, h2d_format):
     """Every unit's host update equals the oracle AdamW applied to the same
-    (captured) bf16 grads and fp32 master, for 3 steps."""
+    (captured) bf16 grads and fp32 master, for 3 steps.  With bf16 H2D the
+    host bf16 copy of every unit is the oracle cast of its master after each
+    step, so both formats stage the same bits."""
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model()
-    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS), wait_timeout=120)
+    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS),
+                   wait_timeout=120, h2d_format=h2d_format)
     orc = oracle.LayerAdamOracle(lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
     ref_units = []
     for ps in units_of(model):
@@ -90,6 +94,9 @@ def test_updates_match_oracle_bit_exact(dev):
         for u, ps in enumerate(units_of(model)):
             for p, a in zip(ps, ref_units[u]):
                 assert np.array_equal(p.detach().numpy().view(np.uint32), a.view(np.uint32)), f"unit {u}"
+            if h2d_format == "bf16":
+                flat = np.concatenate([a.reshape(-1) for a in ref_units[u]])
+                assert np.array_equal(u16(sf.layer_states[u]._cpu_params_bf16), oracle.cast_f32_bf16(flat)), f"unit {u}"
     sf.close()
 
 
@@ -124,13 +131,15 @@ def reference_losses(model, steps_ids, dev):
     return losses, first_grads
 
 
-def test_loss_parity_with_non_offloaded_run(dev):
+@pytest.mark.parametrize("h2d_format", ["fp32", "bf16"])
+def test_loss_parity_with_non_offloaded_run(dev, h2d_format):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model()
     steps = batches(10)
     ref_losses, ref_grads = reference_losses(model, steps, dev)
-    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS), wait_timeout=120)
+    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS),
+                   wait_timeout=120, h2d_format=h2d_format)
     losses = []
     for k, ids in enumerate(steps):
         if k == 0:

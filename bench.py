@@ -16,7 +16,9 @@ One JSON line is printed with the metric (tokens/s), the roofline of the
 staging cast kernel (HBM-bound, measured with HIP events on its stream over
 the timed region), host-link rates of the H2D/D2H copies, and the reference's
 host-side staging + LayerAdam path timed on this machine's cores
-(``cpu_baseline``).
+(``cpu_baseline``).  ``variants`` holds a second timed run on the same model
+with the other parameter H2D format (fp32 masters + GPU cast, or the host
+optimizer's bf16 copy), on fresh batches.
 """
 
 from __future__ import annotations
@@ -115,7 +117,8 @@ def elapsed_stats(records):
     return ms, amt
 
 
-def cpu_baseline(layer_numel: int, total_params: int, tokens: int, resident_params: int, iters: int = 4):
+def cpu_baseline(layer_numel: int, total_params: int, tokens: int, resident_params: int, iters: int = 150,
+                 warmup: int = 5):
     """The reference's host-side work, timed on this host: per unit the fp32 ->
     bf16 cast of the master (reference layer_state.py:301, torch CPU copy),
     twice per step (forward and backward load), the ``grad.float()`` unpack
@@ -159,7 +162,8 @@ def cpu_baseline(layer_numel: int, total_params: int, tokens: int, resident_para
             opt.update(step, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, master.numpy(), gf.numpy(), m.numpy(), v.numpy())
         threads = 1
     t_cast = t_unpack = t_adam = 0.0
-    for it in range(iters + 1):
+    t_all = time.perf_counter()
+    for it in range(iters + warmup):
         t0 = time.perf_counter()
         bf.copy_(master)
         t1 = time.perf_counter()
@@ -167,10 +171,11 @@ def cpu_baseline(layer_numel: int, total_params: int, tokens: int, resident_para
         t2 = time.perf_counter()
         adam(it + 1, gf)
         t3 = time.perf_counter()
-        if it > 0:
+        if it >= warmup:
             t_cast += t1 - t0
             t_unpack += t2 - t1
             t_adam += t3 - t2
+    t_all = time.perf_counter() - t_all
     t_cast, t_unpack, t_adam = (x / iters for x in (t_cast, t_unpack, t_adam))
     per_param = (t_cast * 2 + t_unpack + t_adam) / n
     # units that stay resident are cast once per step, not twice
@@ -182,7 +187,8 @@ def cpu_baseline(layer_numel: int, total_params: int, tokens: int, resident_para
         "unit": "tokens/s",
         "cores": threads,
         "kind": kind,
-        "sample": (f"one Llama-3-8B decoder layer sample ({n:,} params): torch CPU fp32->bf16 cast "
+        "sample": (f"one Llama-3-8B decoder layer sample ({n:,} params), {warmup} warmup + {iters} timed "
+                   f"iterations ({t_all:.1f} s of CPU work): torch CPU fp32->bf16 cast "
                    f"{t_cast * 1e3:.1f} ms, grad.float() {t_unpack * 1e3:.1f} ms, CPU Adam {t_adam * 1e3:.1f} ms "
                    f"({28 * n / t_adam / 1e9:.1f} GB/s at 28 B/param); per-step time = per-param cost x "
                    f"{total_params:,} params (cast twice, resident units once)"),
@@ -190,42 +196,26 @@ def cpu_baseline(layer_numel: int, total_params: int, tokens: int, resident_para
     }
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=3)
-    ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--workload", default="llama3-8b", choices=sorted(WORKLOADS))
-    ap.add_argument("--layers", type=int, default=0, help="override the number of decoder layers")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--timeline", default="", help="write the host timeline of the timed steps to this file")
-    ap.add_argument("--d2h-engine", default="kernel", choices=("sdma", "kernel"),
-                    help="gradient D2H on SDMA engines or by a capped pack kernel")
-    ap.add_argument("--h2d-format", default="fp32", choices=("fp32", "bf16"),
-                    help="parameter H2D as fp32 masters + GPU cast, or as the host optimizer's bf16 copy")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build runs the layer-streaming path on one GPU only; use --gpus 1", file=sys.stderr)
-        sys.exit(2)
+def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_engine: str,
+              timeline: str = "", batch_seed: int = 0) -> dict:
+    """Wrap ``model`` in SlideFSDP, run the warmup steps, then time
+    ``args.steps`` steps between two device synchronisations.  Returns the
+    timings and the per-kernel / per-copy event records; closes the wrapper.
+    A second run on the same model uses another ``batch_seed``: the first
+    run's updates lower the loss on the batches it saw."""
+    import gc
 
     import torch
 
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
-    w = dict(WORKLOADS[args.workload])
-    if args.layers:
-        w["layers"] = args.layers
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    t0 = time.time()
-    model = build_model(w)
-    log(f"[bench] model built in {time.time() - t0:.1f}s")
     t0 = time.time()
     cfg = SlideFSDPConfig(device=dev, lr=1e-5, weight_decay=0.01, attention_implementation="sdpa")
-    sf = SlideFSDP(model, cfg, d2h_engine=args.d2h_engine, h2d_format=args.h2d_format)
-    log(f"[bench] SlideFSDP ready in {time.time() - t0:.1f}s")
+    sf = SlideFSDP(model, cfg, d2h_engine=d2h_engine, h2d_format=h2d_format, resident_layers=resident_layers)
+    log(f"[bench] SlideFSDP ({h2d_format} H2D, {sf.resident_layers} resident decoders, {d2h_engine} D2H) "
+        f"ready in {time.time() - t0:.1f}s")
     B, S = w["batch"], w["seq"]
-    g = torch.Generator().manual_seed(0)
+    g = torch.Generator().manual_seed(batch_seed)
     batches = [torch.randint(0, w["vocab"], (B, S), generator=g).to(dev) for _ in range(args.warmup + args.steps)]
 
     for i in range(args.warmup):
@@ -240,7 +230,7 @@ def main():
     if rt.d2h_engine == "sdma":
         from test1_amd import kernels as _k
         _k.dma_enable_timing(True)
-    if args.timeline:
+    if timeline:
         rt.timeline = []
     torch.cuda.synchronize()
     t_start = time.perf_counter()
@@ -253,24 +243,97 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
     losses = [x.item() for x in losses]
-    if args.timeline:
-        with open(args.timeline, "w") as f:
+    if timeline:
+        with open(timeline, "w") as f:
             for t, th, what, unit in rt.timeline:
                 f.write(f"{(t - t_start) * 1e3:.3f} {th} {what} {unit}\n")
     log(f"[bench] timed {args.steps} steps in {elapsed:.2f}s, losses {losses}")
+    r = {
+        "elapsed": elapsed, "losses": losses, "tokens": B * S * args.steps,
+        "cast": elapsed_stats(rt.stager.cast_timing), "ncast": len(rt.stager.cast_timing or []),
+        "h2d": elapsed_stats(rt.stager.copy_timing), "d2h": elapsed_stats(rt.d2h_timing),
+        "total_params": sf.total_params, "resident_layers": sf.resident_layers,
+        "layer_numel": sum(p.numel() for p in sf.decoder_layers[0].parameters()),
+        "output_numel": sum(p.numel() for p in sf.output_layer.parameters()),
+    }
+    sf.close()
+    del sf, out, rt
+    gc.collect()
+    torch.cuda.empty_cache()
+    return r
 
-    cast_ms, cast_elems = elapsed_stats(rt.stager.cast_timing)
-    h2d_ms, h2d_bytes = elapsed_stats(rt.stager.copy_timing)
-    d2h_ms, d2h_bytes = elapsed_stats(rt.d2h_timing)
-    ncast = len(rt.stager.cast_timing)
+
+def link_stats(r: dict, steps: int) -> dict:
+    (h2d_ms, h2d_bytes), (d2h_ms, d2h_bytes) = r["h2d"], r["d2h"]
+    h2d = h2d_bytes / (h2d_ms * 1e-3) / 1e9 if h2d_ms > 0 else None
+    d2h = d2h_bytes / (d2h_ms * 1e-3) / 1e9 if d2h_ms > 0 else None
+    return {
+        "h2d_gbs": h2d, "d2h_gbs": d2h,
+        "h2d_frac": None if h2d is None else h2d / LINK_PEAK_GBS,
+        "d2h_frac": None if d2h is None else d2h / LINK_PEAK_GBS,
+        "peak_gbs": LINK_PEAK_GBS,
+        "h2d_bytes_per_step": h2d_bytes / steps,
+        "d2h_bytes_per_step": d2h_bytes / steps,
+        "h2d_busy_frac": (h2d_ms * 1e-3) / r["elapsed"],
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", default="llama3-8b", choices=sorted(WORKLOADS))
+    ap.add_argument("--layers", type=int, default=0, help="override the number of decoder layers")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-variants", action="store_true",
+                    help="skip the second timed run with the other parameter H2D format")
+    ap.add_argument("--timeline", default="", help="write the host timeline of the timed steps to this file")
+    ap.add_argument("--d2h-engine", default="kernel", choices=("sdma", "kernel", "copy"),
+                    help="gradient D2H by a capped pack kernel, by DMA copies, or on SDMA engines via ROCr")
+    ap.add_argument("--h2d-format", default="fp32", choices=("fp32", "bf16"),
+                    help="parameter H2D as fp32 masters + GPU cast, or as the host optimizer's bf16 copy")
+    ap.add_argument("--resident-layers", type=int, default=None,
+                    help="decoder layers kept on the GPU from their forward to their backward "
+                         "(default: as many as fit in half of the free HBM)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs the layer-streaming path on one GPU only; use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    w = dict(WORKLOADS[args.workload])
+    if args.layers:
+        w["layers"] = args.layers
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    t0 = time.time()
+    model = build_model(w)
+    log(f"[bench] model built in {time.time() - t0:.1f}s")
+    B, S = w["batch"], w["seq"]
+
+    r = timed_run(model, w, args, dev, args.h2d_format, args.resident_layers, args.d2h_engine, args.timeline)
+    elapsed, losses = r["elapsed"], r["losses"]
+    cast_ms, cast_elems = r["cast"]
+    ncast = r["ncast"]
     cast_bytes = 6 * cast_elems  # read fp32 + write bf16 per element
     cast_gbs = cast_bytes / (cast_ms * 1e-3) / 1e9 if cast_ms > 0 else 0.0
-    tokens = B * S * args.steps
-    value = tokens / elapsed
+    value = r["tokens"] / elapsed
 
-    total_params = sf.total_params
-    layer_numel = sum(p.numel() for p in sf.decoder_layers[0].parameters())
-    resident = layer_numel + sum(p.numel() for p in sf.output_layer.parameters())
+    variants = {}
+    if not args.no_variants:
+        other = "bf16" if args.h2d_format == "fp32" else "fp32"
+        v = timed_run(model, w, args, dev, other, args.resident_layers, args.d2h_engine, batch_seed=1)
+        variants[f"h2d_{other}"] = {
+            "value": v["tokens"] / v["elapsed"], "ms_per_step": v["elapsed"] / args.steps * 1e3,
+            "h2d_format": other, "resident_layers": v["resident_layers"], "d2h_engine": args.d2h_engine,
+            "host_link": link_stats(v, args.steps), "losses": v["losses"],
+        }
+
+    total_params = r["total_params"]
+    layer_numel = r["layer_numel"]
+    resident = layer_numel + r["output_numel"]
     cpu = None
     if not args.no_cpu_baseline:
         t = time.time()
@@ -292,9 +355,13 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (uniform random token ids, random-init N(0,0.02) weights)",
         "config": {"workload": f"{w['model']} causal-LM training step, fp32 masters in pinned host memory, "
-                               f"layer-wise H2D + GPU cast, activation checkpoint offload, host LayerAdam",
+                               f"layer-wise H2D ({args.h2d_format}"
+                               f"{' + GPU RNE cast' if args.h2d_format == 'fp32' else ', host-cast in the AdamW pass'}), "
+                               f"activation checkpoint offload, grad D2H, host LayerAdam",
                    "global_batch": B, "seq_len": S, "layers": w["layers"], "hidden": w["hidden"],
-                   "params": total_params, "parallelism": "none (1 GPU)"},
+                   "params": total_params, "parallelism": "none (1 GPU)",
+                   "h2d_format": args.h2d_format, "resident_layers": r["resident_layers"],
+                   "d2h_engine": args.d2h_engine},
         "roofline": {
             "bound": "hbm",
             "kernel": "cast_flat_kernel (fp32 -> bf16 RNE staging cast)",
@@ -310,21 +377,12 @@ def main():
             "avg_launch_ms": cast_ms / ncast if ncast else None,
             "algorithmic_bytes_per_launch": cast_bytes / ncast if ncast else None,
         },
-        "host_link": {
-            "h2d_gbs": h2d_bytes / (h2d_ms * 1e-3) / 1e9 if h2d_ms > 0 else None,
-            "d2h_gbs": d2h_bytes / (d2h_ms * 1e-3) / 1e9 if d2h_ms > 0 else None,
-            "h2d_frac": (h2d_bytes / (h2d_ms * 1e-3) / 1e9) / LINK_PEAK_GBS if h2d_ms > 0 else None,
-            "d2h_frac": (d2h_bytes / (d2h_ms * 1e-3) / 1e9) / LINK_PEAK_GBS if d2h_ms > 0 else None,
-            "peak_gbs": LINK_PEAK_GBS,
-            "h2d_bytes_per_step": h2d_bytes / args.steps,
-            "d2h_bytes_per_step": d2h_bytes / args.steps,
-            "h2d_busy_frac": (h2d_ms * 1e-3) / elapsed,
-        },
+        "host_link": link_stats(r, args.steps),
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
         "losses": losses,
+        "variants": variants,
     }
     print(json.dumps(res), flush=True)
-    sf.close()
 
 
 if __name__ == "__main__":

@@ -224,7 +224,8 @@ class LayerAdamOracle:
 # Unit schedule of one training step
 # ---------------------------------------------------------------------------
 
-def step_schedule(num_decoders: int, act_offload: bool = True, first_decoder_first: bool = False) -> List[Tuple]:
+def step_schedule(num_decoders: int, act_offload: bool = True, first_decoder_first: bool = False,
+                  resident_units: Tuple[int, ...] = ()) -> List[Tuple]:
     """Expected order of staging events for one training step of a model with
     ``num_decoders`` decoder layers, units numbered 0 (embedding),
     1..L (decoders), L+1 (norm + lm_head).
@@ -248,6 +249,8 @@ def step_schedule(num_decoders: int, act_offload: bool = True, first_decoder_fir
     before the unit's backward is complete; the order of events is the same.
     ``first_decoder_first`` swaps the two initial loads (an ordering the
     reference does not use; the set of events is unchanged).
+    ``resident_units`` (not in the reference) keep their forward load for the
+    backward: their backward ("h2d", u, True) event is absent.
     Parity unpinned beyond this restatement: the reference has no tests.
     """
     L = num_decoders
@@ -262,7 +265,8 @@ def step_schedule(num_decoders: int, act_offload: bool = True, first_decoder_fir
     # backward: output unit first, then decoders L..1, then the embedding
     out.append(("d2h", L + 1))
     for i in range(L, 0, -1):
-        out.append(("h2d", i - 1, True))
+        if i - 1 not in resident_units:
+            out.append(("h2d", i - 1, True))
         if act_offload and i >= 2:
             out.append(("act_h2d", i - 1))
         out.append(("d2h", i))

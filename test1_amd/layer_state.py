@@ -34,6 +34,7 @@ plus the fp32 staging ring (``depth`` chunks of ``chunk_elems``).
 
 from __future__ import annotations
 
+import heapq
 import queue
 import threading
 import time
@@ -268,7 +269,7 @@ class GradStagingRing:
         for i in range(depth):
             self._free.put(i)
 
-    def acquire(self, timeout: Optional[float] = None) -> int:
+    def acquire(self, timeout: Optional[float] = None, unit: Optional[int] = None) -> int:
         try:
             return self._free.get(timeout=timeout)
         except queue.Empty:
@@ -278,6 +279,104 @@ class GradStagingRing:
         self._free.put(idx)
 
 
+class GradSlotsPerUnit:
+    """One pinned bf16 host slot per unit, sized to the unit.
+
+    A unit has at most one gradient offload outstanding (its next backward
+    follows its next forward, which waits for its update), so its slot is
+    always free: gradient D2H never waits for the host optimizer, and
+    updates may run in any order.  Costs 2 bytes of pinned host memory per
+    parameter.
+    """
+
+    def __init__(self, unit_sizes: Dict[int, int], dtype: torch.dtype = torch.bfloat16):
+        self.slots = {u: pinned_empty(max(1, n), dtype) for u, n in unit_sizes.items()}
+
+    def acquire(self, timeout: Optional[float] = None, unit: Optional[int] = None) -> int:
+        if unit not in self.slots:
+            raise KeyError(f"GradSlotsPerUnit: no slot for unit {unit}")
+        return unit
+
+    def release(self, idx: int) -> None:
+        return None
+
+
+class PriorityUpdateExecutor:
+    """One worker thread that runs queued host updates lowest priority value
+    first, among those whose input is ready.
+
+    The reference runs updates first-in first-out, i.e. in backward order
+    (slide_fsdp.py:163), so the units the next forward needs first are
+    updated last.  Taking the ready unit the next forward needs soonest lets
+    the next forward start while later units are still being updated.  Each
+    unit's update is independent of the others' within a step, so the order
+    does not change any result.
+
+    A task may carry a ``ready`` object with ``query()`` and ``synchronize()``
+    (a device event marking the end of its gradient copy).  Copies complete
+    in submission order (one copy stream), so when no queued task is ready
+    the worker waits for the oldest one, never for a later one.
+    """
+
+    def __init__(self, name: str):
+        self._tasks: list = []   # [priority, seq, future, fn, args, ready]
+        self._cv = threading.Condition()
+        self._seq = 0
+        self._stop = False
+        self._thread = threading.Thread(target=self._run, name=name, daemon=True)
+        self._thread.start()
+
+    def submit(self, priority: int, fn: Callable, *args, ready=None) -> Future:
+        f: Future = Future()
+        with self._cv:
+            if self._stop:
+                raise RuntimeError("PriorityUpdateExecutor: shut down")
+            self._tasks.append((priority, self._seq, f, fn, args, ready))
+            self._seq += 1
+            self._cv.notify()
+        return f
+
+    def _pick(self):
+        """Under the lock: (task, must_wait).  The lowest-priority ready task,
+        else the oldest task, to be waited for outside the lock."""
+        for t in sorted(self._tasks, key=lambda t: (t[0], t[1])):
+            if t[5] is None or t[5].query():
+                return t, False
+        return min(self._tasks, key=lambda t: t[1]), True
+
+    def _run(self) -> None:
+        while True:
+            with self._cv:
+                self._cv.wait_for(lambda: self._tasks or self._stop)
+                if not self._tasks:
+                    return
+                task, must_wait = self._pick()
+                if not must_wait:
+                    self._tasks.remove(task)
+            if must_wait:
+                try:
+                    task[5].synchronize()
+                except BaseException:
+                    pass  # the task itself reports the failure when it runs
+                with self._cv:
+                    task, _ = self._pick()
+                    self._tasks.remove(task)
+            _, _, f, fn, args, _ = task
+            if not f.set_running_or_notify_cancel():
+                continue
+            try:
+                f.set_result(fn(*args))
+            except BaseException as e:  # delivered to whoever waits on f
+                f.set_exception(e)
+
+    def shutdown(self, wait: bool = True) -> None:
+        with self._cv:
+            self._stop = True
+            self._cv.notify_all()
+        if wait and self._thread is not threading.current_thread():
+            self._thread.join()
+
+
 class StreamingRuntime:
     """Objects shared by all units of one model: streams, pool, stager, grad
     ring, worker threads and the optional event trace."""
@@ -285,8 +384,8 @@ class StreamingRuntime:
     def __init__(self, device: torch.device, dtype: torch.dtype, max_param_size: int, pool_size: int,
                  stage_chunk_elems: int, stage_depth: int, grad_ring_depth: int, wait_timeout: Optional[float],
                  d2h_workgroups: int = 8, d2h_engine: str = "kernel", h2d_format: str = "fp32"):
-        if d2h_engine not in ("sdma", "kernel"):
-            raise ValueError("d2h_engine must be 'sdma' or 'kernel'")
+        if d2h_engine not in ("sdma", "kernel", "copy"):
+            raise ValueError("d2h_engine must be 'kernel', 'copy' or 'sdma'")
         if h2d_format not in ("fp32", "bf16"):
             raise ValueError("h2d_format must be 'fp32' or 'bf16'")
         if h2d_format == "bf16" and dtype != torch.bfloat16:
@@ -298,9 +397,10 @@ class StreamingRuntime:
         self.h2d_format = h2d_format
         # Gradient D2H: "kernel" (default) packs them with a capped-grid kernel
         # writing into host memory, ~49 GB/s while the link is busy the other
-        # way; "sdma" hands them to SDMA engines through ROCr (no shader
-        # traffic, but engines shared with HIP's own copies left it at
-        # 14 GB/s in the training step).
+        # way, but it slows kernels running beside it; "copy" issues one
+        # stream-ordered DMA copy per parameter (no shader traffic); "sdma"
+        # hands them to SDMA engines through ROCr (engines shared with HIP's
+        # own copies left it at 14 GB/s in the training step).
         self.d2h_engine = d2h_engine
         if d2h_engine == "sdma":
             kernels.dma_init(device)
@@ -317,12 +417,18 @@ class StreamingRuntime:
             self.stager = BF16Loader(self.h2d_stream)
         else:
             self.stager = H2DStager(device, stage_chunk_elems, stage_depth, self.h2d_stream, self.cast_stream)
-        self.grad_ring = GradStagingRing(grad_ring_depth, max_param_size, dtype)
+        # Gradient host slots: a ring of ``grad_ring_depth`` max-size slots,
+        # or (None) one slot per unit, set up by ``init_grad_slots``.
+        self.grad_ring = None if grad_ring_depth is None else GradStagingRing(grad_ring_depth, max_param_size, dtype)
+        self._dtype = dtype
         # One thread issues gradient offloads (it may wait for a free host
         # slot); one thread runs the host optimizer, as the reference's
         # update executor (slide_fsdp.py:163).
         self.offload_executor = ThreadPoolExecutor(max_workers=1, thread_name_prefix="sf-offload")
-        self.update_executor = ThreadPoolExecutor(max_workers=1, thread_name_prefix="sf-update")
+        self.update_executor = PriorityUpdateExecutor("sf-update")
+        # Queue priority of a unit's update (lower runs first); the model sets
+        # it to the unit's position in the next forward.
+        self.update_priority: Callable[[int], int] = lambda unit: unit
         self.wait_timeout = wait_timeout
         self.trace: Optional[List[Tuple]] = None
         self._trace_lock = threading.Lock()
@@ -334,6 +440,10 @@ class StreamingRuntime:
         # {("device_grads", unit): [param.grad clones]}, for checking the
         # pack and the update against the oracle.
         self.capture: Optional[dict] = None
+
+    def init_grad_slots(self, unit_sizes: Dict[int, int]) -> None:
+        if self.grad_ring is None:
+            self.grad_ring = GradSlotsPerUnit(unit_sizes, self._dtype)
 
     def log(self, *event) -> None:
         if self.trace is not None:
@@ -376,6 +486,9 @@ class LayerRuntimeState(nn.Module):
         self._d2h_future: Optional[Future] = None
         self._update_future: Optional[Future] = None
         self._current_gpu_cache: Optional[Dict[str, Any]] = None
+        # A unit of its own (``make_resident``): loaded in the forward and
+        # kept on the device through the backward, never taken from the pool.
+        self._own_unit: Optional[Dict[str, Any]] = None
         self._post_called = False
         self._bwd_armed = False
         self._bwd_compute_done = False
@@ -450,20 +563,20 @@ class LayerRuntimeState(nn.Module):
         streaming while an earlier unit is still busy.
         """
         if self._current_gpu_cache is not None:
-            return  # already resident (last decoder / output unit)
+            return  # already resident (last decoder / output / own unit)
         self.wait_for_update()
         stager = self.runtime.stager
         # The backward of an embedding never reads its weights (its gradient
         # depends only on the indices), so no copy or cast is needed then.
         skip = is_backward and not self.backward_reads_params
         if self._cpu_params_bf16 is not None:
-            unit = self.buffer_pool.acquire(timeout=self.runtime.wait_timeout)
+            unit = self._acquire_unit()
             self._h2d_done = unit["ready"] if skip else stager.load(self._cpu_params_bf16, unit["param"], unit["ready"])
             self._bind_unit(unit, is_backward)
             return
         ticket = None if skip else stager.begin(self._cpu_params_flat)
         try:
-            unit = self.buffer_pool.acquire(timeout=self.runtime.wait_timeout)
+            unit = self._acquire_unit()
         except BaseException:
             if ticket is not None:
                 stager.finish(ticket, self._dummy_dst(), None)
@@ -473,6 +586,32 @@ class LayerRuntimeState(nn.Module):
         else:
             self._h2d_done = stager.finish(ticket, unit["param"], unit["ready"])
         self._bind_unit(unit, is_backward)
+
+    def make_resident(self, buffer: torch.Tensor) -> None:
+        """Give this unit a device buffer of its own (at least ``total_size``
+        elements of the pool dtype).  Its weights are then loaded once per
+        step, in the forward, and stay on the device until its backward has
+        finished: the backward reload of the reference (slide_fsdp.py:443-444)
+        is skipped.  The staged bits are the same either way, since the master
+        only changes in the update that follows the backward."""
+        if buffer.numel() < self.total_size or buffer.dtype != self.buffer_pool.dtype:
+            raise ValueError("make_resident: buffer too small or of the wrong dtype")
+        if self._current_gpu_cache is not None:
+            raise RuntimeError("make_resident: unit is loaded")
+        self._own_unit = {"param": buffer, "grad": None, "ready": None}
+
+    @property
+    def resident_across_steps(self) -> bool:
+        return self._own_unit is not None
+
+    def _acquire_unit(self) -> Dict[str, Any]:
+        if self._own_unit is not None:
+            return self._own_unit
+        return self.buffer_pool.acquire(timeout=self.runtime.wait_timeout)
+
+    def _release_unit(self, unit: Dict[str, Any]) -> None:
+        if unit is not self._own_unit:
+            self.buffer_pool.release(unit)
 
     def _bind_unit(self, unit: Dict[str, Any], is_backward: bool) -> None:
         unit["ready"] = None
@@ -516,6 +655,8 @@ class LayerRuntimeState(nn.Module):
             return
         cur = torch.cuda.current_stream()
         if not is_backward:
+            if unit is self._own_unit:
+                return  # stays loaded for the backward
             ev = _new_event()
             ev.record(cur)
             unit["ready"] = ev
@@ -570,13 +711,13 @@ class LayerRuntimeState(nn.Module):
         unit["ready"] = ev
         self._bind_host_views()
         self._current_gpu_cache = None
-        self.buffer_pool.release(unit)
+        self._release_unit(unit)
 
     def _d2h_task(self, grads: List[Tuple[torch.Tensor, int]], missing: List[Tuple[int, int]],
                   grad_ready: torch.cuda.Event, cast_fence: Optional[torch.cuda.Event] = None) -> None:
         rt = self.runtime
         rt.mark("d2h_task", self.layer_idx)
-        slot = rt.grad_ring.acquire(timeout=rt.wait_timeout)
+        slot = rt.grad_ring.acquire(timeout=rt.wait_timeout, unit=self.layer_idx)
         rt.mark("slot", self.layer_idx)
         try:
             host = rt.grad_ring.slots[slot]
@@ -598,7 +739,12 @@ class LayerRuntimeState(nn.Module):
                 if timing:
                     t0 = torch.cuda.Event(enable_timing=True)
                     t0.record(rt.d2h_stream)
-                kernels.copy_segs_b16(pairs, rt.d2h_stream, max_workgroups=rt.d2h_workgroups)
+                if rt.d2h_engine == "copy":
+                    # stream-ordered DMA copies, one per parameter
+                    for g, h in pairs:
+                        kernels.memcpy_async(h, g, rt.d2h_stream)
+                else:
+                    kernels.copy_segs_b16(pairs, rt.d2h_stream, max_workgroups=rt.d2h_workgroups)
                 for g, _ in grads:
                     g.record_stream(rt.d2h_stream)
                 done = torch.cuda.Event(enable_timing=True) if timing else _new_event()
@@ -615,7 +761,8 @@ class LayerRuntimeState(nn.Module):
         # waited for; the caching allocator cannot hand them out before then.
         keep = grads if handle is not None else None
         del grads, pairs
-        self._update_future = rt.update_executor.submit(self._do_update, slot, done, missing, handle, keep, nbytes)
+        self._update_future = rt.update_executor.submit(rt.update_priority(self.layer_idx), self._do_update,
+                                                        slot, done, missing, handle, keep, nbytes, ready=done)
 
     def wait_for_d2h(self, timeout: Optional[float] = None) -> None:
         """Wait until the gradient offload has been issued (and re-raise its

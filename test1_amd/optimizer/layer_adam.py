@@ -14,10 +14,14 @@ Differences, all deliberate:
   * param groups are also looked up by the ``layer_idx`` they were added
     with, so a unit without parameters (``add_layer_params`` returning -1)
     does not shift later indices.
+  * each instance owns its own native optimizer id (the reference always
+    uses 0, layer_adam.py:59), so two instances in one process do not share
+    or destroy each other's bias-correction state.
 """
 
 from __future__ import annotations
 
+import itertools
 import math
 from collections import OrderedDict, defaultdict
 from typing import Any, DefaultDict, Dict, Iterable, Optional
@@ -29,6 +33,8 @@ from . import cpu_adam as _cpu_adam
 
 class LayerAdam:
     """Layer-wise AdamW over fp32 host parameters (reference layer_adam.py:9-27)."""
+
+    _ids = itertools.count()
 
     def __init__(
         self,
@@ -49,7 +55,10 @@ class LayerAdam:
         self.param_groups = []
         self._groups_by_layer: Dict[int, dict] = {}
         self.cpu_adam = _cpu_adam
-        self.optimizer_id = 0  # one native optimizer for every layer, as the reference
+        # One native optimizer for every layer, as the reference (which always
+        # uses id 0); ids are unique per instance here so that the destructor
+        # of one LayerAdam cannot remove another's state.
+        self.optimizer_id = next(LayerAdam._ids)
         self.cpu_adam.create_adam(self.optimizer_id, lr, betas[0], betas[1], eps, weight_decay, adamw_mode, True)
         self.fp32_optimizer_state = fp32_optimizer_state
         self.num_layer = num_layer

@@ -108,7 +108,10 @@ class SlideFSDP(nn.Module):
                          largest unit, i.e. one chunk per unit)
       stage_depth        staging ring depth (default 3: copies may run up to
                          two units ahead of the unit being cast)
-      grad_ring_depth    pinned gradient slots (default 3)
+      grad_ring_depth    pinned gradient slots of the largest unit's size, or
+                         None (default): one slot per unit, sized to it, so
+                         gradient offload never waits for the host optimizer
+                         (2 bytes of pinned host memory per parameter)
       wait_timeout       seconds before a host wait raises TimeoutError
                          (default None: wait forever, as the reference)
       d2h_engine         "kernel" (default): gradient D2H by a capped-grid pack
@@ -118,11 +121,20 @@ class SlideFSDP(nn.Module):
                          host optimizer keeps a bf16 copy of every master
                          (written in its update pass) and that crosses the
                          link, half the bytes.  Both stage the same bits.
+      resident_layers    decoder layers (the last ones, besides the last
+                         decoder, which always stays) given a device buffer
+                         of their own: loaded once per step in the forward
+                         and kept for the backward instead of reloaded.
+                         Costs 2 bytes per parameter of HBM per layer.
+                         None (default): as many as fit in half of the free
+                         device memory; 0: reload every unit, as the
+                         reference (slide_fsdp.py:443-444).
     """
 
     def __init__(self, model, config: SlideFSDPConfig, *, stage_chunk_elems: Optional[int] = None,
-                 stage_depth: int = 3, grad_ring_depth: int = 3, wait_timeout: Optional[float] = None,
-                 d2h_engine: str = "kernel", h2d_format: str = "fp32"):
+                 stage_depth: int = 3, grad_ring_depth: Optional[int] = None, wait_timeout: Optional[float] = None,
+                 d2h_engine: str = "kernel", h2d_format: str = "fp32",
+                 resident_layers: Optional[int] = None):
         super().__init__()
         if config.param_transfer_mode != "full":
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
@@ -157,6 +169,11 @@ class SlideFSDP(nn.Module):
         self.layer_optimizer = self._create_optimizer(config)
         self.layer_states: List[LayerRuntimeState] = []
         self._create_layer_states()
+        self.runtime.init_grad_slots({s.layer_idx: s.total_size for s in self.layer_states})
+        # Updates run in the order the next forward loads units: the first
+        # decoder, then the embedding, then the rest.
+        self.runtime.update_priority = lambda u: 1 - u if u <= 1 else u
+        self._make_resident(self._auto_resident() if resident_layers is None else int(resident_layers))
         self._setup_autograd_functions()
 
         # The recompute must replay the forward's random numbers only if a
@@ -213,6 +230,34 @@ class SlideFSDP(nn.Module):
             self.layer_states.append(LayerRuntimeState(layer, idx, self.config, self.runtime, self.layer_optimizer,
                                                        is_last_layer=(idx == n - 1)))
 
+    def _auto_resident(self) -> int:
+        """Decoder layers whose weights fit in half of the free device memory."""
+        n_dec = len(self.layer_states) - 2
+        if n_dec < 2:
+            return 0
+        free, _ = torch.cuda.mem_get_info(self.device)
+        budget = free // 2
+        elem = torch.empty((), dtype=self.dtype).element_size()
+        k = 0
+        for unit_idx in range(n_dec - 1, 0, -1):  # from the second-to-last decoder down
+            need = self.layer_states[unit_idx].total_size * elem
+            if need > budget:
+                break
+            budget -= need
+            k += 1
+        return k
+
+    def _make_resident(self, k: int) -> None:
+        n_dec = len(self.layer_states) - 2
+        if k < 0 or k > max(0, n_dec - 1):
+            raise ValueError(f"resident_layers must be in [0, {max(0, n_dec - 1)}]")
+        # decoder units n_dec - 1 - k .. n_dec - 1 (unit index = decoder + 1);
+        # the last decoder (unit n_dec) stays loaded through the pool anyway
+        for unit_idx in range(n_dec - k, n_dec):
+            st = self.layer_states[unit_idx]
+            st.make_resident(torch.empty(st.total_size, dtype=self.dtype, device=self.device))
+        self.resident_layers = k
+
     # ------------------------------------------------------------------
     def _setup_autograd_functions(self) -> None:
         """Autograd functions around each unit (reference slide_fsdp.py:343-430).
@@ -263,10 +308,11 @@ class SlideFSDP(nn.Module):
         self._PreLayerFunction = PreLayerFunction
         self._PostLayerFunction = PostLayerFunction
 
+        self._hook_handles = []
         for idx, state in enumerate(self.layer_states):
             state._post_called = False
             for p in state._grad_params:
-                p.register_post_accumulate_grad_hook(self._make_grad_hook(state, idx))
+                self._hook_handles.append(p.register_post_accumulate_grad_hook(self._make_grad_hook(state, idx)))
 
     def _make_grad_hook(self, state: LayerRuntimeState, idx: int):
         def hook(param):
@@ -470,10 +516,15 @@ class SlideFSDP(nn.Module):
         return output_dir
 
     def close(self) -> None:
-        """Finish queued work and stop the worker threads."""
+        """Finish queued work, stop the worker threads and detach the
+        gradient hooks from the model's parameters (which would otherwise keep
+        this wrapper's host state alive)."""
         try:
             self.wait_for_updates()
         finally:
+            for h in getattr(self, "_hook_handles", []):
+                h.remove()
+            self._hook_handles = []
             self.runtime.shutdown()
 
     def __del__(self):

@@ -40,29 +40,38 @@ def u16(t):
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-def test_schedule_matches_oracle(dev):
+@pytest.mark.parametrize("resident", [0, L - 1])
+def test_schedule_matches_oracle(dev, resident):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
-    sf = SlideFSDP(make_model(), SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD), wait_timeout=120)
-    ids = batches(1)[0].to(dev)
-    sf.runtime.trace = []
-    sf(input_ids=ids, labels=ids)
-    sf.wait_for_updates()
-    assert sf.runtime.trace == oracle.step_schedule(L, first_decoder_first=True)
+    sf = SlideFSDP(make_model(), SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD), wait_timeout=120,
+                   resident_layers=resident)
+    ids = batches(2)
+    for k in range(2):
+        sf.runtime.trace = []
+        sf(input_ids=ids[k].to(dev), labels=ids[k].to(dev))
+        sf.wait_for_updates()
+        # resident decoders are units L - resident .. L - 1
+        exp = oracle.step_schedule(L, first_decoder_first=True, resident_units=tuple(range(L - resident, L)))
+        assert sf.runtime.trace == exp, f"step {k}"
     sf.close()
 
 
-@pytest.mark.parametrize("h2d_format", ["fp32", "bf16"])
-def test_updates_match_oracle_bit_exact(dev, h2d_format):
+MODES = [("fp32", 0), ("bf16", 0), ("fp32", L - 1), ("bf16", L - 1)]
+
+
+@pytest.mark.parametrize("h2d_format,resident", MODES)
+def test_updates_match_oracle_bit_exact(dev, h2d_format, resident):
     """Every unit's host update equals the oracle AdamW applied to the same
     (captured) bf16 grads and fp32 master, for 3 steps.  With bf16 H2D the
     host bf16 copy of every unit is the oracle cast of its master after each
-    step, so both formats stage the same bits."""
+    step, so both formats stage the same bits.  ``resident`` decoder layers
+    keep their forward weights for the backward."""
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model()
     sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS),
-                   wait_timeout=120, h2d_format=h2d_format)
+                   wait_timeout=120, h2d_format=h2d_format, resident_layers=resident)
     orc = oracle.LayerAdamOracle(lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
     ref_units = []
     for ps in units_of(model):
@@ -131,15 +140,15 @@ def reference_losses(model, steps_ids, dev):
     return losses, first_grads
 
 
-@pytest.mark.parametrize("h2d_format", ["fp32", "bf16"])
-def test_loss_parity_with_non_offloaded_run(dev, h2d_format):
+@pytest.mark.parametrize("h2d_format,resident", MODES)
+def test_loss_parity_with_non_offloaded_run(dev, h2d_format, resident):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model()
     steps = batches(10)
     ref_losses, ref_grads = reference_losses(model, steps, dev)
     sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS),
-                   wait_timeout=120, h2d_format=h2d_format)
+                   wait_timeout=120, h2d_format=h2d_format, resident_layers=resident)
     losses = []
     for k, ids in enumerate(steps):
         if k == 0:

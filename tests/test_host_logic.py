@@ -7,6 +7,7 @@ import time
 import pytest
 import torch
 
+import oracle
 from test1_amd.layer_state import LayerBufferPool
 
 
@@ -40,3 +41,81 @@ def test_distributed_sync_factory_single_process():
 
     s = create_distributed_sync(SlideFSDPConfig(device=torch.device("cpu")))
     assert isinstance(s, NoOpSync) and s.world_size == 1 and s.rank == 0
+
+
+def test_step_schedule_resident_units_drop_backward_loads():
+    full = oracle.step_schedule(4, first_decoder_first=True)
+    res = oracle.step_schedule(4, first_decoder_first=True, resident_units=(2, 3))
+    assert [e for e in full if e not in (("h2d", 2, True), ("h2d", 3, True))] == res
+    assert len(full) - len(res) == 2
+
+
+def test_priority_update_executor_runs_lowest_first_and_reports_errors():
+    from test1_amd.layer_state import PriorityUpdateExecutor
+
+    ex = PriorityUpdateExecutor("test-upd")
+    gate = threading.Event()
+    order = []
+    first = ex.submit(0, gate.wait, 10)  # holds the worker while the rest queue up
+    futs = [ex.submit(p, order.append, p) for p in (5, 3, 7, 1, 3)]
+    bad = ex.submit(4, lambda: 1 / 0)
+    gate.set()
+    for f in futs:
+        f.result(timeout=10)
+    assert first.result(timeout=10) is True
+    assert order == [1, 3, 3, 5, 7]
+    with pytest.raises(ZeroDivisionError):
+        bad.result(timeout=10)
+    ex.shutdown(wait=True)
+    with pytest.raises(RuntimeError):
+        ex.submit(0, order.append, 0)
+
+
+class _FakeReady:
+    """Stands in for a copy-completion event; ``synchronize`` completes it."""
+
+    def __init__(self, log, name):
+        self.done, self.log, self.name = False, log, name
+
+    def query(self):
+        return self.done
+
+    def synchronize(self):
+        self.log.append(("waited", self.name))
+        self.done = True
+
+
+def test_priority_update_executor_skips_tasks_whose_input_is_not_ready():
+    from test1_amd.layer_state import PriorityUpdateExecutor
+
+    ex = PriorityUpdateExecutor("test-upd2")
+    gate = threading.Event()
+    log = []
+    ex.submit(-1, gate.wait, 10)
+    r_old, r_new = _FakeReady(log, "old"), _FakeReady(log, "new")
+    ready_mid = _FakeReady(log, "mid")
+    ready_mid.done = True
+    # priority 1 is not ready: the ready priority-5 task runs first, then the
+    # worker waits for the OLDEST pending copy (priority 9), never the newer one
+    f9 = ex.submit(9, log.append, 9, ready=r_old)
+    f5 = ex.submit(5, log.append, 5, ready=ready_mid)
+    f1 = ex.submit(1, log.append, 1, ready=r_new)
+    gate.set()
+    for f in (f9, f5, f1):
+        f.result(timeout=10)
+    assert log == [5, ("waited", "old"), 9, ("waited", "new"), 1]
+    ex.shutdown(wait=True)
+
+
+def test_grad_slots_per_unit_are_sized_and_never_block(monkeypatch):
+    from test1_amd import layer_state
+    from test1_amd.layer_state import GradSlotsPerUnit
+
+    # pinned memory needs a GPU; plain host tensors stand in for it here
+    monkeypatch.setattr(layer_state, "pinned_empty", lambda n, dt: torch.empty(n, dtype=dt))
+    slots = GradSlotsPerUnit({0: 10, 1: 0, 2: 7}, torch.bfloat16)
+    assert slots.slots[0].numel() == 10 and slots.slots[2].numel() == 7
+    assert slots.acquire(timeout=0, unit=2) == 2 and slots.acquire(timeout=0, unit=2) == 2
+    slots.release(2)
+    with pytest.raises(KeyError):
+        slots.acquire(unit=5)

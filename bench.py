@@ -289,7 +289,7 @@ def main():
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the second timed run with the other parameter H2D format")
     ap.add_argument("--timeline", default="", help="write the host timeline of the timed steps to this file")
-    ap.add_argument("--d2h-engine", default="kernel", choices=("sdma", "kernel", "copy"),
+    ap.add_argument("--d2h-engine", default="sdma", choices=("sdma", "kernel", "copy"),
                     help="gradient D2H by a capped pack kernel, by DMA copies, or on SDMA engines via ROCr")
     ap.add_argument("--h2d-format", default="fp32", choices=("fp32", "bf16"),
                     help="parameter H2D as fp32 masters + GPU cast, or as the host optimizer's bf16 copy")

@@ -182,10 +182,18 @@ int sf_dma_copy_d2h(const sf_seg* segs, int nsegs, uint64_t* signals,
                     int max_signals, int* nsignals);
 
 /* Block until every handle completed, then release them.  If start_ns and
- * end_ns are non-null and timing is enabled, they receive the earliest start
- * and latest end of the copies (GPU clock, ns). */
+ * end_ns are non-null and timing is enabled, *start_ns receives 0 and
+ * *end_ns the time from the earliest start to the latest end of the copies
+ * in ns (both 0 when timing is off). */
 int sf_dma_wait(const uint64_t* signals, int nsignals, uint64_t* start_ns,
                 uint64_t* end_ns);
+
+/* Non-blocking completion test of copies started by sf_dma_copy_d2h:
+ * *done = 1 when every signal has completed, else 0.  The signals stay
+ * valid (sf_dma_wait still has to be called to release them).  No
+ * reference counterpart (the reference's D2H is a blocking torch copy,
+ * layer_state.py:367-393); used to run host updates as their copies land. */
+int sf_dma_query(const uint64_t* signals, int nsignals, int* done);
 
 /* Record start/end times of later copies (1) or stop (0). */
 int sf_dma_enable_timing(int on);

@@ -73,6 +73,7 @@ HIP_SIGNATURES = {
     "sf_dma_copy_d2h": [ctypes.POINTER(SfSeg), _i, ctypes.POINTER(ctypes.c_uint64), _i, ctypes.POINTER(_i)],
     "sf_dma_wait": [ctypes.POINTER(ctypes.c_uint64), _i, ctypes.POINTER(ctypes.c_uint64),
                     ctypes.POINTER(ctypes.c_uint64)],
+    "sf_dma_query": [ctypes.POINTER(ctypes.c_uint64), _i, ctypes.POINTER(ctypes.c_int)],
     "sf_dma_enable_timing": [_i],
 }
 

@@ -414,6 +414,7 @@ struct DmaAgents {
     int device = -1;
     bool ok = false;
     uint32_t engine_mask = 0;  // one SDMA engine bit; 0: runtime's choice
+    uint64_t ts_freq = 0;      // HSA system timestamp ticks per second
 };
 DmaAgents g_dma;
 std::mutex g_dma_mu;
@@ -463,6 +464,10 @@ int sf_dma_init(int device) {
     g_dma.gpu = sc.gpu;
     g_dma.cpu = sc.cpu;
     g_dma.device = device;
+    // Copy profiling times come in system timestamp ticks.
+    uint64_t freq = 0;
+    if (hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP_FREQUENCY, &freq) != HSA_STATUS_SUCCESS) freq = 0;
+    g_dma.ts_freq = freq;
     g_dma.ok = true;
     // Engines for device -> host copies.  HIP's own host<->device copies run
     // on the first SDMA engines, and a copy queued on the same engine waits
@@ -565,10 +570,28 @@ int sf_dma_wait(const uint64_t* signals, int nsignals, uint64_t* start_ns, uint6
         if (st != HSA_STATUS_SUCCESS && rc == SF_OK) rc = hsa_status_to_sf(st);
     }
     if (start_ns != nullptr && end_ns != nullptr) {
-        *start_ns = t0 == UINT64_MAX ? 0 : t0;
-        *end_ns = t1;
+        if (t0 == UINT64_MAX || g_dma.ts_freq == 0) {
+            *start_ns = *end_ns = 0;
+        } else {
+            // ticks -> ns, relative to the first start (avoids overflow)
+            *start_ns = 0;
+            *end_ns = uint64_t((long double)(t1 - t0) * 1e9L / (long double)g_dma.ts_freq);
+        }
     }
     return rc;
+}
+
+int sf_dma_query(const uint64_t* signals, int nsignals, int* done) {
+    if (done == nullptr || nsignals < 0 || (nsignals > 0 && signals == nullptr)) return SF_EINVAL;
+    *done = 1;
+    for (int i = 0; i < nsignals; ++i) {
+        if (signals[i] == 0) continue;
+        if (hsa_signal_load_scacquire(hsa_signal_t{signals[i]}) >= 1) {
+            *done = 0;
+            break;
+        }
+    }
+    return SF_OK;
 }
 
 int sf_dma_enable_timing(int on) {

@@ -9,6 +9,7 @@ asynchronous on ``stream`` (default: the current stream).
 from __future__ import annotations
 
 import ctypes
+import time
 import os
 from typing import Optional, Sequence, Tuple
 
@@ -244,6 +245,29 @@ def dma_copy_d2h(pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]]):
     _native.check(_native.hip().sf_dma_copy_d2h(arr, len(segs), handles, cap, ctypes.byref(count)),
                   "sf_dma_copy_d2h")
     return (handles, count.value)
+
+
+def dma_query(handle) -> bool:
+    """True once every copy of ``handle`` has completed (does not release it)."""
+    handles, n = handle
+    done = ctypes.c_int(0)
+    _native.check(_native.hip().sf_dma_query(handles, n, ctypes.byref(done)), "sf_dma_query")
+    return bool(done.value)
+
+
+class DmaReady:
+    """``query()`` / ``synchronize()`` view of an SDMA copy handle, the
+    interface of a device event."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    def query(self) -> bool:
+        return dma_query(self.handle)
+
+    def synchronize(self) -> None:
+        while not dma_query(self.handle):
+            time.sleep(50e-6)
 
 
 def dma_wait(handle) -> Tuple[int, int]:

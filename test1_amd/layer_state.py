@@ -383,7 +383,7 @@ class StreamingRuntime:
 
     def __init__(self, device: torch.device, dtype: torch.dtype, max_param_size: int, pool_size: int,
                  stage_chunk_elems: int, stage_depth: int, grad_ring_depth: int, wait_timeout: Optional[float],
-                 d2h_workgroups: int = 8, d2h_engine: str = "kernel", h2d_format: str = "fp32"):
+                 d2h_workgroups: int = 8, d2h_engine: str = "sdma", h2d_format: str = "fp32"):
         if d2h_engine not in ("sdma", "kernel", "copy"):
             raise ValueError("d2h_engine must be 'kernel', 'copy' or 'sdma'")
         if h2d_format not in ("fp32", "bf16"):
@@ -395,12 +395,13 @@ class StreamingRuntime:
         # them on the GPU; "bf16" copies a bf16 host copy that the optimizer
         # keeps current, half the bytes on the host link.
         self.h2d_format = h2d_format
-        # Gradient D2H: "kernel" (default) packs them with a capped-grid kernel
-        # writing into host memory, ~49 GB/s while the link is busy the other
-        # way, but it slows kernels running beside it; "copy" issues one
-        # stream-ordered DMA copy per parameter (no shader traffic); "sdma"
-        # hands them to SDMA engines through ROCr (engines shared with HIP's
-        # own copies left it at 14 GB/s in the training step).
+        # Gradient D2H: "sdma" (default) hands them to SDMA engines of their
+        # own through ROCr, ~50 GB/s with no shader traffic, so the backward
+        # kernels beside it run at full speed; "kernel" packs them with a
+        # capped-grid kernel writing into host memory (~49 GB/s, but every
+        # kernel running beside a PCIe-writing kernel slows down, the GEMMs
+        # ~2-4x); "copy" issues one hipMemcpyAsync per parameter, which the
+        # runtime performs with a blit kernel (~18 GB/s).
         self.d2h_engine = d2h_engine
         if d2h_engine == "sdma":
             kernels.dma_init(device)
@@ -762,7 +763,8 @@ class LayerRuntimeState(nn.Module):
         keep = grads if handle is not None else None
         del grads, pairs
         self._update_future = rt.update_executor.submit(rt.update_priority(self.layer_idx), self._do_update,
-                                                        slot, done, missing, handle, keep, nbytes, ready=done)
+                                                        slot, done, missing, handle, keep, nbytes,
+                                                        ready=done if handle is None else kernels.DmaReady(handle))
 
     def wait_for_d2h(self, timeout: Optional[float] = None) -> None:
         """Wait until the gradient offload has been issued (and re-raise its

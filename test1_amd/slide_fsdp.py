@@ -114,8 +114,10 @@ class SlideFSDP(nn.Module):
                          (2 bytes of pinned host memory per parameter)
       wait_timeout       seconds before a host wait raises TimeoutError
                          (default None: wait forever, as the reference)
-      d2h_engine         "kernel" (default): gradient D2H by a capped-grid pack
-                         kernel into host memory; "sdma": on SDMA engines
+      d2h_engine         "sdma" (default): gradient D2H on SDMA engines of its
+                         own; "kernel": by a capped-grid pack kernel writing
+                         into host memory (slows the backward kernels beside
+                         it); "copy": hipMemcpyAsync per parameter
       h2d_format         "fp32" (default): the fp32 masters cross the host
                          link and are cast to bf16 on the GPU; "bf16": the
                          host optimizer keeps a bf16 copy of every master
@@ -133,7 +135,7 @@ class SlideFSDP(nn.Module):
 
     def __init__(self, model, config: SlideFSDPConfig, *, stage_chunk_elems: Optional[int] = None,
                  stage_depth: int = 3, grad_ring_depth: Optional[int] = None, wait_timeout: Optional[float] = None,
-                 d2h_engine: str = "kernel", h2d_format: str = "fp32",
+                 d2h_engine: str = "sdma", h2d_format: str = "fp32",
                  resident_layers: Optional[int] = None):
         super().__init__()
         if config.param_transfer_mode != "full":

@@ -57,11 +57,13 @@ def test_schedule_matches_oracle(dev, resident):
     sf.close()
 
 
-MODES = [("fp32", 0), ("bf16", 0), ("fp32", L - 1), ("bf16", L - 1)]
+# (parameter H2D format, resident decoder layers, gradient D2H engine)
+MODES = [("fp32", 0, "sdma"), ("bf16", 0, "sdma"), ("fp32", L - 1, "sdma"), ("bf16", L - 1, "sdma"),
+         ("fp32", 0, "kernel"), ("bf16", L - 1, "kernel")]
 
 
-@pytest.mark.parametrize("h2d_format,resident", MODES)
-def test_updates_match_oracle_bit_exact(dev, h2d_format, resident):
+@pytest.mark.parametrize("h2d_format,resident,d2h_engine", MODES)
+def test_updates_match_oracle_bit_exact(dev, h2d_format, resident, d2h_engine):
     """Every unit's host update equals the oracle AdamW applied to the same
     (captured) bf16 grads and fp32 master, for 3 steps.  With bf16 H2D the
     host bf16 copy of every unit is the oracle cast of its master after each
@@ -71,7 +73,7 @@ def test_updates_match_oracle_bit_exact(dev, h2d_format, resident):
 
     model = make_model()
     sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS),
-                   wait_timeout=120, h2d_format=h2d_format, resident_layers=resident)
+                   wait_timeout=120, h2d_format=h2d_format, resident_layers=resident, d2h_engine=d2h_engine)
     orc = oracle.LayerAdamOracle(lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
     ref_units = []
     for ps in units_of(model):
@@ -140,15 +142,15 @@ def reference_losses(model, steps_ids, dev):
     return losses, first_grads
 
 
-@pytest.mark.parametrize("h2d_format,resident", MODES)
-def test_loss_parity_with_non_offloaded_run(dev, h2d_format, resident):
+@pytest.mark.parametrize("h2d_format,resident,d2h_engine", MODES)
+def test_loss_parity_with_non_offloaded_run(dev, h2d_format, resident, d2h_engine):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model()
     steps = batches(10)
     ref_losses, ref_grads = reference_losses(model, steps, dev)
     sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS),
-                   wait_timeout=120, h2d_format=h2d_format, resident_layers=resident)
+                   wait_timeout=120, h2d_format=h2d_format, resident_layers=resident, d2h_engine=d2h_engine)
     losses = []
     for k, ids in enumerate(steps):
         if k == 0:

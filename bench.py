@@ -104,16 +104,29 @@ def traffic_factor():
 
 
 def elapsed_stats(records):
-    """(total ms, total bytes or elements) from (start_event, end_event, amount)
-    records or from (ms, amount) records."""
+    """(busy ms, total bytes or elements) from (start_event, end_event, amount)
+    records (summed) or ("interval_ns", start, end, amount) records of copies
+    that may overlap one another (busy = union of the intervals)."""
     ms = amt = 0.0
-    for r in records:
-        if len(r) == 3:
+    intervals = []
+    for r in records or []:
+        if len(r) == 4:
+            intervals.append((r[1], r[2]))
+            amt += r[3]
+        else:
             ms += r[0].elapsed_time(r[1])
             amt += r[2]
+    intervals.sort()
+    cur_s = cur_e = None
+    for s, e in intervals:
+        if cur_e is None or s > cur_e:
+            if cur_e is not None:
+                ms += (cur_e - cur_s) * 1e-6
+            cur_s, cur_e = s, e
         else:
-            ms += r[0]
-            amt += r[1]
+            cur_e = max(cur_e, e)
+    if cur_e is not None:
+        ms += (cur_e - cur_s) * 1e-6
     return ms, amt
 
 
@@ -263,6 +276,17 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
     return r
 
 
+def host_mem_available() -> int:
+    """MemAvailable of this host in bytes (0 if unknown)."""
+    try:
+        for line in open("/proc/meminfo"):
+            if line.startswith("MemAvailable:"):
+                return int(line.split()[1]) * 1024
+    except OSError:
+        pass
+    return 0
+
+
 def link_stats(r: dict, steps: int) -> dict:
     (h2d_ms, h2d_bytes), (d2h_ms, d2h_bytes) = r["h2d"], r["d2h"]
     h2d = h2d_bytes / (h2d_ms * 1e-3) / 1e9 if h2d_ms > 0 else None
@@ -322,9 +346,24 @@ def main():
     value = r["tokens"] / elapsed
 
     variants = {}
-    if not args.no_variants:
-        other = "bf16" if args.h2d_format == "fp32" else "fp32"
-        v = timed_run(model, w, args, dev, other, args.resident_layers, args.d2h_engine, batch_seed=1)
+    v = None
+    other = "bf16" if args.h2d_format == "fp32" else "fp32"
+    # host bytes the second wrapper allocates: fp32 master, bf16 grad slot and two fp32 moments
+    # per parameter, plus the bf16 copy with bf16 H2D; the first run's masters stay alive
+    need = r["total_params"] * (4 + 2 + 8 + (2 if other == "bf16" else 0))
+    avail = host_mem_available()
+    if not args.no_variants and avail and need > 0.8 * avail:
+        log(f"[bench] variant h2d_{other} skipped: needs ~{need / 1e9:.0f} GB of host memory, "
+            f"{avail / 1e9:.0f} GB available")
+        variants[f"h2d_{other}"] = {"skipped": f"needs ~{need / 1e9:.0f} GB host memory, {avail / 1e9:.0f} GB available"}
+    elif not args.no_variants:
+        try:
+            v = timed_run(model, w, args, dev, other, args.resident_layers, args.d2h_engine, batch_seed=1)
+        except RuntimeError as e:  # e.g. the host cannot pin the bf16 copies
+            log(f"[bench] variant h2d_{other} failed: {e}")
+            v = None
+            variants[f"h2d_{other}"] = {"skipped": str(e)[:300]}
+    if not args.no_variants and v is not None:
         variants[f"h2d_{other}"] = {
             "value": v["tokens"] / v["elapsed"], "ms_per_step": v["elapsed"] / args.steps * 1e3,
             "h2d_format": other, "resident_layers": v["resident_layers"], "d2h_engine": args.d2h_engine,

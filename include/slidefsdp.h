@@ -182,9 +182,9 @@ int sf_dma_copy_d2h(const sf_seg* segs, int nsegs, uint64_t* signals,
                     int max_signals, int* nsignals);
 
 /* Block until every handle completed, then release them.  If start_ns and
- * end_ns are non-null and timing is enabled, *start_ns receives 0 and
- * *end_ns the time from the earliest start to the latest end of the copies
- * in ns (both 0 when timing is off). */
+ * end_ns are non-null and timing is enabled, they receive the earliest start
+ * and the latest end of the copies, in ns of the HSA system clock (both 0
+ * when timing is off). */
 int sf_dma_wait(const uint64_t* signals, int nsignals, uint64_t* start_ns,
                 uint64_t* end_ns);
 

@@ -129,11 +129,19 @@ def cpu() -> ctypes.CDLL:
 
 
 class NativeError(RuntimeError):
-    """A nonzero status from the C ABI."""
+    """A nonzero status from the C ABI (``status`` holds it)."""
+
+    def __init__(self, msg: str, status: int = 0):
+        super().__init__(msg)
+        self.status = status
+
+
+# hipErrorOutOfMemory, as the HIP entry points return it
+HIP_ERROR_OUT_OF_MEMORY = 2
 
 
 def check(status: int, what: str, lib: ctypes.CDLL | None = None) -> None:
     if status != 0:
         lib = lib or hip()
         msg = lib.sf_error_string(status).decode(errors="replace")
-        raise NativeError(f"{what} failed: {msg} (status {status})")
+        raise NativeError(f"{what} failed: {msg} (status {status})", status)

@@ -39,13 +39,13 @@ import queue
 import threading
 import time
 from collections import OrderedDict, deque
-from concurrent.futures import Future, ThreadPoolExecutor
+from concurrent.futures import Future
 from typing import Any, Callable, Dict, List, Optional, Tuple
 
 import torch
 import torch.nn as nn
 
-from . import kernels
+from . import _native, kernels
 from .optimizer import cpu_adam as _cpu_adam
 from .pinned import pinned_empty
 
@@ -290,7 +290,9 @@ class GradSlotsPerUnit:
     """
 
     def __init__(self, unit_sizes: Dict[int, int], dtype: torch.dtype = torch.bfloat16):
-        self.slots = {u: pinned_empty(max(1, n), dtype) for u, n in unit_sizes.items()}
+        self.slots = {}
+        for u, n in unit_sizes.items():
+            self.slots[u] = pinned_empty(max(1, n), dtype)
 
     def acquire(self, timeout: Optional[float] = None, unit: Optional[int] = None) -> int:
         if unit not in self.slots:
@@ -313,16 +315,23 @@ class PriorityUpdateExecutor:
     does not change any result.
 
     A task may carry a ``ready`` object with ``query()`` and ``synchronize()``
-    (a device event marking the end of its gradient copy).  Copies complete
-    in submission order (one copy stream), so when no queued task is ready
-    the worker waits for the oldest one, never for a later one.
+    (a device event marking the end of its input's production).  Inputs
+    complete in submission order (one stream or engine queue), so when no
+    queued task is ready the worker waits for the oldest one, never for a
+    later one.
+
+    ``gate`` (optional) is called by the worker before each pick, outside the
+    lock, and may block until a resource is free (a host gradient slot); its
+    result is passed to the picked task as its first argument.  The choice is
+    made once the resource is there, so it goes to the most urgent task.
     """
 
-    def __init__(self, name: str):
+    def __init__(self, name: str, gate: Optional[Callable[[], Any]] = None):
         self._tasks: list = []   # [priority, seq, future, fn, args, ready]
         self._cv = threading.Condition()
         self._seq = 0
         self._stop = False
+        self._gate = gate
         self._thread = threading.Thread(target=self._run, name=name, daemon=True)
         self._thread.start()
 
@@ -350,6 +359,19 @@ class PriorityUpdateExecutor:
                 self._cv.wait_for(lambda: self._tasks or self._stop)
                 if not self._tasks:
                     return
+            token, gate_error = None, None
+            if self._gate is not None:
+                try:
+                    token = self._gate()
+                except BaseException as e:  # e.g. no slot freed in time: fail the oldest task
+                    gate_error = e
+            with self._cv:
+                if gate_error is not None:
+                    task = min(self._tasks, key=lambda t: t[1])
+                    self._tasks.remove(task)
+                    if task[2].set_running_or_notify_cancel():
+                        task[2].set_exception(gate_error)
+                    continue
                 task, must_wait = self._pick()
                 if not must_wait:
                     self._tasks.remove(task)
@@ -362,6 +384,8 @@ class PriorityUpdateExecutor:
                     task, _ = self._pick()
                     self._tasks.remove(task)
             _, _, f, fn, args, _ = task
+            if self._gate is not None:
+                args = (token,) + tuple(args)
             if not f.set_running_or_notify_cancel():
                 continue
             try:
@@ -425,7 +449,9 @@ class StreamingRuntime:
         # One thread issues gradient offloads (it may wait for a free host
         # slot); one thread runs the host optimizer, as the reference's
         # update executor (slide_fsdp.py:163).
-        self.offload_executor = ThreadPoolExecutor(max_workers=1, thread_name_prefix="sf-offload")
+        # Gradient offloads: issued by one thread, the most urgent ready unit
+        # first (``init_grad_slots`` sets it up once the slots exist).
+        self.offload_executor: Optional[PriorityUpdateExecutor] = None
         self.update_executor = PriorityUpdateExecutor("sf-update")
         # Queue priority of a unit's update (lower runs first); the model sets
         # it to the unit's position in the next forward.
@@ -442,9 +468,33 @@ class StreamingRuntime:
         # pack and the update against the oracle.
         self.capture: Optional[dict] = None
 
-    def init_grad_slots(self, unit_sizes: Dict[int, int]) -> None:
+    def init_grad_slots(self, unit_sizes: Dict[int, int], fallback_depth: int = 3) -> None:
+        """One pinned slot per unit; if the host cannot pin that much (the
+        driver caps pinned memory well below the host's RAM on some
+        machines), a ring of ``fallback_depth`` slots of the largest unit.
+        Then the offload thread: with a ring it takes a free slot first and
+        then the most urgent unit whose gradients are complete (the others
+        wait in HBM); with per-unit slots it never waits for a slot."""
         if self.grad_ring is None:
+            self._alloc_grad_slots(unit_sizes, fallback_depth)
+        if self.offload_executor is None:
+            ring = self.grad_ring
+            gate = None if isinstance(ring, GradSlotsPerUnit) else (lambda: ring.acquire(timeout=self.wait_timeout))
+            self.offload_executor = PriorityUpdateExecutor("sf-offload", gate=gate)
+
+    def _alloc_grad_slots(self, unit_sizes: Dict[int, int], fallback_depth: int) -> None:
+        try:
             self.grad_ring = GradSlotsPerUnit(unit_sizes, self._dtype)
+            return
+        except _native.NativeError as e:
+            if e.status != _native.HIP_ERROR_OUT_OF_MEMORY:
+                raise
+        # Outside the handler: the traceback no longer holds the slots pinned
+        # so far, so they are released before the ring is pinned.
+        need = 2 * sum(unit_sizes.values())
+        print(f"SlideFSDP: {need / 1e9:.1f} GB of pinned gradient slots (one per unit) do not fit; "
+              f"using a ring of {fallback_depth} slots", flush=True)
+        self.grad_ring = GradStagingRing(fallback_depth, self.pool.max_param_size, self._dtype)
 
     def log(self, *event) -> None:
         if self.trace is not None:
@@ -456,7 +506,8 @@ class StreamingRuntime:
             self.timeline.append((time.perf_counter(), threading.current_thread().name, what, unit))
 
     def shutdown(self) -> None:
-        self.offload_executor.shutdown(wait=True)
+        if self.offload_executor is not None:
+            self.offload_executor.shutdown(wait=True)
         self.update_executor.shutdown(wait=True)
 
 
@@ -501,7 +552,14 @@ class LayerRuntimeState(nn.Module):
         # before their backward (the reference reloads every unit,
         # slide_fsdp.py:443-444).
         self.backward_reads_params = not isinstance(self.layer, nn.Embedding)
-        self._cpu_params_flat = pinned_empty(self.total_size, torch.float32)
+        # The fp32 master is the H2D source with fp32 H2D and must be pinned;
+        # with bf16 H2D only the host optimizer touches it, so it stays in
+        # pageable memory and the pinned budget (which the driver caps well
+        # below the host's RAM on some machines) goes to the bf16 copy.
+        if runtime.h2d_format == "bf16":
+            self._cpu_params_flat = torch.empty(self.total_size, dtype=torch.float32)
+        else:
+            self._cpu_params_flat = pinned_empty(self.total_size, torch.float32)
         self._param_maps: "OrderedDict[str, Tuple[int, torch.Size, int]]" = OrderedDict()
         self._param_views: "OrderedDict[str, torch.Tensor]" = OrderedDict()
         self._params: List[nn.Parameter] = []
@@ -509,7 +567,15 @@ class LayerRuntimeState(nn.Module):
         # bf16 H2D: a pinned bf16 copy of the master, rewritten by every update.
         self._cpu_params_bf16: Optional[torch.Tensor] = None
         if runtime.h2d_format == "bf16":
-            self._cpu_params_bf16 = pinned_empty(self.total_size, torch.bfloat16)
+            try:
+                self._cpu_params_bf16 = pinned_empty(self.total_size, torch.bfloat16)
+            except _native.NativeError as e:
+                if e.status != _native.HIP_ERROR_OUT_OF_MEMORY:
+                    raise
+                raise RuntimeError(
+                    "h2d_format='bf16' keeps a pinned bf16 copy of every master (2 bytes per parameter) "
+                    "and this host cannot pin that much"
+                ) from e
             self.refresh_host_copy()
         self._grad_params = [p for p in self._params if p.requires_grad]
         self._grads_seen = 0
@@ -689,8 +755,9 @@ class LayerRuntimeState(nn.Module):
         self.update_finished.clear()
         self.runtime.log("d2h", self.layer_idx)
         self.runtime.mark("post_backward", self.layer_idx)
-        self._d2h_future = self.runtime.offload_executor.submit(self._d2h_task, grads, missing, grad_ready,
-                                                                cast_fence)
+        rt = self.runtime
+        self._d2h_future = rt.offload_executor.submit(rt.update_priority(self.layer_idx), self._d2h_task,
+                                                      grads, missing, grad_ready, cast_fence, ready=grad_ready)
         self._grads_offloaded = True
         self._maybe_release_after_backward()
 
@@ -714,11 +781,17 @@ class LayerRuntimeState(nn.Module):
         self._current_gpu_cache = None
         self._release_unit(unit)
 
-    def _d2h_task(self, grads: List[Tuple[torch.Tensor, int]], missing: List[Tuple[int, int]],
-                  grad_ready: torch.cuda.Event, cast_fence: Optional[torch.cuda.Event] = None) -> None:
+    def _d2h_task(self, *args) -> None:
+        """Offload thread: copy this unit's gradients into a host slot, then
+        queue the update.  Called as ``(grads, missing, grad_ready, cast_fence)``
+        with per-unit slots, or with a ring slot taken by the thread first."""
         rt = self.runtime
+        if len(args) == 5:
+            slot, grads, missing, grad_ready, cast_fence = args
+        else:
+            grads, missing, grad_ready, cast_fence = args
+            slot = rt.grad_ring.acquire(timeout=rt.wait_timeout, unit=self.layer_idx)
         rt.mark("d2h_task", self.layer_idx)
-        slot = rt.grad_ring.acquire(timeout=rt.wait_timeout, unit=self.layer_idx)
         rt.mark("slot", self.layer_idx)
         try:
             host = rt.grad_ring.slots[slot]
@@ -799,7 +872,7 @@ class LayerRuntimeState(nn.Module):
                 rt.mark("dma_done", self.layer_idx)
                 del keep
                 if rt.d2h_timing is not None and t1 > t0:
-                    rt.d2h_timing.append(((t1 - t0) * 1e-6, nbytes))
+                    rt.d2h_timing.append(("interval_ns", t0, t1, nbytes))
             else:
                 d2h_done.synchronize()
             for off, size in missing:

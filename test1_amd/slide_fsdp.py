@@ -118,11 +118,12 @@ class SlideFSDP(nn.Module):
                          own; "kernel": by a capped-grid pack kernel writing
                          into host memory (slows the backward kernels beside
                          it); "copy": hipMemcpyAsync per parameter
-      h2d_format         "fp32" (default): the fp32 masters cross the host
-                         link and are cast to bf16 on the GPU; "bf16": the
-                         host optimizer keeps a bf16 copy of every master
-                         (written in its update pass) and that crosses the
-                         link, half the bytes.  Both stage the same bits.
+      h2d_format         "fp32" (default): the fp32 masters (pinned) cross the
+                         host link and are cast to bf16 on the GPU; "bf16":
+                         the host optimizer keeps a pinned bf16 copy of every
+                         master (written in its update pass) and that crosses
+                         the link, half the bytes, while the fp32 masters
+                         stay in pageable memory.  Both stage the same bits.
       resident_layers    decoder layers (the last ones, besides the last
                          decoder, which always stays) given a device buffer
                          of their own: loaded once per step in the forward
@@ -532,5 +533,6 @@ class SlideFSDP(nn.Module):
     def __del__(self):
         rt = getattr(self, "runtime", None)
         if rt is not None:
-            rt.offload_executor.shutdown(wait=False)
+            if rt.offload_executor is not None:
+                rt.offload_executor.shutdown(wait=False)
             rt.update_executor.shutdown(wait=False)

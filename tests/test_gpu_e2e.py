@@ -57,13 +57,15 @@ def test_schedule_matches_oracle(dev, resident):
     sf.close()
 
 
-# (parameter H2D format, resident decoder layers, gradient D2H engine)
-MODES = [("fp32", 0, "sdma"), ("bf16", 0, "sdma"), ("fp32", L - 1, "sdma"), ("bf16", L - 1, "sdma"),
-         ("fp32", 0, "kernel"), ("bf16", L - 1, "kernel")]
+# (parameter H2D format, resident decoder layers, gradient D2H engine, host gradient slots:
+#  None = one per unit, k = a ring of k)
+MODES = [("fp32", 0, "sdma", None), ("bf16", 0, "sdma", None), ("fp32", L - 1, "sdma", None),
+         ("bf16", L - 1, "sdma", None), ("fp32", 0, "kernel", None), ("bf16", L - 1, "kernel", None),
+         ("fp32", L - 1, "sdma", 2), ("bf16", 0, "kernel", 2)]
 
 
-@pytest.mark.parametrize("h2d_format,resident,d2h_engine", MODES)
-def test_updates_match_oracle_bit_exact(dev, h2d_format, resident, d2h_engine):
+@pytest.mark.parametrize("h2d_format,resident,d2h_engine,ring", MODES)
+def test_updates_match_oracle_bit_exact(dev, h2d_format, resident, d2h_engine, ring):
     """Every unit's host update equals the oracle AdamW applied to the same
     (captured) bf16 grads and fp32 master, for 3 steps.  With bf16 H2D the
     host bf16 copy of every unit is the oracle cast of its master after each
@@ -73,7 +75,8 @@ def test_updates_match_oracle_bit_exact(dev, h2d_format, resident, d2h_engine):
 
     model = make_model()
     sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS),
-                   wait_timeout=120, h2d_format=h2d_format, resident_layers=resident, d2h_engine=d2h_engine)
+                   wait_timeout=120, h2d_format=h2d_format, resident_layers=resident, d2h_engine=d2h_engine,
+                   grad_ring_depth=ring)
     orc = oracle.LayerAdamOracle(lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
     ref_units = []
     for ps in units_of(model):
@@ -142,15 +145,16 @@ def reference_losses(model, steps_ids, dev):
     return losses, first_grads
 
 
-@pytest.mark.parametrize("h2d_format,resident,d2h_engine", MODES)
-def test_loss_parity_with_non_offloaded_run(dev, h2d_format, resident, d2h_engine):
+@pytest.mark.parametrize("h2d_format,resident,d2h_engine,ring", MODES)
+def test_loss_parity_with_non_offloaded_run(dev, h2d_format, resident, d2h_engine, ring):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model()
     steps = batches(10)
     ref_losses, ref_grads = reference_losses(model, steps, dev)
     sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS),
-                   wait_timeout=120, h2d_format=h2d_format, resident_layers=resident, d2h_engine=d2h_engine)
+                   wait_timeout=120, h2d_format=h2d_format, resident_layers=resident, d2h_engine=d2h_engine,
+                   grad_ring_depth=ring)
     losses = []
     for k, ids in enumerate(steps):
         if k == 0:

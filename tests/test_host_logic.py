@@ -119,3 +119,60 @@ def test_grad_slots_per_unit_are_sized_and_never_block(monkeypatch):
     slots.release(2)
     with pytest.raises(KeyError):
         slots.acquire(unit=5)
+
+
+def test_grad_slots_fall_back_to_a_ring_when_pinning_fails(monkeypatch):
+    from test1_amd import _native, layer_state
+
+    calls = []
+
+    def fake_pinned(n, dt):
+        calls.append(n)
+        if len(calls) > 2:  # the host refuses to pin more after two slots
+            raise _native.NativeError("sf_host_alloc failed: out of memory", _native.HIP_ERROR_OUT_OF_MEMORY)
+        return torch.empty(n, dtype=dt)
+
+    monkeypatch.setattr(layer_state, "pinned_empty", fake_pinned)
+    rt = object.__new__(layer_state.StreamingRuntime)
+    rt.grad_ring, rt._dtype, rt.offload_executor, rt.wait_timeout = None, torch.bfloat16, None, None
+    rt.pool = type("P", (), {"max_param_size": 9})()
+    ring_slots = []
+    monkeypatch.setattr(layer_state, "GradStagingRing",
+                        lambda depth, n, dt: ring_slots.append((depth, n)) or "ring")
+    rt.init_grad_slots({0: 5, 1: 9, 2: 7, 3: 3})
+    assert rt.grad_ring == "ring" and ring_slots == [(3, 9)]
+    rt.offload_executor.shutdown(wait=True)
+
+    # any other failure is not swallowed
+    def broken(n, dt):
+        raise _native.NativeError("sf_host_alloc failed: invalid argument", 9001)
+
+    monkeypatch.setattr(layer_state, "pinned_empty", broken)
+    rt.grad_ring = None
+    with pytest.raises(_native.NativeError):
+        rt.init_grad_slots({0: 5})
+
+
+def test_gated_executor_gives_the_slot_to_the_most_urgent_ready_task():
+    from test1_amd.layer_state import PriorityUpdateExecutor
+    import queue as _q
+
+    slots = _q.Queue()
+    got = []
+    ex = PriorityUpdateExecutor("test-gate", gate=lambda: slots.get(timeout=10))
+    # three offloads queue up while no slot is free
+    futs = [ex.submit(p, lambda slot, p=p: got.append((p, slot)), ready=None) for p in (30, 10, 20)]
+    time.sleep(0.1)
+    assert got == []
+    for s in ("a", "b", "c"):
+        slots.put(s)
+    for f in futs:
+        f.result(timeout=10)
+    assert got == [(10, "a"), (20, "b"), (30, "c")]
+    # a gate that fails fails the oldest task, and the worker keeps going
+    ex2 = PriorityUpdateExecutor("test-gate2", gate=lambda: (_ for _ in ()).throw(TimeoutError("no slot")))
+    f = ex2.submit(1, got.append, 0)
+    with pytest.raises(TimeoutError):
+        f.result(timeout=10)
+    ex2.shutdown(wait=True)
+    ex.shutdown(wait=True)

@@ -53,6 +53,11 @@ from .pinned import pinned_empty
 from .sliding_checkpoint import ActivationRing, SlidingCheckpoint
 
 
+try:  # transformers >= 5: masks are built by a module-level function
+    from transformers.masking_utils import create_causal_mask as _hf_create_causal_mask
+except ImportError:  # older versions keep the decoder's _update_causal_mask
+    _hf_create_causal_mask = None
+
 class OutputLayer(nn.Module):
     """Final norm + lm_head + shifted cross-entropy as one unit (reference
     slide_fsdp.py:45-113, the branch without the optional fused kernel:
@@ -407,6 +412,13 @@ class SlideFSDP(nn.Module):
         causal_mask = None
         if self._update_causal_mask is not None:
             causal_mask = self._update_causal_mask(attention_mask, hidden_states, cache_position, None, None)
+        elif attention_mask is not None and _hf_create_causal_mask is not None:
+            # transformers >= 5 builds the mask with a module-level function;
+            # the reference only looks for the decoder method (slide_fsdp.py:234,
+            # 557-561) and so drops padding masks with these versions.
+            causal_mask = _hf_create_causal_mask(config=self.model_config, inputs_embeds=hidden_states,
+                                                 attention_mask=attention_mask, past_key_values=None,
+                                                 position_ids=cache_position.unsqueeze(0))
         if self.position_embeddings is None and self.rotary_emb is not None:
             self.position_embeddings = self.rotary_emb(hidden_states, cache_position.unsqueeze(0))
 

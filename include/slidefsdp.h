@@ -123,6 +123,25 @@ int sf_copy_segs_b16(const sf_seg* segs, int nsegs, int max_workgroups,
 int sf_fill_b16(uint16_t* dst, size_t n, uint16_t value,
                 sf_stream_t stream);
 
+/* Row gather for a row-sparse embedding unit.  For t < ntok,
+ * dst[t*row_len .. +row_len) = src row ids[t] of a [nrows, row_len] table,
+ * rounded fp32 -> bf16 (RNE, NaN -> 0xFFFF) by the f32 variant, copied by the
+ * b16 one.  src and dst may be device addresses of pinned host memory (the
+ * forward reads only the batch's rows of the host master; the backward
+ * writes only the batch's gradient rows to host).  An id outside
+ * [0, nrows) gives a row of 0xFFFF and sets *bad = 1 (bad may be NULL).
+ * max_workgroups > 0 caps the grid (host destinations).  Replaces the full
+ * staging of the embedding unit (layer_state.py:296-314) for its forward
+ * lookup (slide_fsdp.py:543-545, nn.Embedding) and the full gradient D2H
+ * of that unit (layer_state.py:367-393). */
+int sf_gather_rows_f32_bf16(const float* src, const int64_t* ids, size_t ntok,
+                            size_t row_len, size_t nrows, uint16_t* dst,
+                            uint32_t* bad, int max_workgroups,
+                            sf_stream_t stream);
+int sf_gather_rows_b16(const uint16_t* src, const int64_t* ids, size_t ntok,
+                       size_t row_len, size_t nrows, uint16_t* dst,
+                       uint32_t* bad, int max_workgroups, sf_stream_t stream);
+
 /* ---------------------------------------------------------------------
  * Copies and pinned host memory (libsf_hip.so)
  * ------------------------------------------------------------------- */
@@ -264,6 +283,20 @@ int sf_adam_update_cast(int optimizer_id, size_t step, float lr, float beta1,
                         int bias_correction, float* params, const void* grads,
                         int g_dtype, float* exp_avg, float* exp_avg_sq,
                         uint16_t* params_bf16, size_t n);
+
+/* sf_adam_update_cast over a [n_rows, row_len] tensor whose gradient is
+ * zero except in some rows: row r takes its gradient from row row_slot[r]
+ * of grads ([n_grad_rows, row_len], g_dtype), or zeros when row_slot[r] < 0.
+ * Every element gets exactly the dense update (row_len must be a multiple
+ * of 16, so no element falls in the scalar tail).  Replaces adam_update on
+ * the embedding unit's dense `grad.float()` (layer_adam.py:404) when only
+ * the batch's rows were offloaded. */
+int sf_adam_update_rows(int optimizer_id, size_t step, float lr, float beta1,
+                        float beta2, float eps, float weight_decay,
+                        int bias_correction, float* params, float* exp_avg,
+                        float* exp_avg_sq, uint16_t* params_bf16,
+                        size_t n_rows, size_t row_len, const int64_t* row_slot,
+                        const void* grads, size_t n_grad_rows, int g_dtype);
 
 /* OpenMP team size used by the host AdamW (<= 0: library default). */
 int sf_cpu_set_threads(int nthreads);

@@ -63,6 +63,8 @@ HIP_SIGNATURES = {
     "sf_unpack_b16": [_vp, ctypes.POINTER(SfSeg), _i, _i, _vp],
     "sf_copy_segs_b16": [ctypes.POINTER(SfSeg), _i, _i, _vp],
     "sf_fill_b16": [_vp, _sz, ctypes.c_uint16, _vp],
+    "sf_gather_rows_f32_bf16": [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _i, _vp],
+    "sf_gather_rows_b16": [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _i, _vp],
     "sf_memcpy_async": [_vp, _vp, _sz, _i, _vp],
     "sf_host_alloc": [ctypes.POINTER(_vp), _sz],
     "sf_host_free": [_vp],
@@ -87,6 +89,7 @@ CPU_SIGNATURES = {
     "sf_adam_update_cast": [_i, _sz, _f, _f, _f, _f, _f, _i, _vp, _vp, _i, _vp, _vp, _vp, _sz],
     "sf_cpu_adam_step_cast": [_vp, _vp, _i, _vp, _vp, _vp, _sz, ctypes.POINTER(SfAdamHparams)],
     "sf_cpu_cast_f32_bf16": [_vp, _vp, _sz],
+    "sf_adam_update_rows": [_i, _sz, _f, _f, _f, _f, _f, _i, _vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _sz, _i],
     "sf_cpu_set_threads": [_i],
     "sf_cpu_has_avx512": [],
 }

@@ -33,7 +33,9 @@
 #include <cstring>
 #include <memory>
 #include <mutex>
+#include <type_traits>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/slidefsdp.h"
 
@@ -362,14 +364,15 @@ int sf_adam_update(int optimizer_id, size_t step, float lr, float beta1, float b
                                params, grads, g_dtype, exp_avg, exp_avg_sq, nullptr, n);
 }
 
-int sf_adam_update_cast(int optimizer_id, size_t step, float lr, float beta1, float beta2, float eps,
-                        float weight_decay, int bias_correction, float* params, const void* grads,
-                        int g_dtype, float* exp_avg, float* exp_avg_sq, uint16_t* params_bf16, size_t n) {
-    std::shared_ptr<AdamState> st = find_state(optimizer_id);
-    if (!st) return SF_ENOOPT;
-    if (g_dtype != SF_DTYPE_F32 && g_dtype != SF_DTYPE_BF16) return SF_EDTYPE;
-    if (n > 0 && (!params || !grads || !exp_avg || !exp_avg_sq)) return SF_EINVAL;
-    sf_adam_hparams hp;
+}  // extern "C"
+
+namespace {
+
+// The scalars of one stateful update (cpu_adam.h:57-89, 108-141): advance the
+// optimizer's beta powers for ``step`` and derive the bias corrections.
+void stateful_hparams(AdamState& stt, size_t step, float lr, float beta1, float beta2, float eps,
+                      float weight_decay, int bias_correction, sf_adam_hparams& hp) {
+    AdamState* st = &stt;
     {
         std::lock_guard<std::mutex> lk(st->mu);
         st->increment_step(step, beta1, beta2);
@@ -393,7 +396,70 @@ int sf_adam_update_cast(int optimizer_id, size_t step, float lr, float beta1, fl
         hp.bias_correction2 = bc2;
         hp.adamw_mode = st->adamw ? 1 : 0;
     }
+}
+
+// Rows of a [n_rows, row_len] tensor; row r takes its gradient from
+// grads[row_slot[r]] or, for row_slot[r] < 0, zeros.  row_len is a multiple
+// of 16, so every row starts a 16-element group and no element falls in the
+// reference's scalar tail: each element gets exactly the dense update.
+template <int GDT>
+void adam_rows(float* p, float* m, float* v, uint16_t* pb, size_t n_rows, size_t row_len,
+               const int64_t* row_slot, const void* grads, const Scalars& c) {
+    using G = typename std::conditional<GDT == SF_DTYPE_BF16, uint16_t, float>::type;
+    const G* g = static_cast<const G*>(grads);
+    std::vector<G> zeros(row_len, G(0));
+    const bool avx = host_has_avx512();
+    int nt = g_threads > 0 ? g_threads : omp_get_max_threads();
+    const long rows_per_chunk = long(std::max<size_t>(1, (size_t(1) << 15) / row_len));
+    const long nchunks = long((n_rows + rows_per_chunk - 1) / rows_per_chunk);
+#pragma omp parallel for num_threads(nt) schedule(dynamic, 1)
+    for (long k = 0; k < nchunks; ++k) {
+        const size_t r0 = size_t(k) * rows_per_chunk, r1 = std::min(n_rows, r0 + size_t(rows_per_chunk));
+        for (size_t r = r0; r < r1; ++r) {
+            const size_t o = r * row_len;
+            const G* gr = row_slot[r] >= 0 ? g + size_t(row_slot[r]) * row_len : zeros.data();
+            uint16_t* pbr = pb ? pb + o : nullptr;
+            if (avx) adam_range_avx512<GDT>(p + o, gr, m + o, v + o, 0, row_len, c, pbr);
+            else adam_range_scalar<GDT>(p + o, gr, m + o, v + o, 0, row_len, c, pbr);
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int sf_adam_update_cast(int optimizer_id, size_t step, float lr, float beta1, float beta2, float eps,
+                        float weight_decay, int bias_correction, float* params, const void* grads,
+                        int g_dtype, float* exp_avg, float* exp_avg_sq, uint16_t* params_bf16, size_t n) {
+    std::shared_ptr<AdamState> st = find_state(optimizer_id);
+    if (!st) return SF_ENOOPT;
+    if (g_dtype != SF_DTYPE_F32 && g_dtype != SF_DTYPE_BF16) return SF_EDTYPE;
+    if (n > 0 && (!params || !grads || !exp_avg || !exp_avg_sq)) return SF_EINVAL;
+    sf_adam_hparams hp;
+    stateful_hparams(*st, step, lr, beta1, beta2, eps, weight_decay, bias_correction, hp);
     return sf_cpu_adam_step_cast(params, grads, g_dtype, exp_avg, exp_avg_sq, params_bf16, n, &hp);
+}
+
+int sf_adam_update_rows(int optimizer_id, size_t step, float lr, float beta1, float beta2, float eps,
+                        float weight_decay, int bias_correction, float* params, float* exp_avg,
+                        float* exp_avg_sq, uint16_t* params_bf16, size_t n_rows, size_t row_len,
+                        const int64_t* row_slot, const void* grads, size_t n_grad_rows, int g_dtype) {
+    std::shared_ptr<AdamState> st = find_state(optimizer_id);
+    if (!st) return SF_ENOOPT;
+    if (g_dtype != SF_DTYPE_F32 && g_dtype != SF_DTYPE_BF16) return SF_EDTYPE;
+    if (n_rows == 0 || row_len == 0) return SF_OK;
+    if (row_len % 16 != 0) return SF_EINVAL;
+    if (!params || !exp_avg || !exp_avg_sq || !row_slot || (n_grad_rows > 0 && !grads)) return SF_EINVAL;
+    for (size_t r = 0; r < n_rows; ++r) {
+        if (row_slot[r] >= 0 && size_t(row_slot[r]) >= n_grad_rows) return SF_EINVAL;
+    }
+    sf_adam_hparams hp;
+    stateful_hparams(*st, step, lr, beta1, beta2, eps, weight_decay, bias_correction, hp);
+    const Scalars c = make_scalars(hp);
+    if (g_dtype == SF_DTYPE_BF16) adam_rows<SF_DTYPE_BF16>(params, exp_avg, exp_avg_sq, params_bf16, n_rows, row_len, row_slot, grads, c);
+    else adam_rows<SF_DTYPE_F32>(params, exp_avg, exp_avg_sq, params_bf16, n_rows, row_len, row_slot, grads, c);
+    return SF_OK;
 }
 
 int sf_adam_destroy(int optimizer_id) {

@@ -101,6 +101,48 @@ __global__ __launch_bounds__(kThreads) void cast_flat_kernel(
     }
 }
 
+// ---------------------------------------------------------------------
+// Row gather: dst row t = src row ids[t] (rows of row_len elements), cast
+// fp32 -> bf16 (kCast) or copied as 16-bit values.  One workgroup per row
+// per iteration, grid-stride over the rows; src may be pinned host memory
+// (the row-sparse embedding load) and dst may be pinned host memory (the
+// row-sparse gradient offload, then with a capped grid).  An id outside
+// [0, nrows) yields a row of 0xFFFF (a NaN in bf16) and sets *bad.
+// ---------------------------------------------------------------------
+template <bool kCast>
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(
+    const void* __restrict__ src, const int64_t* __restrict__ ids, uint64_t ntok, uint64_t row_len,
+    uint64_t nrows, uint16_t* __restrict__ dst, uint32_t* __restrict__ bad, int vec) {
+    for (uint64_t t = blockIdx.x; t < ntok; t += gridDim.x) {
+        const int64_t r = ids[t];
+        uint16_t* out = dst + t * row_len;
+        if (r < 0 || uint64_t(r) >= nrows) {
+            for (uint64_t j = threadIdx.x; j < row_len; j += kThreads) out[j] = 0xFFFFu;
+            if (bad != nullptr && threadIdx.x == 0) bad[0] = 1u;
+            continue;
+        }
+        const uint64_t base = uint64_t(r) * row_len;
+        if (vec) {
+            const uint64_t g8 = row_len / kGroup;
+            for (uint64_t g = threadIdx.x; g < g8; g += kThreads) {
+                u32x4 v;
+                if (kCast) {
+                    const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(src) + base + g * kGroup);
+                    v = cast8(p[0], p[1]);
+                } else {
+                    v = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + base)[g];
+                }
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(out) + g);
+            }
+        } else {
+            for (uint64_t j = threadIdx.x; j < row_len; j += kThreads) {
+                out[j] = kCast ? uint16_t(rne_bf16(__float_as_uint(static_cast<const float*>(src)[base + j])))
+                               : static_cast<const uint16_t*>(src)[base + j];
+            }
+        }
+    }
+}
+
 // Scalar cast for tails and for pointers that are not 16-byte aligned.
 __global__ __launch_bounds__(kThreads) void cast_scalar_kernel(
     const float* __restrict__ src, uint16_t* __restrict__ dst, uint64_t n) {
@@ -263,6 +305,26 @@ inline int hip_status(hipError_t e) {
 }
 }  // namespace
 
+namespace {
+template <bool kCast>
+int launch_gather_rows(const void* src, const int64_t* ids, size_t ntok, size_t row_len, size_t nrows,
+                       uint16_t* dst, uint32_t* bad, int max_workgroups, hipStream_t st, size_t src_elem) {
+    if (ntok == 0 || row_len == 0) return SF_OK;
+    if (src == nullptr || ids == nullptr || dst == nullptr) return SF_EINVAL;
+    if ((reinterpret_cast<uintptr_t>(dst) & 1) != 0) return SF_EINVAL;
+    // the destination rows must not overlap the source table
+    const uintptr_t s0 = reinterpret_cast<uintptr_t>(src), d0 = reinterpret_cast<uintptr_t>(dst);
+    if (s0 < d0 + 2 * ntok * row_len && d0 < s0 + src_elem * nrows * row_len) return SF_EOVERLAP;
+    const int vec = (row_len % kGroup == 0) && ((s0 | d0) & 15) == 0;
+    uint64_t grid = ntok;
+    if (max_workgroups > 0 && grid > uint64_t(max_workgroups)) grid = uint64_t(max_workgroups);
+    if (grid > kMaxBlocks) grid = kMaxBlocks;
+    hipLaunchKernelGGL(gather_rows_kernel<kCast>, dim3(uint32_t(grid)), dim3(kThreads), 0, st, src, ids,
+                       uint64_t(ntok), uint64_t(row_len), uint64_t(nrows), dst, bad, vec);
+    return hip_status(hipGetLastError());
+}
+}  // namespace
+
 extern "C" {
 
 const char* sf_error_string(int status) {
@@ -353,6 +415,18 @@ int sf_unpack_b16(const uint16_t* src, const sf_seg* segs, int nsegs, int max_wo
         if (rc != SF_OK) return rc;
     }
     return SF_OK;
+}
+
+int sf_gather_rows_f32_bf16(const float* src, const int64_t* ids, size_t ntok, size_t row_len, size_t nrows,
+                            uint16_t* dst, uint32_t* bad, int max_workgroups, sf_stream_t stream) {
+    return launch_gather_rows<true>(src, ids, ntok, row_len, nrows, dst, bad, max_workgroups,
+                                    reinterpret_cast<hipStream_t>(stream), 4);
+}
+
+int sf_gather_rows_b16(const uint16_t* src, const int64_t* ids, size_t ntok, size_t row_len, size_t nrows,
+                       uint16_t* dst, uint32_t* bad, int max_workgroups, sf_stream_t stream) {
+    return launch_gather_rows<false>(src, ids, ntok, row_len, nrows, dst, bad, max_workgroups,
+                                     reinterpret_cast<hipStream_t>(stream), 2);
 }
 
 int sf_fill_b16(uint16_t* dst, size_t n, uint16_t value, sf_stream_t stream) {

@@ -166,6 +166,47 @@ def fill_b16_(dst: torch.Tensor, value: int = 0, stream: Optional[torch.cuda.Str
     return dst
 
 
+def gather_rows(table: torch.Tensor, ids: torch.Tensor, dst: torch.Tensor, bad: Optional[torch.Tensor] = None,
+                stream: Optional[torch.cuda.Stream] = None, max_workgroups: int = 0) -> torch.Tensor:
+    """``dst[t] = table[ids[t]]`` for a 2-D ``table`` (fp32: rounded to bf16;
+    16-bit: copied) into a 16-bit ``dst`` of shape [len(ids), row_len].
+
+    ``table`` and ``dst`` may be pinned host tensors (read or written over the
+    host link by the kernel); ``ids`` is an int64 GPU tensor.  An id out of
+    range yields a row of 0xFFFF and sets ``bad[0] = 1`` (``bad``: a uint32/
+    int32 tensor of one element, GPU or pinned host)."""
+    if table.dim() != 2:
+        raise ValueError("gather_rows: table must be 2-D")
+    nrows, row_len = table.shape
+    _require_contig(table, "table")
+    _require_contig(dst, "dst")
+    _require_cuda(ids, "ids")
+    _require_contig(ids, "ids")
+    if ids.dtype != torch.int64:
+        raise TypeError("gather_rows: ids must be int64")
+    if dst.element_size() != 2 or dst.numel() < ids.numel() * row_len:
+        raise ValueError("gather_rows: dst must be 16-bit with room for len(ids) rows")
+    for t, what in ((table, "table"), (dst, "dst")):
+        if t.device.type == "cpu" and not t.is_pinned():
+            raise ValueError(f"gather_rows: a host {what} must be pinned")
+    bad_ptr = None
+    if bad is not None:
+        if bad.element_size() != 4 or bad.numel() < 1:
+            raise ValueError("gather_rows: bad must hold one 32-bit word")
+        if bad.device.type == "cpu" and not bad.is_pinned():
+            raise ValueError("gather_rows: a host bad flag must be pinned")
+        bad_ptr = device_address(bad)
+    if table.dtype == torch.float32:
+        fn = _native.hip().sf_gather_rows_f32_bf16
+    elif table.element_size() == 2:
+        fn = _native.hip().sf_gather_rows_b16
+    else:
+        raise TypeError(f"gather_rows: unsupported table dtype {table.dtype}")
+    _native.check(fn(device_address(table), ids.data_ptr(), ids.numel(), row_len, nrows, device_address(dst),
+                     bad_ptr, int(max_workgroups), _stream_ptr(stream)), "sf_gather_rows")
+    return dst
+
+
 def memcpy_async(dst: torch.Tensor, src: torch.Tensor, stream: Optional[torch.cuda.Stream] = None,
                  nbytes: Optional[int] = None) -> None:
     """Asynchronous byte copy between contiguous tensors on ``stream``.

@@ -541,6 +541,9 @@ class LayerRuntimeState(nn.Module):
         # A unit of its own (``make_resident``): loaded in the forward and
         # kept on the device through the backward, never taken from the pool.
         self._own_unit: Optional[Dict[str, Any]] = None
+        # Row-sparse embedding (``enable_row_sparse``): only the batch's rows
+        # cross the host link, in both directions.
+        self.row_sparse = False
         self._post_called = False
         self._bwd_armed = False
         self._bwd_compute_done = False
@@ -629,6 +632,11 @@ class LayerRuntimeState(nn.Module):
         staging ring are issued before the pool wait, so the host link keeps
         streaming while an earlier unit is still busy.
         """
+        if self.row_sparse:
+            # rows are gathered by the lookup itself (gather_rows); the
+            # backward of a lookup reads no weights
+            self.runtime.log("h2d", self.layer_idx, is_backward)
+            return
         if self._current_gpu_cache is not None:
             return  # already resident (last decoder / output / own unit)
         self.wait_for_update()
@@ -861,6 +869,122 @@ class LayerRuntimeState(nn.Module):
         for (name, (off, shape, size)), p in self._named():
             views[p] = host[off:off + size].view(shape)
         return views
+
+    # ------------------------------------------------------------------
+    # Row-sparse embedding unit
+    def enable_row_sparse(self) -> None:
+        """Move only the rows a batch uses, for an ``nn.Embedding`` unit.
+
+        Forward: ``gather_rows`` reads the batch's rows straight from the
+        pinned host table (fp32 master, or its bf16 copy) with one kernel and
+        rounds them to bf16: the lookup's output, bit for bit, without staging
+        the table (reference layer_state.py:296-314 stages all of it, 2 or 4
+        bytes per parameter).  Backward: ``offload_rows`` computes the dense
+        table gradient on the device as the lookup's own backward does and
+        sends only the batch's rows to host; the host AdamW then updates the
+        whole table with zero gradient elsewhere (``sf_adam_update_rows``),
+        which is the dense update's result."""
+        emb = self.layer
+        if not isinstance(emb, nn.Embedding) or emb.max_norm is not None or emb.scale_grad_by_freq or emb.sparse:
+            raise ValueError("enable_row_sparse: a plain nn.Embedding unit is required")
+        V, H = emb.weight.shape
+        if H % 16 != 0 or len(self._params) != 1:
+            raise ValueError("enable_row_sparse: the row length must be a multiple of 16")
+        self.row_sparse = True
+        self._rows_shape = (V, H)
+        self._bad_ids = pinned_empty(1, torch.int32)
+        self._bad_ids.zero_()
+        self._rows_host: Optional[torch.Tensor] = None
+        self._ids_host: Optional[torch.Tensor] = None
+
+    def _host_table(self) -> torch.Tensor:
+        V, H = self._rows_shape
+        src = self._cpu_params_bf16 if self._cpu_params_bf16 is not None else self._cpu_params_flat
+        return src.view(V, H)
+
+    def gather_rows(self, ids: torch.Tensor) -> torch.Tensor:
+        """Forward lookup: [*ids.shape, H] bf16 rows of the current master."""
+        self.wait_for_update()
+        V, H = self._rows_shape
+        flat = ids.reshape(-1)
+        if flat.dtype != torch.int64:
+            flat = flat.long()
+        if not flat.is_contiguous():
+            flat = flat.contiguous()
+        out = torch.empty(tuple(ids.shape) + (H,), dtype=torch.bfloat16, device=self.runtime.device)
+        # The flag's previous writer (last step's lookup) finished before that
+        # step's update, which wait_for_update has just waited for.
+        self._bad_ids.zero_()
+        kernels.gather_rows(self._host_table(), flat, out.view(-1, H), bad=self._bad_ids,
+                            stream=torch.cuda.current_stream())
+        self._bwd_compute_done = False
+        self._grads_offloaded = False
+        self.runtime.log("h2d", self.layer_idx, False)
+        self.runtime.mark("h2d_issued", self.layer_idx)
+        return out
+
+    def offload_rows(self, grad_out: torch.Tensor, ids: torch.Tensor) -> None:
+        """Backward of the lookup: dense table gradient on the device (as the
+        lookup's backward computes it), its batch rows to pinned host slots,
+        then the update is queued."""
+        rt = self.runtime
+        V, H = self._rows_shape
+        flat = ids.reshape(-1)
+        ntok = flat.numel()
+        pad = self.layer.padding_idx if self.layer.padding_idx is not None else -1
+        dense = torch.ops.aten.embedding_dense_backward(grad_out.reshape(ntok, H), flat, V, pad, False)
+        if rt.capture is not None:
+            rt.capture[("device_grads", self.layer_idx)] = [dense.detach().clone().view(V, H)]
+        if self._rows_host is None or self._rows_host.shape[0] < ntok:
+            self._rows_host = pinned_empty((ntok, H), torch.bfloat16)
+            self._ids_host = pinned_empty(ntok, torch.int64)
+        grad_ready = _new_event()
+        grad_ready.record(torch.cuda.current_stream())
+        with self._grad_lock:
+            self._post_called = True
+            self._bwd_armed = False
+        self.update_finished.clear()
+        rt.log("d2h", self.layer_idx)
+        rt.mark("post_backward", self.layer_idx)
+        rt.d2h_stream.wait_event(grad_ready)
+        kernels.gather_rows(dense, flat, self._rows_host[:ntok], stream=rt.d2h_stream,
+                            max_workgroups=rt.d2h_workgroups)
+        kernels.memcpy_async(self._ids_host[:ntok], flat, rt.d2h_stream)
+        dense.record_stream(rt.d2h_stream)
+        flat.record_stream(rt.d2h_stream)
+        done = _new_event()
+        done.record(rt.d2h_stream)
+        self._grads_offloaded = True
+        self._bwd_compute_done = True
+        self._update_future = rt.update_executor.submit(rt.update_priority(self.layer_idx), self._do_update_rows,
+                                                        done, ntok, ready=done)
+
+    def _do_update_rows(self, d2h_done: torch.cuda.Event, ntok: int) -> bool:
+        rt = self.runtime
+        V, H = self._rows_shape
+        try:
+            rt.mark("update_start", self.layer_idx)
+            d2h_done.synchronize()
+            if int(self._bad_ids[0]) != 0:
+                raise ValueError(f"embedding unit {self.layer_idx}: input ids outside [0, {V})")
+            ids = self._ids_host[:ntok]
+            rows = self._rows_host[:ntok]
+            row_slot = torch.full((V,), -1, dtype=torch.int64)
+            row_slot[ids] = torch.arange(ntok, dtype=torch.int64)
+            if rt.capture is not None:
+                dense = torch.zeros(V, H, dtype=rows.dtype)
+                dense[ids] = rows
+                rt.capture[self.layer_idx] = (dense.view(-1), self._cpu_params_flat.clone())
+            with self.update_lock:
+                if self.layer_optimizer is not None:
+                    self.layer_optimizer.step_rows(self.layer_idx, row_slot, rows,
+                                                   param_view=self._cpu_params_flat.view(V, H),
+                                                   bf16_view=None if self._cpu_params_bf16 is None
+                                                   else self._cpu_params_bf16.view(V, H))
+            rt.mark("adam_done", self.layer_idx)
+        finally:
+            self.update_finished.set()
+        return True
 
     def _do_update(self, slot: int, d2h_done: Optional[torch.cuda.Event], missing: List[Tuple[int, int]],
                    dma_handle=None, keep=None, nbytes: int = 0) -> bool:

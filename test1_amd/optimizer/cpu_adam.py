@@ -96,6 +96,41 @@ def adam_update(optimizer_id: int, step: int, lr: float, beta1: float, beta2: fl
     return 0
 
 
+def adam_update_rows(optimizer_id: int, step: int, lr: float, beta1: float, beta2: float, eps: float,
+                     weight_decay: float, bias_correction: bool, params: torch.Tensor, exp_avg: torch.Tensor,
+                     exp_avg_sq: torch.Tensor, row_slot: torch.Tensor, grads: torch.Tensor,
+                     params_bf16: Optional[torch.Tensor] = None) -> int:
+    """``adam_update`` of a 2-D ``params`` [n_rows, row_len] whose gradient is
+    zero except in the rows named by ``row_slot`` (int64 [n_rows]: the row of
+    ``grads`` [k, row_len] holding row r's gradient, or -1).  Gives the bits
+    of the dense update with the scattered gradient."""
+    if params.dim() != 2:
+        raise ValueError("adam_update_rows: params must be 2-D")
+    n_rows, row_len = params.shape
+    for t, name in ((params, "params"), (exp_avg, "exp_avg"), (exp_avg_sq, "exp_avg_sq")):
+        if t.dtype != torch.float32 or t.device.type != "cpu" or not t.is_contiguous() or t.numel() != params.numel():
+            raise ValueError(f"adam_update_rows: {name} must be a contiguous fp32 CPU tensor of params' size")
+    if row_slot.dtype != torch.int64 or row_slot.numel() != n_rows or not row_slot.is_contiguous():
+        raise ValueError("adam_update_rows: row_slot must be a contiguous int64 tensor of n_rows")
+    gcode = _grad_dtype_code(grads)
+    if gcode < 0:
+        raise RuntimeError(f"Adam optimizer with grad type {grads.dtype} is not supported on current hardware")
+    if grads.device.type != "cpu" or not grads.is_contiguous() or grads.numel() % max(1, row_len):
+        raise ValueError("adam_update_rows: grads must be a contiguous CPU tensor of whole rows")
+    pb = None
+    if params_bf16 is not None:
+        if (params_bf16.dtype != torch.bfloat16 or params_bf16.device.type != "cpu"
+                or not params_bf16.is_contiguous() or params_bf16.numel() != params.numel()):
+            raise ValueError("adam_update_rows: params_bf16 must be a contiguous bf16 CPU tensor of the params' size")
+        pb = params_bf16.data_ptr()
+    _check(_lib().sf_adam_update_rows(int(optimizer_id), int(step), lr, beta1, beta2, eps, weight_decay,
+                                      1 if bias_correction else 0, params.data_ptr(), exp_avg.data_ptr(),
+                                      exp_avg_sq.data_ptr(), pb, n_rows, row_len, row_slot.data_ptr(),
+                                      grads.data_ptr(), grads.numel() // max(1, row_len), gcode),
+           "adam_update_rows")
+    return 0
+
+
 def cast_f32_bf16(src: torch.Tensor, dst: torch.Tensor) -> torch.Tensor:
     """``dst`` = round-to-nearest-even bf16 of ``src`` (NaN -> 0xFFFF), on the
     host AdamW's threads.  Both contiguous CPU tensors of the same size."""

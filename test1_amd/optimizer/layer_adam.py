@@ -191,6 +191,26 @@ class LayerAdam:
                                    None if bf16_views is None else bf16_views[p])
         return loss
 
+    @torch.no_grad()
+    def step_rows(self, layer_idx: int, row_slot: torch.Tensor, rows: torch.Tensor,
+                  param_view: torch.Tensor, bf16_view: Optional[torch.Tensor] = None):
+        """Update a one-parameter unit (a [V, H] table) whose gradient is zero
+        outside the rows that ``row_slot`` maps into ``rows`` (not in the
+        reference: the dense ``step_with_grad_views`` on the scattered
+        gradient gives the same bits)."""
+        group = self._group(layer_idx)
+        if len(group["params"]) != 1:
+            raise ValueError("step_rows: the unit must hold exactly one parameter")
+        group["step"] += 1
+        p = group["params"][0]
+        st = self.state[p]
+        beta1, beta2 = group["betas"]
+        shape = param_view.shape
+        self.cpu_adam.adam_update_rows(self.optimizer_id, group["step"], group["lr"], beta1, beta2, group["eps"],
+                                       group["weight_decay"], group["bias_correction"], param_view,
+                                       st["exp_avg"].view(shape), st["exp_avg_sq"].view(shape), row_slot, rows,
+                                       params_bf16=bf16_view)
+
     def update_learning_rate(self, new_lr):
         """Set the learning rate of every group (reference layer_adam.py:427-442)."""
         self.defaults["lr"] = new_lr

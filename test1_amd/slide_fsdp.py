@@ -137,12 +137,16 @@ class SlideFSDP(nn.Module):
                          None (default): as many as fit in half of the free
                          device memory; 0: reload every unit, as the
                          reference (slide_fsdp.py:443-444).
+      row_sparse_embedding  True (default): the embedding unit moves only the
+                         rows a batch uses (lookup rows gathered from the host
+                         table, gradient rows offloaded); False: the whole
+                         table both ways, as the reference.  Same bits.
     """
 
     def __init__(self, model, config: SlideFSDPConfig, *, stage_chunk_elems: Optional[int] = None,
                  stage_depth: int = 3, grad_ring_depth: Optional[int] = None, wait_timeout: Optional[float] = None,
                  d2h_engine: str = "sdma", h2d_format: str = "fp32",
-                 resident_layers: Optional[int] = None):
+                 resident_layers: Optional[int] = None, row_sparse_embedding: bool = True):
         super().__init__()
         if config.param_transfer_mode != "full":
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
@@ -177,7 +181,9 @@ class SlideFSDP(nn.Module):
         self.layer_optimizer = self._create_optimizer(config)
         self.layer_states: List[LayerRuntimeState] = []
         self._create_layer_states()
-        self.runtime.init_grad_slots({s.layer_idx: s.total_size for s in self.layer_states})
+        if row_sparse_embedding and self._row_sparse_ok():
+            self.layer_states[0].enable_row_sparse()
+        self.runtime.init_grad_slots({s.layer_idx: s.total_size for s in self.layer_states if not s.row_sparse})
         # Updates run in the order the next forward loads units: the first
         # decoder, then the embedding, then the rest.
         self.runtime.update_priority = lambda u: 1 - u if u <= 1 else u
@@ -237,6 +243,11 @@ class SlideFSDP(nn.Module):
         for idx, layer in enumerate(self.all_layers):
             self.layer_states.append(LayerRuntimeState(layer, idx, self.config, self.runtime, self.layer_optimizer,
                                                        is_last_layer=(idx == n - 1)))
+
+    def _row_sparse_ok(self) -> bool:
+        emb = self.embed_tokens
+        return (isinstance(emb, nn.Embedding) and emb.max_norm is None and not emb.scale_grad_by_freq
+                and not emb.sparse and emb.weight.shape[1] % 16 == 0 and len(list(emb.parameters())) == 1)
 
     def _auto_resident(self) -> int:
         """Decoder layers whose weights fit in half of the free device memory."""
@@ -313,8 +324,26 @@ class SlideFSDP(nn.Module):
                 sf._on_pre_backward(ctx.layer_state)
                 return grad_output, None, None
 
+        class EmbeddingRows(torch.autograd.Function):
+            """Row-sparse lookup of the embedding unit.  The weight is an input
+            only so that the output requires grad; its gradient goes to the
+            host as rows (``offload_rows``), never into ``weight.grad``."""
+
+            @staticmethod
+            def forward(ctx, ids, layer_state, weight):
+                ctx.layer_state = layer_state
+                ctx.save_for_backward(ids)
+                return layer_state.gather_rows(ids)
+
+            @staticmethod
+            def backward(ctx, grad_out):
+                (ids,) = ctx.saved_tensors
+                ctx.layer_state.offload_rows(grad_out, ids)
+                return None, None, None
+
         self._PreLayerFunction = PreLayerFunction
         self._PostLayerFunction = PostLayerFunction
+        self._EmbeddingRows = EmbeddingRows
 
         self._hook_handles = []
         for idx, state in enumerate(self.layer_states):
@@ -402,10 +431,14 @@ class SlideFSDP(nn.Module):
         # reference issues the embedding first (slide_fsdp.py:536-541).
         if next_state is not None:
             next_state.to_device_async(is_backward=False)
-        embed_state.to_device_async(is_backward=False)
         embed_state._post_called = False
-        embed_state.wait_for_h2d()
-        hidden_states = embed_state.layer(input_ids)
+        if embed_state.row_sparse:
+            ids = input_ids if input_ids.device == self.device else input_ids.to(self.device)
+            hidden_states = self._EmbeddingRows.apply(ids, embed_state, self.embed_tokens.weight)
+        else:
+            embed_state.to_device_async(is_backward=False)
+            embed_state.wait_for_h2d()
+            hidden_states = embed_state.layer(input_ids)
         hidden_states = self._PostLayerFunction.apply(hidden_states, embed_state, False)
 
         cache_position = torch.arange(0, seq_length, device=hidden_states.device)

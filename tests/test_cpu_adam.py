@@ -175,3 +175,52 @@ def test_host_cast_matches_golden():
                                  params_bf16=torch.empty(8))
         finally:
             cpu_adam.destroy_adam(71)
+
+
+@pytest.mark.parametrize("grad_dtype", [torch.float32, torch.bfloat16])
+def test_row_sparse_update_equals_dense_update(grad_dtype):
+    # A [V, H] table whose gradient is zero outside a few rows: the row-sparse
+    # update gives the dense update's bits for params, moments and the bf16
+    # copy, over three steps (the bias-correction state advances the same way).
+    rng = np.random.default_rng(3)
+    V, H = 1000, 64
+    p0 = torch.from_numpy((rng.standard_normal((V, H)) * 0.02).astype(np.float32))
+    dense = [p0.clone(), torch.zeros(V, H), torch.zeros(V, H), torch.empty(V, H, dtype=torch.bfloat16)]
+    sparse = [p0.clone(), torch.zeros(V, H), torch.zeros(V, H), torch.empty(V, H, dtype=torch.bfloat16)]
+    cpu_adam.create_adam(80, 1e-3, 0.9, 0.999, 1e-8, 0.01, True)
+    cpu_adam.create_adam(81, 1e-3, 0.9, 0.999, 1e-8, 0.01, True)
+    for step in (1, 2, 3):
+        ids = torch.from_numpy(rng.integers(0, V, 37))  # with repeats
+        rows = torch.from_numpy((rng.standard_normal((37, H)) * 1e-3).astype(np.float32)).to(grad_dtype)
+        # repeated ids carry the same (summed) row, as gathered from a dense grad
+        first = {}
+        for k, r in enumerate(ids.tolist()):
+            first.setdefault(r, k)
+        for k, r in enumerate(ids.tolist()):
+            rows[k] = rows[first[r]]
+        g = torch.zeros(V, H, dtype=grad_dtype)
+        g[ids] = rows
+        cpu_adam.adam_update(80, step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, dense[0], g, dense[1], dense[2],
+                             params_bf16=dense[3])
+        row_slot = torch.full((V,), -1, dtype=torch.int64)
+        row_slot[ids] = torch.arange(37)
+        cpu_adam.adam_update_rows(81, step, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, sparse[0], sparse[1], sparse[2],
+                                  row_slot, rows, params_bf16=sparse[3])
+        for a, b in zip(dense, sparse):
+            assert torch.equal(a.view(torch.int16 if a.dtype == torch.bfloat16 else torch.int32),
+                               b.view(torch.int16 if b.dtype == torch.bfloat16 else torch.int32)), step
+    cpu_adam.destroy_adam(80)
+    cpu_adam.destroy_adam(81)
+
+
+def test_row_sparse_update_rejects_bad_shapes():
+    cpu_adam.create_adam(82, 1e-3)
+    p, m, v = torch.zeros(4, 24), torch.zeros(4, 24), torch.zeros(4, 24)
+    slot = torch.tensor([0, -1, -1, -1])
+    with pytest.raises(RuntimeError, match="failed"):  # row length not a multiple of 16
+        cpu_adam.adam_update_rows(82, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, True, p, m, v, slot, torch.zeros(1, 24))
+    p, m, v = torch.zeros(4, 32), torch.zeros(4, 32), torch.zeros(4, 32)
+    with pytest.raises(RuntimeError, match="failed"):  # a slot beyond the gradient rows
+        cpu_adam.adam_update_rows(82, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, True, p, m, v,
+                                  torch.tensor([0, 1, -1, -1]), torch.zeros(1, 32))
+    cpu_adam.destroy_adam(82)

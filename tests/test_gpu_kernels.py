@@ -180,3 +180,43 @@ def test_sdma_copy_d2h(dev):
     kernels.dma_wait(h)
     exp = oracle.pack_b16([p.view(torch.int16).numpy() for p in parts])
     assert np.array_equal(host.view(torch.int16).numpy().view(np.uint16), exp)
+
+
+@pytest.mark.parametrize("row_len", [4096, 24, 13])
+def test_gather_rows_from_pinned_host_table(dev, row_len):
+    # fp32 rows read by the kernel from pinned host memory, rounded to bf16:
+    # equal to the oracle cast of the same rows (vector path for row_len % 8
+    # == 0, scalar path otherwise), repeated ids included.
+    V, ntok = 257, 300
+    table = pinned_empty((V, row_len), torch.float32)
+    table.copy_(rand_f32(V * row_len, row_len).view(V, row_len))
+    ids = torch.from_numpy(np.random.default_rng(row_len).integers(0, V, ntok)).to(dev)
+    out = torch.full((ntok, row_len), 3.0, dtype=torch.bfloat16, device=dev)
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    kernels.gather_rows(table, ids, out, bad=bad)
+    torch.cuda.synchronize()
+    exp = oracle.cast_f32_bf16(table.numpy()[ids.cpu().numpy()].reshape(-1))
+    assert np.array_equal(bits16(out).reshape(-1), exp)
+    assert int(bad.item()) == 0
+
+
+def test_gather_rows_b16_into_pinned_host_and_bad_ids(dev):
+    # 16-bit rows copied from device memory into pinned host memory by a
+    # capped grid (the gradient-row offload); ids out of range give 0xFFFF
+    # rows and raise the flag, in-range rows are unaffected.
+    V, H = 64, 128
+    table = torch.randn(V, H, device=dev).bfloat16()
+    ids = torch.tensor([3, 0, 63, 64, -1, 3, 17], dtype=torch.int64, device=dev)
+    out = pinned_empty((ids.numel(), H), torch.bfloat16)
+    bad = pinned_empty(1, torch.int32)
+    bad.zero_()
+    kernels.gather_rows(table, ids, out, bad=bad, max_workgroups=2)
+    torch.cuda.synchronize()
+    t = bits16(table)
+    o = bits16(out)
+    for k, r in enumerate(ids.tolist()):
+        if 0 <= r < V:
+            assert np.array_equal(o[k], t[r]), k
+        else:
+            assert (o[k] == 0xFFFF).all(), k
+    assert int(bad[0]) == 1

@@ -54,10 +54,13 @@ def test_round_trip_bit_exact_small(dev, use_ring):
     assert torch.equal(hg_off.view(torch.int16), hg_ref.view(torch.int16))
 
 
-def test_round_trip_llama3_8b_checkpoint_shape(dev):
-    """32 layers of [4, 1024, 4096] bf16 checkpoints (32 MiB each) through the
-    pinned slots and back, bit-exact."""
-    L, shape = 32, (4, 1024, 4096)
+@pytest.mark.parametrize("L,shape", [(32, (4, 1024, 4096)), (48, (2, 4096, 5120))],
+                         ids=["llama3-8b", "qwen2.5-14b"])
+def test_round_trip_model_checkpoint_shapes(dev, L, shape):
+    """The models' checkpoints through the pinned slots and back, bit-exact:
+    32 layers of [4, 1024, 4096] bf16 (32 MiB each, Llama-3-8B at batch 4 x
+    1024) and 48 layers of [2, 4096, 5120] (80 MiB each, Qwen2.5-14B at batch
+    2 x 4096)."""
     ws = [torch.full((shape[-1],), 1.0 + 1e-2 * i, dtype=torch.bfloat16, device=dev, requires_grad=True)
           for i in range(L)]
     seen = {}

@@ -15,15 +15,25 @@ V, H, I, L = 1024, 256, 512, 3
 LR, BETAS, EPS, WD = 1e-3, (0.9, 0.999), 1e-8, 0.01
 
 
-def make_model():
-    from transformers import LlamaConfig, LlamaForCausalLM
-
-    cfg = LlamaConfig(vocab_size=V, hidden_size=H, intermediate_size=I, num_hidden_layers=L,
-                      num_attention_heads=8, num_key_value_heads=4, max_position_embeddings=512,
-                      rope_theta=500000.0, tie_word_embeddings=False)
+def make_model(arch: str = "llama"):
+    """A small model of the Llama-3 family, or of the Qwen2 family (q/k/v
+    projections with biases, as Qwen2.5-14B)."""
+    if arch == "llama":
+        from transformers import LlamaConfig as C, LlamaForCausalLM as M
+    else:
+        from transformers import Qwen2Config as C, Qwen2ForCausalLM as M
+    cfg = C(vocab_size=V, hidden_size=H, intermediate_size=I, num_hidden_layers=L,
+            num_attention_heads=8, num_key_value_heads=4, max_position_embeddings=512,
+            rope_theta=500000.0, tie_word_embeddings=False)
     cfg._attn_implementation = "sdpa"
     torch.manual_seed(1234)
-    return LlamaForCausalLM(cfg)
+    model = M(cfg)
+    if arch != "llama":
+        with torch.no_grad():  # non-zero biases, so that their updates are checked too
+            for name, p in model.named_parameters():
+                if name.endswith(".bias"):
+                    p.normal_(0.0, 0.02)
+    return model
 
 
 def units_of(model):
@@ -59,13 +69,16 @@ def test_schedule_matches_oracle(dev, resident):
 
 # (parameter H2D format, resident decoder layers, gradient D2H engine, host gradient slots:
 #  None = one per unit, k = a ring of k)
-MODES = [("fp32", 0, "sdma", None), ("bf16", 0, "sdma", None), ("fp32", L - 1, "sdma", None),
-         ("bf16", L - 1, "sdma", None), ("fp32", 0, "kernel", None), ("bf16", L - 1, "kernel", None),
-         ("fp32", L - 1, "sdma", 2), ("bf16", 0, "kernel", 2)]
+#  and the model family
+MODES = [("fp32", 0, "sdma", None, "llama"), ("bf16", 0, "sdma", None, "llama"),
+         ("fp32", L - 1, "sdma", None, "llama"), ("bf16", L - 1, "sdma", None, "llama"),
+         ("fp32", 0, "kernel", None, "llama"), ("bf16", L - 1, "kernel", None, "llama"),
+         ("fp32", L - 1, "sdma", 2, "llama"), ("bf16", 0, "kernel", 2, "llama"),
+         ("fp32", L - 1, "sdma", None, "qwen2"), ("bf16", 0, "kernel", None, "qwen2")]
 
 
-@pytest.mark.parametrize("h2d_format,resident,d2h_engine,ring", MODES)
-def test_updates_match_oracle_bit_exact(dev, h2d_format, resident, d2h_engine, ring):
+@pytest.mark.parametrize("h2d_format,resident,d2h_engine,ring,arch", MODES)
+def test_updates_match_oracle_bit_exact(dev, h2d_format, resident, d2h_engine, ring, arch):
     """Every unit's host update equals the oracle AdamW applied to the same
     (captured) bf16 grads and fp32 master, for 3 steps.  With bf16 H2D the
     host bf16 copy of every unit is the oracle cast of its master after each
@@ -73,7 +86,7 @@ def test_updates_match_oracle_bit_exact(dev, h2d_format, resident, d2h_engine, r
     keep their forward weights for the backward."""
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
-    model = make_model()
+    model = make_model(arch)
     sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS),
                    wait_timeout=120, h2d_format=h2d_format, resident_layers=resident, d2h_engine=d2h_engine,
                    grad_ring_depth=ring)
@@ -145,11 +158,11 @@ def reference_losses(model, steps_ids, dev):
     return losses, first_grads
 
 
-@pytest.mark.parametrize("h2d_format,resident,d2h_engine,ring", MODES)
-def test_loss_parity_with_non_offloaded_run(dev, h2d_format, resident, d2h_engine, ring):
+@pytest.mark.parametrize("h2d_format,resident,d2h_engine,ring,arch", MODES)
+def test_loss_parity_with_non_offloaded_run(dev, h2d_format, resident, d2h_engine, ring, arch):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
-    model = make_model()
+    model = make_model(arch)
     steps = batches(10)
     ref_losses, ref_grads = reference_losses(model, steps, dev)
     sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS),

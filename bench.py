@@ -276,6 +276,19 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
     return r
 
 
+def megatron_flops_per_step(w: dict) -> float:
+    """Model FLOPs of one training step by the Megatron-LM estimate with GQA
+    and SwiGLU that the reference reports (utils/metric.py:4-53): 3 passes x
+    2 FLOPs per multiply-add x 2 (forward GEMM pairs), no recompute term."""
+    B, S, L, H = w["batch"], w["seq"], w["layers"], w["hidden"]
+    heads, kv, inter, vocab = w["heads"], w["kv"], w["inter"], w["vocab"]
+    q_ratio = (H // heads) * heads / H
+    attention = (1 + kv / heads + S / H) * q_ratio
+    mlp = inter / H * 1.5
+    logits = vocab / (2 * L * H)
+    return 12.0 * B * S * L * H * H * (attention + mlp + logits)
+
+
 def host_mem_available() -> int:
     """MemAvailable of this host in bytes (0 if unknown)."""
     try:
@@ -417,6 +430,12 @@ def main():
             "algorithmic_bytes_per_launch": cast_bytes / ncast if ncast else None,
         },
         "host_link": link_stats(r, args.steps),
+        "model_tflops": {
+            "flops_per_step": megatron_flops_per_step(w),
+            "tflops": megatron_flops_per_step(w) / (elapsed / args.steps) / 1e12,
+            "note": "Megatron-LM estimate as the reference's utils/metric.py (no recompute term); "
+                    "context only: the step is bound by the host link, not by MFMA",
+        },
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
         "losses": losses,
         "variants": variants,

@@ -224,7 +224,8 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
 
     t0 = time.time()
     cfg = SlideFSDPConfig(device=dev, lr=1e-5, weight_decay=0.01, attention_implementation="sdpa")
-    sf = SlideFSDP(model, cfg, d2h_engine=d2h_engine, h2d_format=h2d_format, resident_layers=resident_layers)
+    sf = SlideFSDP(model, cfg, d2h_engine=d2h_engine, h2d_format=h2d_format, resident_layers=resident_layers,
+                   fused_cross_entropy=args.fused_ce)
     log(f"[bench] SlideFSDP ({h2d_format} H2D, {sf.resident_layers} resident decoders, {d2h_engine} D2H) "
         f"ready in {time.time() - t0:.1f}s")
     B, S = w["batch"], w["seq"]
@@ -333,6 +334,8 @@ def main():
     ap.add_argument("--resident-layers", type=int, default=None,
                     help="decoder layers kept on the GPU from their forward to their backward "
                          "(default: as many as fit in half of the free HBM)")
+    ap.add_argument("--fused-ce", action="store_true",
+                    help="chunked linear + cross entropy in the output unit (no [B,S,V] logits)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs the layer-streaming path on one GPU only; use --gpus 1", file=sys.stderr)
@@ -413,7 +416,7 @@ def main():
                    "global_batch": B, "seq_len": S, "layers": w["layers"], "hidden": w["hidden"],
                    "params": total_params, "parallelism": "none (1 GPU)",
                    "h2d_format": args.h2d_format, "resident_layers": r["resident_layers"],
-                   "d2h_engine": args.d2h_engine},
+                   "d2h_engine": args.d2h_engine, "fused_cross_entropy": args.fused_ce},
         "roofline": {
             "bound": "hbm",
             "kernel": "cast_flat_kernel (fp32 -> bf16 RNE staging cast)",

@@ -47,6 +47,7 @@ from transformers.modeling_outputs import CausalLMOutputWithPast
 
 from .config import SlideFSDPConfig
 from .distributed_sync import create_distributed_sync
+from .fused_ce import chunked_linear_cross_entropy
 from .layer_state import LayerRuntimeState, StreamingRuntime
 from .optimizer import LayerAdam
 from .pinned import pinned_empty
@@ -60,21 +61,34 @@ except ImportError:  # older versions keep the decoder's _update_causal_mask
 
 class OutputLayer(nn.Module):
     """Final norm + lm_head + shifted cross-entropy as one unit (reference
-    slide_fsdp.py:45-113, the branch without the optional fused kernel:
-    full logits and ``nn.CrossEntropyLoss``)."""
+    slide_fsdp.py:45-113).  ``fused=False``: full logits and
+    ``nn.CrossEntropyLoss``, the reference's branch without a fused kernel;
+    ``fused=True``: the chunked linear + cross entropy of ``fused_ce`` in
+    place of the reference's optional fused kernel (loss only, no logits,
+    as that branch)."""
 
-    def __init__(self, norm: nn.Module, lm_head: nn.Module, hidden_size: int):
+    def __init__(self, norm: nn.Module, lm_head: nn.Module, hidden_size: int, fused: bool = False,
+                 chunk_rows: int = 0):
         super().__init__()
         self.norm = norm
         self.lm_head = lm_head
         self.hidden_size = hidden_size
-        self.lce = None
+        self.fused = fused
+        self.chunk_rows = chunk_rows
+        self.lce = chunked_linear_cross_entropy if fused else None
         self.loss_fn = nn.CrossEntropyLoss()
 
     def forward(self, hidden_states: torch.Tensor, labels: Optional[torch.Tensor] = None):
         hidden_states = self.norm(hidden_states)
-        logits = self.lm_head(hidden_states)
         loss = None
+        logits = None
+        if labels is not None and self.fused:
+            shift_hidden = hidden_states[..., :-1, :].contiguous().view(-1, self.hidden_size)
+            shift_labels = labels[..., 1:].contiguous().view(-1)
+            loss = self.lce(shift_hidden, self.lm_head.weight, shift_labels, self.loss_fn.ignore_index,
+                            self.chunk_rows)
+            return loss, logits
+        logits = self.lm_head(hidden_states)
         if labels is not None:
             shift_logits = logits[..., :-1, :].contiguous()
             shift_labels = labels[..., 1:].contiguous()
@@ -141,12 +155,17 @@ class SlideFSDP(nn.Module):
                          rows a batch uses (lookup rows gathered from the host
                          table, gradient rows offloaded); False: the whole
                          table both ways, as the reference.  Same bits.
+      fused_cross_entropy  False (default): full logits + nn.CrossEntropyLoss,
+                         the reference's path without its optional fused
+                         kernel; True: chunked linear + cross entropy (loss
+                         only, no [B,S,V] logits), in place of that kernel.
     """
 
     def __init__(self, model, config: SlideFSDPConfig, *, stage_chunk_elems: Optional[int] = None,
                  stage_depth: int = 3, grad_ring_depth: Optional[int] = None, wait_timeout: Optional[float] = None,
                  d2h_engine: str = "sdma", h2d_format: str = "fp32",
-                 resident_layers: Optional[int] = None, row_sparse_embedding: bool = True):
+                 resident_layers: Optional[int] = None, row_sparse_embedding: bool = True,
+                 fused_cross_entropy: bool = False):
         super().__init__()
         if config.param_transfer_mode != "full":
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
@@ -169,6 +188,7 @@ class SlideFSDP(nn.Module):
         self.world_size = 1
         self.dist_sync = create_distributed_sync(config)
 
+        self._fused_ce = bool(fused_cross_entropy)
         self._split_model(model)
         self.max_param_size = self._calculate_max_param_size()
         self.total_params = sum(sum(p.numel() for p in layer.parameters()) for layer in self.all_layers)
@@ -216,7 +236,8 @@ class SlideFSDP(nn.Module):
         lm_head = model.get_output_embeddings()
         if lm_head is not None and lm_head.weight is self.embed_tokens.weight:
             raise NotImplementedError("tied input/output embeddings are not supported (one parameter in two units)")
-        self.output_layer = OutputLayer(norm=decoder.norm, lm_head=lm_head, hidden_size=model.config.hidden_size)
+        self.output_layer = OutputLayer(norm=decoder.norm, lm_head=lm_head, hidden_size=model.config.hidden_size,
+                                        fused=getattr(self, "_fused_ce", False))
         self.all_layers = [self.embed_tokens] + list(self.decoder_layers) + [self.output_layer]
 
     def _decoders_use_rng(self) -> bool:

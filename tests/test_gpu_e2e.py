@@ -1,7 +1,10 @@
-"""SlideFSDP end to end on a small Llama: staging order, update parity with the
-oracle, and loss parity with a non-offloaded PyTorch bf16 run over 10 steps."""
+"""SlideFSDP end to end on small Llama and Qwen2 models, across the runtime's
+options: staging order, update parity with the oracle (bit-exact), loss
+parity with a non-offloaded PyTorch bf16 run over 10 steps, padding masks,
+learning-rate changes and save_pretrained."""
 
 import copy
+import os
 
 import numpy as np
 import pytest
@@ -234,4 +237,57 @@ def test_padding_mask_matches_non_offloaded_run(dev):
     loss2 = sf(input_ids=ids, attention_mask=mask, labels=labels).loss.item()
     sf.wait_for_updates()
     assert np.isfinite(out.loss.item()) and np.isfinite(loss2)
+    sf.close()
+
+
+def test_learning_rate_change_and_save_pretrained(dev, tmp_path):
+    """update_learning_rate takes effect at the next update (two steps checked
+    bit-exact against the oracle with the same learning rates), and
+    save_pretrained writes the bf16 rounding of every fp32 master, then leaves
+    the parameters on their masters."""
+    from safetensors.torch import load_file
+
+    from test1_amd import SlideFSDP, SlideFSDPConfig
+
+    model = make_model()
+    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS),
+                   wait_timeout=120)
+    orc = oracle.LayerAdamOracle(lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
+    ref_units = []
+    for ps in units_of(model):
+        arrs = [p.detach().numpy().copy() for p in ps]
+        ref_units.append(arrs)
+        orc.add_layer(arrs)
+    for k, (ids, lr) in enumerate(zip(batches(2), (LR, LR / 7))):
+        if k == 1:
+            sf.update_learning_rate(lr)
+            orc.lr = lr
+        sf.runtime.capture = {}
+        ids = ids.to(dev)
+        sf(input_ids=ids, labels=ids)
+        sf.wait_for_updates()
+        for u in range(L + 1, -1, -1):
+            g = u16(sf.runtime.capture[u][0])
+            parts, off = [], 0
+            for a in ref_units[u]:
+                parts.append(g[off:off + a.size].reshape(a.shape))
+                off += a.size
+            orc.step_layer(u, parts)
+    for u, ps in enumerate(units_of(model)):
+        for p, a in zip(ps, ref_units[u]):
+            assert np.array_equal(p.detach().numpy().view(np.uint32), a.view(np.uint32)), f"unit {u}"
+
+    out = sf.save_pretrained(str(tmp_path / "ckpt"))
+    saved = {}
+    for name in os.listdir(out):
+        if name.endswith(".safetensors"):
+            saved.update(load_file(os.path.join(out, name)))
+    named = dict(model.named_parameters())
+    assert set(saved) == set(named)
+    for n, t in saved.items():
+        p = named[n]
+        assert t.dtype == torch.bfloat16
+        assert np.array_equal(u16(t).reshape(-1), oracle.cast_f32_bf16(p.detach().numpy().reshape(-1))), n
+    for p in named.values():
+        assert p.dtype == torch.float32 and p.device.type == "cpu"
     sf.close()

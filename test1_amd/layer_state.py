@@ -453,6 +453,9 @@ class StreamingRuntime:
         # first (``init_grad_slots`` sets it up once the slots exist).
         self.offload_executor: Optional[PriorityUpdateExecutor] = None
         self.update_executor = PriorityUpdateExecutor("sf-update")
+        # Units with their own device buffer are staged for the next forward
+        # by the update thread, right after their update.
+        self.stage_after_update = False
         # Queue priority of a unit's update (lower runs first); the model sets
         # it to the unit's position in the next forward.
         self.update_priority: Callable[[int], int] = lambda unit: unit
@@ -544,6 +547,10 @@ class LayerRuntimeState(nn.Module):
         # Row-sparse embedding (``enable_row_sparse``): only the batch's rows
         # cross the host link, in both directions.
         self.row_sparse = False
+        # Own unit already staged with the next step's weights by the update
+        # thread (``stage_for_next_forward``): (unit, copy-and-cast event).
+        self._prefetched: Optional[Tuple[Dict[str, Any], torch.cuda.Event]] = None
+        self._prefetch_lock = threading.Lock()
         self._post_called = False
         self._bwd_armed = False
         self._bwd_compute_done = False
@@ -607,10 +614,32 @@ class LayerRuntimeState(nn.Module):
         return zip(self._param_maps.items(), self._params)
 
     def refresh_host_copy(self) -> None:
-        """Recompute the bf16 host copy from the fp32 master (bf16 H2D only).
-        Updates keep it current; call this after writing the master directly."""
+        """Recompute the bf16 host copy from the fp32 master (bf16 H2D only)
+        and drop a staging made for the next forward.  Updates keep both
+        current; call this after writing the master directly."""
+        with self._prefetch_lock:
+            self._prefetched = None
         if self._cpu_params_bf16 is not None and self.total_size:
             _cpu_adam.cast_f32_bf16(self._cpu_params_flat, self._cpu_params_bf16)
+
+    def stage_for_next_forward(self) -> None:
+        """Stage the freshly updated master into this unit's own device buffer
+        (update thread, right after the update).  The copy starts during the
+        backward, when the host-to-device direction of the link is otherwise
+        idle, instead of in the next forward; the cast waits for the buffer's
+        last reader (the unit's backward).  Same bits as staging in the
+        forward: the master does not change before the next update."""
+        unit = self._own_unit
+        if unit is None or self._current_gpu_cache is not None or self.row_sparse:
+            return
+        stager = self.runtime.stager
+        if self._cpu_params_bf16 is not None:
+            done = stager.load(self._cpu_params_bf16, unit["param"], unit["ready"])
+        else:
+            done = stager.finish(stager.begin(self._cpu_params_flat), unit["param"], unit["ready"])
+        with self._prefetch_lock:
+            self._prefetched = (unit, done)
+        self.runtime.mark("staged_after_update", self.layer_idx)
 
     def _bind_device_views(self, unit: Dict[str, Any]) -> None:
         buf = unit["param"]
@@ -640,6 +669,14 @@ class LayerRuntimeState(nn.Module):
         if self._current_gpu_cache is not None:
             return  # already resident (last decoder / output / own unit)
         self.wait_for_update()
+        # Checked after the update: the update thread stages an own unit for
+        # the next forward as the last part of the update task.
+        with self._prefetch_lock:
+            pre, self._prefetched = self._prefetched, None
+        if pre is not None:
+            unit, self._h2d_done = pre
+            self._bind_unit(unit, is_backward)
+            return
         stager = self.runtime.stager
         # The backward of an embedding never reads its weights (its gradient
         # depends only on the indices), so no copy or cast is needed then.
@@ -1015,6 +1052,8 @@ class LayerRuntimeState(nn.Module):
                                                               param_views=self._master_views(),
                                                               bf16_views=self._bf16_views())
             rt.mark("adam_done", self.layer_idx)
+            if rt.stage_after_update:
+                self.stage_for_next_forward()
         finally:
             rt.grad_ring.release(slot)
             self.update_finished.set()

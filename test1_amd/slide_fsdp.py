@@ -155,6 +155,13 @@ class SlideFSDP(nn.Module):
                          rows a batch uses (lookup rows gathered from the host
                          table, gradient rows offloaded); False: the whole
                          table both ways, as the reference.  Same bits.
+      stage_after_update  True (default): a unit with its own device buffer
+                         is staged with its updated weights by the update
+                         thread right after its update, i.e. during the
+                         backward, when the host-to-device direction of the
+                         link is idle, instead of in the next forward.  With
+                         every decoder resident, the last decoder and the
+                         output unit get own buffers too.  Same bits.
       fused_cross_entropy  False (default): full logits + nn.CrossEntropyLoss,
                          the reference's path without its optional fused
                          kernel; True: chunked linear + cross entropy (loss
@@ -165,7 +172,7 @@ class SlideFSDP(nn.Module):
                  stage_depth: int = 3, grad_ring_depth: Optional[int] = None, wait_timeout: Optional[float] = None,
                  d2h_engine: str = "sdma", h2d_format: str = "fp32",
                  resident_layers: Optional[int] = None, row_sparse_embedding: bool = True,
-                 fused_cross_entropy: bool = False):
+                 fused_cross_entropy: bool = False, stage_after_update: bool = True):
         super().__init__()
         if config.param_transfer_mode != "full":
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
@@ -207,6 +214,7 @@ class SlideFSDP(nn.Module):
         # Updates run in the order the next forward loads units: the first
         # decoder, then the embedding, then the rest.
         self.runtime.update_priority = lambda u: 1 - u if u <= 1 else u
+        self.runtime.stage_after_update = bool(stage_after_update)
         self._make_resident(self._auto_resident() if resident_layers is None else int(resident_layers))
         self._setup_autograd_functions()
 
@@ -265,6 +273,16 @@ class SlideFSDP(nn.Module):
             self.layer_states.append(LayerRuntimeState(layer, idx, self.config, self.runtime, self.layer_optimizer,
                                                        is_last_layer=(idx == n - 1)))
 
+    def _act_prefetch_stream(self) -> torch.cuda.Stream:
+        """Stream of the backward's checkpoint prefetches: behind the weight
+        copies on the H2D stream, unless those run during the backward
+        (staging after updates); then the D2H stream, which the SDMA gradient
+        offload leaves free in the backward."""
+        rt = self.runtime
+        if rt.stage_after_update and rt.d2h_engine == "sdma":
+            return rt.d2h_stream
+        return rt.h2d_stream
+
     def _row_sparse_ok(self) -> bool:
         emb = self.embed_tokens
         return (isinstance(emb, nn.Embedding) and emb.max_norm is None and not emb.scale_grad_by_freq
@@ -297,6 +315,16 @@ class SlideFSDP(nn.Module):
             st = self.layer_states[unit_idx]
             st.make_resident(torch.empty(st.total_size, dtype=self.dtype, device=self.device))
         self.resident_layers = k
+        if self.runtime.stage_after_update and n_dec >= 1 and k == n_dec - 1:
+            # Every decoder but the last has its own buffer: give the last
+            # decoder and the output unit theirs as well, so that all units are
+            # staged right after their update (the pool is then unused).
+            free, _ = torch.cuda.mem_get_info(self.device)
+            elem = torch.empty((), dtype=self.dtype).element_size()
+            extra = [self.layer_states[n_dec], self.layer_states[n_dec + 1]]
+            if sum(st.total_size for st in extra) * elem < free // 4:
+                for st in extra:
+                    st.make_resident(torch.empty(st.total_size, dtype=self.dtype, device=self.device))
 
     # ------------------------------------------------------------------
     def _setup_autograd_functions(self) -> None:
@@ -495,7 +523,7 @@ class SlideFSDP(nn.Module):
                                        prefetch_ring=self._act_ring, trace=trace,
                                        max_workgroups=self.runtime.d2h_workgroups,
                                        stream=self.runtime.d2h_stream,
-                                       prefetch_stream=self.runtime.h2d_stream,
+                                       prefetch_stream=self._act_prefetch_stream(),
                                        pack_fence=self.runtime.stager.fence_after_casts):
                     hidden_states = checkpoint(_layer_forward, hidden_states, causal_mask, self.position_embeddings,
                                                layer_state.layer, **ckpt_kw)

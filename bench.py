@@ -267,6 +267,8 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
         "cast": elapsed_stats(rt.stager.cast_timing), "ncast": len(rt.stager.cast_timing or []),
         "h2d": elapsed_stats(rt.stager.copy_timing), "d2h": elapsed_stats(rt.d2h_timing),
         "total_params": sf.total_params, "resident_layers": sf.resident_layers,
+        "stage_after_update": sf.runtime.stage_after_update,
+        "row_sparse_embedding": sf.layer_states[0].row_sparse,
         "layer_numel": sum(p.numel() for p in sf.decoder_layers[0].parameters()),
         "output_numel": sum(p.numel() for p in sf.output_layer.parameters()),
     }
@@ -416,7 +418,9 @@ def main():
                    "global_batch": B, "seq_len": S, "layers": w["layers"], "hidden": w["hidden"],
                    "params": total_params, "parallelism": "none (1 GPU)",
                    "h2d_format": args.h2d_format, "resident_layers": r["resident_layers"],
-                   "d2h_engine": args.d2h_engine, "fused_cross_entropy": args.fused_ce},
+                   "d2h_engine": args.d2h_engine, "fused_cross_entropy": args.fused_ce,
+                   "stage_after_update": r["stage_after_update"],
+                   "row_sparse_embedding": r["row_sparse_embedding"]},
         "roofline": {
             "bound": "hbm",
             "kernel": "cast_flat_kernel (fp32 -> bf16 RNE staging cast)",

@@ -30,6 +30,7 @@ import os
 import sys
 import time
 from concurrent.futures import ThreadPoolExecutor
+from typing import Optional
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
@@ -206,6 +207,7 @@ def cpu_baseline(layer_numel: int, total_params: int, tokens: int, resident_para
                    f"({28 * n / t_adam / 1e9:.1f} GB/s at 28 B/param); per-step time = per-param cost x "
                    f"{total_params:,} params (cast twice, resident units once)"),
         "ms_per_layer": {"cast": t_cast * 1e3, "unpack": t_unpack * 1e3, "adam": t_adam * 1e3},
+        "adam_gbs": 28 * n / t_adam / 1e9,
     }
 
 
@@ -290,6 +292,21 @@ def megatron_flops_per_step(w: dict) -> float:
     mlp = inter / H * 1.5
     logits = vocab / (2 * L * H)
     return 12.0 * B * S * L * H * H * (attention + mlp + logits)
+
+
+def host_dram_stats(r: dict, args, cpu: Optional[dict]) -> dict:
+    """Host DRAM traffic of one step: the host AdamW's 26 B per parameter
+    (28 with the bf16 copy) plus what the copy engines read and write.  The
+    reference rate is a streaming AdamW on the same cores in the same run
+    (the CPU baseline's), the nearest this host gets to its DRAM peak."""
+    adam_b = (28 if args.h2d_format == "bf16" else 26) * r["total_params"]
+    h2d = r["h2d"][1] / args.steps
+    d2h = r["d2h"][1] / args.steps
+    step_s = r["elapsed"] / args.steps
+    total = adam_b + h2d + d2h
+    ref = None if cpu is None else cpu.get("adam_gbs")
+    return {"bytes_per_step": total, "adam_bytes_per_step": adam_b, "achieved_gbs": total / step_s / 1e9,
+            "streaming_adam_gbs": ref, "frac_of_streaming_adam": None if not ref else total / step_s / 1e9 / ref}
 
 
 def host_mem_available() -> int:
@@ -443,6 +460,7 @@ def main():
             "note": "Megatron-LM estimate as the reference's utils/metric.py (no recompute term); "
                     "context only: the step is bound by the host link, not by MFMA",
         },
+        "host_dram": host_dram_stats(r, args, cpu),
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
         "losses": losses,
         "variants": variants,

@@ -1,4 +1,4 @@
-"""Device buffer pool and per-unit runtime of the layer-streaming path.
+"""Device buffers and the per-unit runtime of the layer-streaming path.
 
 Reference layer_state.py:28-467.  The reference casts each unit's fp32
 master to bf16 on the host (one thread, layer_state.py:301), copies the bf16
@@ -6,30 +6,35 @@ layer to the GPU and blocks on the copy stream (:326); gradients come back
 through one shared pinned buffer (:367-381), which serialises each offload
 behind the previous unit's CPU update (:362-363).
 
-Here the GPU does the staging, and everything on the GPU is ordered with
-events instead of host waits:
+Here the GPU does the staging, and work on the GPU is ordered with events
+instead of host waits:
 
-* H2D: the pinned fp32 master is copied by DMA into a device fp32 staging
-  ring (``H2DStager``), one chunk per slot, on ``h2d_stream``; a HIP kernel
-  casts each chunk to bf16 (RNE) into the pool unit on ``cast_stream``.
-  The cast waits for the unit's ``ready`` event: the event after which the
-  unit's previous contents are no longer read (the compute that used it, or
-  the D2H of its gradients).  The reference has no such fence
-  (layer_state.py:292-315 start the next H2D into a unit released on the
-  host without waiting for the compute stream).
-* The compute stream waits for the unit's load with ``wait_event``; no host
-  thread blocks on a copy.
-* Gradients: after the last gradient of a unit is accumulated, one pack
-  kernel gathers the per-parameter bf16 grads into the unit's contiguous
-  grad buffer (offset-identical to the fp32 master), a DMA copies it into a
-  pinned slot of ``GradStagingRing`` (2 deep, so unit i's offload waits for
-  unit i+2's update, not unit i+1's), and the update thread runs LayerAdam
-  on the slot in place.
+* Units live in a 2-unit pool (``LayerBufferPool``, the reference's) or in a
+  device buffer of their own (``make_resident``): an own buffer keeps the
+  forward's weights for the backward, and is staged with the next step's
+  weights by the update thread right after the unit's update
+  (``stage_for_next_forward``), i.e. during the backward.
+* H2D: ``H2DStager`` copies the pinned fp32 master by DMA into a device fp32
+  ring on ``h2d_stream`` and a HIP kernel casts it to bf16 (RNE) into the
+  unit on ``cast_stream``; with bf16 H2D, ``BF16Loader`` copies the host
+  optimizer's bf16 copy straight into the unit.  Either waits for the unit's
+  ``ready`` event, after which its previous contents are no longer read (the
+  reference has no such fence: layer_state.py:292-315 start the next H2D
+  into a unit released on the host without waiting for the compute stream).
+* Gradients: once a unit's last gradient is accumulated, the offload thread
+  copies the per-parameter bf16 grads straight into a pinned host slot (one
+  per unit, ``GradSlotsPerUnit``, or a ring when the host cannot pin that
+  much), on SDMA engines or by a capped pack kernel, and queues the update;
+  the update thread (``PriorityUpdateExecutor``) runs LayerAdam on the slot,
+  taking among the units whose copies have landed the one the next forward
+  needs first.
+* The embedding unit can be row-sparse (``enable_row_sparse``): only the
+  batch's rows are read from the host table and only their gradient rows
+  come back.
 
-Memory layout in HBM (per pool unit, ``max_param_size`` elements):
-  unit["param"]  bf16, views offset-identical to the fp32 master
-  unit["grad"]   bf16, packed gradients in the same layout
-plus the fp32 staging ring (``depth`` chunks of ``chunk_elems``).
+Memory layout in HBM (per unit, offset-identical to the fp32 master):
+  unit["param"]  bf16 weights (pool units: ``max_param_size`` elements)
+plus the fp32 staging ring (``depth`` chunks of ``chunk_elems``) with fp32 H2D.
 """
 
 from __future__ import annotations

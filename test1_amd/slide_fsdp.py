@@ -8,12 +8,17 @@ its gradients are on the host, so callers never call ``optimizer.step()``.
 
 The model is split into units ``[embedding] + decoder layers + [norm +
 lm_head]`` (reference slide_fsdp.py:213-244).  fp32 masters of every unit
-live in pinned host memory; at most ``gpu_buffer_pool_size`` units are on the
-GPU at once, as bf16.  Unit i+1 is loaded while unit i computes
-(``PreLayerFunction``), unit i is released after its forward
-(``PostLayerFunction``), and in backward each unit's gradients go to the host
-and into LayerAdam while earlier units are still computing.  Checkpoint
-inputs are offloaded by ``SlidingCheckpoint``.
+live in host memory (pinned, or pageable with bf16 H2D).  On the GPU a unit
+is bf16, in one of the ``gpu_buffer_pool_size`` pool units, as in the
+reference, or in a buffer of its own when HBM allows (``resident_layers``);
+an own buffer keeps the forward's weights for the backward and is staged with
+the next step's weights right after the unit's update.  Unit i+1 is loaded
+while unit i computes (``PreLayerFunction``), a pool unit is released after
+its forward (``PostLayerFunction``), and in backward each unit's gradients go
+to the host and into LayerAdam while earlier units are still computing; the
+update thread takes the units the next forward needs first.  The embedding
+moves only the batch's rows (``row_sparse_embedding``).  Checkpoint inputs are
+offloaded by ``SlidingCheckpoint``.
 
 Single GPU only: ``param_transfer_mode="full"`` and no collectives (the
 reference's ``NoOpSync``, distributed_sync.py:313-362).
@@ -32,7 +37,12 @@ Differences from the reference, each a correctness or memory fix:
   * ``save_pretrained`` restores the fp32 masters after writing bf16 weights
     (slide_fsdp.py:721-725 leaves the parameters detached from them);
   * the mask slot of the activation offload is allocated only if a mask
-    tensor is actually saved.
+    tensor is actually saved;
+  * padding masks are built with transformers' ``create_causal_mask`` when
+    the decoder has no ``_update_causal_mask`` (transformers >= 5), where the
+    reference drops them (slide_fsdp.py:557-561).
+The performance options (own buffers, staging after updates, update order,
+row-sparse embedding, bf16 H2D, SDMA gradient copies) change no bits.
 """
 
 from __future__ import annotations

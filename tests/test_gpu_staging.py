@@ -67,3 +67,83 @@ def test_stream_layers_into_two_unit_pool(dev, chunk):
         assert np.array_equal(bits16(snap), exp), f"layer {j}"
         w = torch.from_numpy(exp[: sizes[j] // 1024 * 1024].view(np.int16).copy()).view(torch.bfloat16)
         assert torch.allclose(tot.cpu(), w.float().view(-1, 1024).sum(), rtol=1e-4, atol=1e-3)
+
+
+def test_param_streaming_llama3_8b_32_layers(dev):
+    """32 Llama-3-8B decoder layers (218,112,000 fp32 parameters each, seeded
+    per layer, in pinned host memory) streamed through a 2-unit bf16 pool:
+    the load of layer i+1 is issued before layer i's forward, on [1, 1024,
+    4096] bf16 N(0, 1) hidden states.  Every unit equals the RNE cast of its
+    master (whole layer against torch's device cast, a slice against the
+    oracle), and the output equals the same forward with weights cast by
+    torch."""
+    from transformers import LlamaConfig
+    from transformers.models.llama.modeling_llama import LlamaDecoderLayer, LlamaRotaryEmbedding
+
+    cfg = LlamaConfig(hidden_size=4096, intermediate_size=14336, num_attention_heads=32, num_key_value_heads=8,
+                      head_dim=128, rope_theta=500000.0, max_position_embeddings=2048)
+    cfg._attn_implementation = "sdpa"
+    L = 32
+    with torch.device("meta"):
+        layer = LlamaDecoderLayer(cfg, 0)
+    names = [(n, p.shape, p.numel()) for n, p in layer.named_parameters()]
+    N = sum(k for _, _, k in names)
+    assert N == 218_112_000
+    layer = layer.to_empty(device=dev).to(torch.bfloat16)
+    rope = LlamaRotaryEmbedding(config=cfg).to(dev)
+
+    masters = []
+    for i in range(L):
+        g = torch.Generator(device=dev).manual_seed(1000 + i)
+        m = pinned_empty(N, torch.float32)
+        m.copy_(torch.randn(N, generator=g, device=dev) * 0.02)
+        masters.append(m)
+    h0 = torch.randn(1, 1024, 4096, generator=torch.Generator(device=dev).manual_seed(7), device=dev).bfloat16()
+    pos = rope(h0, torch.arange(1024, device=dev).unsqueeze(0))
+
+    def bind(flat):
+        off = 0
+        for (name, shape, k), p in zip(names, layer.parameters()):
+            p.data = flat[off:off + k].view(shape)
+            off += k
+
+    def fwd(h):
+        with torch.no_grad():
+            out = layer(h, attention_mask=None, position_embeddings=pos)
+        return out[0] if isinstance(out, tuple) else out
+
+    h2d, cast = torch.cuda.Stream(), torch.cuda.Stream()
+    pool = LayerBufferPool(N, torch.bfloat16, dev, 2)
+    st = H2DStager(dev, N, 2, h2d, cast)
+    comp = torch.cuda.current_stream()
+    mismatched = []
+    units = {}
+    h = h0
+    nxt = pool.acquire(timeout=60)
+    units[0] = (nxt, st.load(masters[0], nxt["param"], nxt["ready"]))
+    for i in range(L):
+        if i + 1 < L:  # prefetch layer i+1 before layer i's forward
+            u = pool.acquire(timeout=60)
+            units[i + 1] = (u, st.load(masters[i + 1], u["param"], u["ready"]))
+        unit, done = units.pop(i)
+        comp.wait_event(done)
+        ref = masters[i].to(dev, non_blocking=False).to(torch.bfloat16)
+        if not torch.equal(unit["param"][:N].view(torch.int16), ref.view(torch.int16)):
+            mismatched.append(i)
+        if i in (0, L - 1):
+            sl = slice(N - 4_000_000, N)
+            assert np.array_equal(bits16(unit["param"][sl]), oracle.cast_f32_bf16(masters[i].numpy()[sl])), i
+        bind(unit["param"])
+        h = fwd(h)
+        ev = torch.cuda.Event()
+        ev.record(comp)
+        unit["ready"] = ev
+        pool.release(unit)
+    assert not mismatched, f"units differ from the cast of their master: {mismatched}"
+    # reference: the same 32 forwards with weights cast by torch
+    r = h0
+    for i in range(L):
+        bind(masters[i].to(dev).to(torch.bfloat16))
+        r = fwd(r)
+    torch.cuda.synchronize()
+    assert torch.equal(h.view(torch.int16), r.view(torch.int16))

@@ -4,6 +4,7 @@
  * Two shared libraries implement this header:
  *   libsf_hip.so  device kernels, copies and pinned host memory (HIP, gfx950)
  *   libsf_cpu.so  the host AdamW used by LayerAdam (C++, AVX-512 + OpenMP)
+ *                 and the storage offload engine (C++, worker threads)
  *
  * Conventions shared by every entry point:
  *   - Plain pointers and sizes only; no framework types cross this boundary.
@@ -37,7 +38,10 @@ typedef void* sf_stream_t;
 #define SF_EDTYPE 9003      /* dtype combination not supported */
 #define SF_ENOOPT 9004      /* unknown optimizer id */
 #define SF_EOVERLAP 9005    /* source and destination ranges overlap */
+#define SF_ENOREQ 9006      /* unknown or already released I/O ticket */
+#define SF_EALIGN 9007      /* O_DIRECT transfer not aligned to SF_IO_ALIGN */
 #define SF_EDMA_BASE 10000  /* + (hsa_status_t & 0xFFF): a ROCr DMA call failed */
+#define SF_EIO_BASE 20000   /* + errno: a file operation failed */
 
 /* Maximum number of segments one segment-table call accepts. */
 #define SF_MAX_SEGS 64
@@ -302,6 +306,72 @@ int sf_adam_update_rows(int optimizer_id, size_t step, float lr, float beta1,
 int sf_cpu_set_threads(int nthreads);
 /* 1 if the AVX-512 path is used on this host, 0 for the portable path. */
 int sf_cpu_has_avx512(void);
+
+/* ---------------------------------------------------------------------
+ * Storage offload engine (libsf_cpu.so)
+ *
+ * Moves host buffers to and from files: checkpointed activations (through
+ * pinned bounce slots) and LayerAdam moments.  Replaces the reference's two
+ * storage back ends, neither of which exists for ROCm:
+ *   kvikio CuFile raw_write_async / raw_read_async (GPUDirect Storage;
+ *     sliding_checkpoint.py:133-202)
+ *   tensornvme DiskOffloader async_write / async_read / sync_*_events
+ *     (optimizer/layer_adam/layer_adam.py:89-103, 197-244)
+ * A request is cut into chunk_bytes pieces moved by n_threads workers with
+ * pread/pwrite.  Files are opened with O_DIRECT where the file system allows
+ * it; then the buffer address, the size and the file offset of a request
+ * must be multiples of SF_IO_ALIGN (SF_EALIGN otherwise).  Pinned host
+ * memory from hipHostMalloc cannot be pinned again by the kernel for direct
+ * I/O; chunks of such buffers are copied through a per-worker staging buffer.
+ * ------------------------------------------------------------------- */
+
+#define SF_IO_READ 0
+#define SF_IO_WRITE 1
+#define SF_IO_ALIGN 4096
+
+typedef struct sf_io sf_io;
+
+/* Start an engine with n_threads workers (1..256); chunk_bytes 0 selects
+ * 8 MiB, other values are rounded up to SF_IO_ALIGN. */
+int sf_io_create(int n_threads, size_t chunk_bytes, sf_io** out);
+/* Finish every queued request, stop the workers and free the engine. */
+int sf_io_destroy(sf_io* io);
+
+/* Open (creating) a file for reading and writing.  direct = 1 asks for
+ * O_DIRECT; where the file system refuses it the file is opened buffered and
+ * *direct_out (if non-null) is 0.  unlink_now = 1 removes the name at once,
+ * so the space is returned when the descriptor is closed or the process
+ * ends.  (kvikio.CuFile(path, "w"/"r"), sliding_checkpoint.py:148, 179;
+ * DiskOffloader(dir, ...), layer_adam.py:98.) */
+int sf_io_open(const char* path, int direct, int unlink_now, int* fd,
+               int* direct_out);
+/* Extend the file to at least `bytes` (unwritten ranges read as zeros). */
+int sf_io_reserve(int fd, uint64_t bytes);
+int sf_io_close(int fd);
+
+/* Queue a read (SF_IO_READ: file -> buf) or write (SF_IO_WRITE: buf -> file)
+ * of `bytes` at file `offset`; *ticket names the request.  The buffer must
+ * stay valid until the request completes.  (raw_write_async /
+ * raw_read_async, sliding_checkpoint.py:149, 181; async_write / async_read,
+ * layer_adam.py:205-207, 216-218.) */
+int sf_io_submit(sf_io* io, int fd, int op, void* buf, size_t bytes,
+                 uint64_t offset, uint64_t* ticket);
+/* Non-blocking: *done = 1 once the request completed, and then the return
+ * value is its status (0, or SF_EIO_BASE + errno of the first failed chunk).
+ * The ticket stays valid. */
+int sf_io_query(sf_io* io, uint64_t ticket, int* done);
+/* Block until the request completed, release the ticket and return its
+ * status; submit_ns / done_ns (if non-null) receive its CLOCK_MONOTONIC
+ * submit and completion times.  (check_bytes_done / sync_*_events,
+ * sliding_checkpoint.py:177, 190; layer_adam.py:227, 236.) */
+int sf_io_wait(sf_io* io, uint64_t ticket, uint64_t* submit_ns,
+               uint64_t* done_ns);
+/* Bytes read and written by completed requests, the time during which at
+ * least one request was in flight (ns), and the bytes that went through a
+ * worker's staging buffer because the kernel could not pin the caller's
+ * pages for direct I/O (memory from hipHostMalloc). */
+int sf_io_stats(sf_io* io, uint64_t* bytes_read, uint64_t* bytes_written,
+                uint64_t* busy_ns, uint64_t* bytes_staged);
 
 #ifdef __cplusplus
 }

@@ -210,6 +210,10 @@ class LayerAdamOracle:
         self.groups.append({"params": list(params), "step": 0, "m": m, "v": v, "views": views})
         return len(self.groups) - 1
 
+    def moments(self, idx: int):
+        """The layer's flat (exp_avg, exp_avg_sq)."""
+        return self.groups[idx]["m"], self.groups[idx]["v"]
+
     def step_layer(self, idx: int, grads: Sequence[np.ndarray]) -> None:
         """grads: per-parameter arrays, float32 or bf16 bit patterns (uint16)."""
         grp = self.groups[idx]

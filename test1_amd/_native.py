@@ -29,6 +29,10 @@ SF_DTYPE_F32 = 0
 SF_DTYPE_BF16 = 1
 SF_DTYPE_F16 = 2
 SF_MAX_SEGS = 64
+SF_IO_READ = 0
+SF_IO_WRITE = 1
+SF_IO_ALIGN = 4096
+SF_EALIGN = 9007
 
 
 class SfSeg(ctypes.Structure):
@@ -92,6 +96,16 @@ CPU_SIGNATURES = {
     "sf_adam_update_rows": [_i, _sz, _f, _f, _f, _f, _f, _i, _vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _sz, _i],
     "sf_cpu_set_threads": [_i],
     "sf_cpu_has_avx512": [],
+    "sf_io_create": [_i, _sz, ctypes.POINTER(_vp)],
+    "sf_io_destroy": [_vp],
+    "sf_io_open": [ctypes.c_char_p, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)],
+    "sf_io_reserve": [_i, ctypes.c_uint64],
+    "sf_io_close": [_i],
+    "sf_io_submit": [_vp, _i, _i, _vp, _sz, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)],
+    "sf_io_query": [_vp, ctypes.c_uint64, ctypes.POINTER(_i)],
+    "sf_io_wait": [_vp, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
+    "sf_io_stats": [_vp, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
+                    ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
 }
 
 _lock = threading.Lock()

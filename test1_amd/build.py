@@ -6,7 +6,8 @@ libsf_hip.so: hipcc for gfx950.  Packed-fp32 instruction selection is
 disabled (``-target-feature -packed-fp32-ops``); the host pass of hipcc
 warns that it does not know the feature, which is expected.
 libsf_cpu.so: g++ with OpenMP; AVX-512 is selected per function at run time,
-and -ffp-contract=off keeps every scalar operation a single rounding.
+and -ffp-contract=off keeps every scalar operation a single rounding.  The
+storage offload engine (worker threads, pread/pwrite) is in the same library.
 """
 
 from __future__ import annotations
@@ -56,7 +57,8 @@ def build_cpu(verbose: bool = False) -> str:
     out = os.path.join(LIB, "libsf_cpu.so")
     tmp = _atomic_out(out)
     _run([CXX, "-O3", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off", "-Wall",
-          "-I", INCLUDE, "-o", tmp, os.path.join(CSRC, "sf_cpu_adam.cpp")], verbose)
+          "-I", INCLUDE, "-o", tmp, os.path.join(CSRC, "sf_cpu_adam.cpp"), os.path.join(CSRC, "sf_io.cpp"),
+          "-pthread"], verbose)
     os.replace(tmp, out)
     return out
 

@@ -280,8 +280,19 @@ const char* sf_error_string(int status) {
         case SF_EINVAL: return "sf: invalid argument (null pointer, bad size or enum)";
         case SF_EDTYPE: return "sf: dtype combination not supported";
         case SF_ENOOPT: return "sf: unknown optimizer id";
-        default: return "sf: unknown status";
+        case SF_ENOREQ: return "sf: unknown or already released I/O ticket";
+        case SF_EALIGN: return "sf: O_DIRECT transfer: buffer, size and offset must be multiples of SF_IO_ALIGN";
+        default: break;
     }
+    if (status > SF_EIO_BASE && status < SF_EIO_BASE + 4096) {
+        // strerror_r (GNU) may return a static string or fill the buffer.
+        static thread_local char buf[160];
+        char msg[128];
+        const char* e = strerror_r(status - SF_EIO_BASE, msg, sizeof msg);
+        snprintf(buf, sizeof buf, "sf: file I/O failed: %s", e);
+        return buf;
+    }
+    return "sf: unknown status";
 }
 
 int sf_abi_version(void) { return 1; }

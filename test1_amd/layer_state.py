@@ -406,6 +406,23 @@ class PriorityUpdateExecutor:
             self._thread.join()
 
 
+class _UpdateReady:
+    """``query`` is true once the gradients have landed and the moments are
+    in memory; ``synchronize`` waits for the gradients only (the update reads
+    moments that are still on storage itself), so an executor that waits for
+    its oldest task never waits on a read that needs a buffer held by
+    another queued unit."""
+
+    def __init__(self, grads_ready, optimizer, unit: int):
+        self.grads_ready, self.optimizer, self.unit = grads_ready, optimizer, unit
+
+    def query(self) -> bool:
+        return self.grads_ready.query() and self.optimizer.states_ready(self.unit)
+
+    def synchronize(self) -> None:
+        self.grads_ready.synchronize()
+
+
 class StreamingRuntime:
     """Objects shared by all units of one model: streams, pool, stager, grad
     ring, worker threads and the optional event trace."""
@@ -885,9 +902,20 @@ class LayerRuntimeState(nn.Module):
         # waited for; the caching allocator cannot hand them out before then.
         keep = grads if handle is not None else None
         del grads, pairs
+        ready = done if handle is None else kernels.DmaReady(handle)
         self._update_future = rt.update_executor.submit(rt.update_priority(self.layer_idx), self._do_update,
                                                         slot, done, missing, handle, keep, nbytes,
-                                                        ready=done if handle is None else kernels.DmaReady(handle))
+                                                        ready=self._update_ready(ready))
+
+    def _update_ready(self, grads_ready):
+        """Readiness of this unit's update: its gradients on the host and,
+        with optimizer moments on storage, the moments read back (whose read
+        is queued here, in the order the gradients land)."""
+        opt = self.layer_optimizer
+        if opt is None or getattr(opt, "offloader", None) is None:
+            return grads_ready
+        opt.prefetch_states(self.layer_idx, self.runtime.update_priority(self.layer_idx))
+        return _UpdateReady(grads_ready, opt, self.layer_idx)
 
     def wait_for_d2h(self, timeout: Optional[float] = None) -> None:
         """Wait until the gradient offload has been issued (and re-raise its
@@ -999,7 +1027,7 @@ class LayerRuntimeState(nn.Module):
         self._grads_offloaded = True
         self._bwd_compute_done = True
         self._update_future = rt.update_executor.submit(rt.update_priority(self.layer_idx), self._do_update_rows,
-                                                        done, ntok, ready=done)
+                                                        done, ntok, ready=self._update_ready(done))
 
     def _do_update_rows(self, d2h_done: torch.cuda.Event, ntok: int) -> bool:
         rt = self.runtime

@@ -17,6 +17,12 @@ Differences, all deliberate:
   * each instance owns its own native optimizer id (the reference always
     uses 0, layer_adam.py:59), so two instances in one process do not share
     or destroy each other's bias-correction state.
+  * NVMe offload (``nvme_offload_fraction > 0``) keeps the reference's
+    choice of moments (exp_avg, plus exp_avg_sq above 0.5) but stores them
+    through the native storage engine (``StateOffloader``) instead of
+    tensornvme, with ``nvme_buffers`` host buffers as a write-back cache;
+    callers that update out of order name the next units with
+    ``prefetch_states``.
 """
 
 from __future__ import annotations
@@ -29,6 +35,7 @@ from typing import Any, DefaultDict, Dict, Iterable, Optional
 import torch
 
 from . import cpu_adam as _cpu_adam
+from .state_offload import StateOffloader
 
 
 class LayerAdam:
@@ -49,6 +56,7 @@ class LayerAdam:
         nvme_offload_fraction: float = 0.0,
         offload_dir: str = "/NVME1",
         prefetch: bool = True,
+        nvme_buffers: int = 4,
     ):
         self.defaults = dict(lr=lr, bias_correction=bias_correction, betas=betas, eps=eps,
                              weight_decay=weight_decay, adamw_mode=adamw_mode)
@@ -70,16 +78,28 @@ class LayerAdam:
         self.pin_memory = nvme_offload_fraction > 0.0
         self.exp_avg_flat: "OrderedDict[int, torch.Tensor]" = OrderedDict()
         self.exp_avg_sq_flat: "OrderedDict[int, torch.Tensor]" = OrderedDict()
+        # Moments offloaded to storage: exp_avg when the fraction is > 0, and
+        # exp_avg_sq too when it is > 0.5 (reference layer_adam.py:209-218).
+        self._offloaded = ()
+        self._hinted = False
         if nvme_offload_fraction > 0.0:
-            # NVMe state offload is not part of this build; the reference needs
-            # tensornvme for it (layer_adam.py:89-98) and raises the same way.
-            raise ModuleNotFoundError("Please install tensornvme to use NVMeOptimizer")
-        self.offload_dir = None
-        self.offloader = None
+            if offload_dir is None:
+                raise ValueError("offload_dir cannot be None")
+            self._offloaded = ("exp_avg", "exp_avg_sq") if nvme_offload_fraction > 0.5 else ("exp_avg",)
+            self.offload_dir = offload_dir
+            self.offloader = StateOffloader(offload_dir, len(self._offloaded), n_buffers=nvme_buffers)
+        else:
+            self.offload_dir = None
+            self.offloader = None
 
     def __del__(self):
         try:
             self.cpu_adam.destroy_adam(self.optimizer_id)
+        except Exception:
+            pass
+        try:
+            if self.offloader is not None:
+                self.offloader.close()
         except Exception:
             pass
 
@@ -105,16 +125,75 @@ class LayerAdam:
         self._groups_by_layer[layer_idx] = group
         numel = sum(p.numel() for p in params)
         state_type = torch.float32 if self.fp32_optimizer_state else params[0].dtype
-        self.exp_avg_flat[layer_idx] = torch.zeros(numel, dtype=state_type)
-        self.exp_avg_sq_flat[layer_idx] = torch.zeros(numel, dtype=state_type)
+        if self._offloaded and state_type != torch.float32:
+            raise ValueError("LayerAdam: NVMe offload keeps fp32 moments")
+        # Offloaded moments have no host tensor between steps (the
+        # reference frees their storage after the write, layer_adam.py:205-207).
+        for name, flat in (("exp_avg", self.exp_avg_flat), ("exp_avg_sq", self.exp_avg_sq_flat)):
+            flat[layer_idx] = (torch.empty(0, dtype=state_type) if name in self._offloaded
+                               else torch.zeros(numel, dtype=state_type))
+        if self._offloaded:
+            self.offloader.register(layer_idx, numel)
+        self._bind_states(layer_idx)
+        return layer_idx
+
+    def _bind_states(self, layer_idx: int) -> None:
+        """Point ``state[p]`` at the unit's flat moments (empty views for
+        moments that are on storage)."""
         off = 0
-        for p in params:
+        m_flat, v_flat = self.exp_avg_flat[layer_idx], self.exp_avg_sq_flat[layer_idx]
+        for p in self._group(layer_idx)["params"]:
             n = p.numel()
             st = self.state[p]
-            st["exp_avg"] = self.exp_avg_flat[layer_idx][off:off + n].view(p.shape)
-            st["exp_avg_sq"] = self.exp_avg_sq_flat[layer_idx][off:off + n].view(p.shape)
+            for name, flat in (("exp_avg", m_flat), ("exp_avg_sq", v_flat)):
+                st[name] = flat[off:off + n].view(p.shape) if flat.numel() else flat
             off += n
-        return layer_idx
+
+    # ------------------------------------------------------------------
+    # Storage offload (reference layer_adam.py:197-244)
+    def prefetch_states(self, layer_idx: int, priority: float = 0.0) -> None:
+        """Start reading ``layer_idx``'s moments from storage (not in the
+        reference, whose ``_pre_step`` always prefetches ``layer_idx - 1``):
+        a caller that knows its update order names the units itself, after
+        which steps no longer guess."""
+        if self.offloader is not None:
+            self._hinted = True
+            self.offloader.prefetch(layer_idx, priority)
+
+    def states_ready(self, layer_idx: int) -> bool:
+        """True if a step of ``layer_idx`` would not wait for storage."""
+        return self.offloader is None or self.offloader.ready(layer_idx)
+
+    def _pre_step(self, layer_idx: int) -> None:
+        if self.offloader is None:
+            return
+        if self.prefetch and not self._hinted:
+            # the reference's order: updates run in descending unit order
+            units = self.offloader.units()
+            prev = layer_idx - 1 if layer_idx - 1 in self._groups_by_layer else max(units)
+            if prev != layer_idx:
+                self.offloader.prefetch(prev, 0.0)
+        moments = self.offloader.acquire(layer_idx)
+        for name, t in zip(self._offloaded, moments):
+            (self.exp_avg_flat if name == "exp_avg" else self.exp_avg_sq_flat)[layer_idx] = t
+        self._bind_states(layer_idx)
+
+    def _post_step(self, layer_idx: int) -> None:
+        if self.offloader is None:
+            return
+        for name in self._offloaded:
+            (self.exp_avg_flat if name == "exp_avg" else self.exp_avg_sq_flat)[layer_idx] = torch.empty(0)
+        self._bind_states(layer_idx)
+        self.offloader.release(layer_idx)
+
+    def layer_states(self, layer_idx: int):
+        """Copies of ``layer_idx``'s (exp_avg, exp_avg_sq), from storage when
+        they are offloaded (not in the reference)."""
+        if self.offloader is None:
+            return self.exp_avg_flat[layer_idx].clone(), self.exp_avg_sq_flat[layer_idx].clone()
+        moments = dict(zip(self._offloaded, self.offloader.read_back(layer_idx)))
+        return (moments.get("exp_avg", self.exp_avg_flat[layer_idx].clone()),
+                moments.get("exp_avg_sq", self.exp_avg_sq_flat[layer_idx].clone()))
 
     def torch_adam_update(self, data, grad, exp_avg, exp_avg_sq, lr, beta1, beta2, eps,
                           weight_decay, bias_correction1, bias_correction2):
@@ -133,6 +212,9 @@ class LayerAdam:
     def _groups_to_update(self, layer_idx: Optional[int]):
         if layer_idx is not None:
             return [self._group(layer_idx)]
+        if self.offloader is not None:
+            # reference layer_adam.py:289-290
+            raise RuntimeError("LayerAdam: with NVMe offload, step one layer at a time")
         return list(self.param_groups)
 
     def _update_param(self, group: dict, p: torch.Tensor, grad: torch.Tensor,
@@ -155,12 +237,17 @@ class LayerAdam:
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
-        for group in self._groups_to_update(layer_idx):
-            group["step"] += 1
-            for p in group["params"]:
-                if p.grad is None:
-                    continue
-                self._update_param(group, p, p.grad.data)
+        groups = self._groups_to_update(layer_idx)
+        self._pre_step(layer_idx)
+        try:
+            for group in groups:
+                group["step"] += 1
+                for p in group["params"]:
+                    if p.grad is None:
+                        continue
+                    self._update_param(group, p, p.grad.data)
+        finally:
+            self._post_step(layer_idx)
         return loss
 
     @torch.no_grad()
@@ -180,15 +267,20 @@ class LayerAdam:
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
-        for group in self._groups_to_update(layer_idx):
-            group["step"] += 1
-            for p in group["params"]:
-                grad = grad_views.get(p) if grad_views else None
-                if grad is None:
-                    print(f"Warning: no gradient view for a parameter of shape {tuple(p.shape)}; skipped")
-                    continue
-                self._update_param(group, p, grad, None if param_views is None else param_views[p],
-                                   None if bf16_views is None else bf16_views[p])
+        groups = self._groups_to_update(layer_idx)
+        self._pre_step(layer_idx)
+        try:
+            for group in groups:
+                group["step"] += 1
+                for p in group["params"]:
+                    grad = grad_views.get(p) if grad_views else None
+                    if grad is None:
+                        print(f"Warning: no gradient view for a parameter of shape {tuple(p.shape)}; skipped")
+                        continue
+                    self._update_param(group, p, grad, None if param_views is None else param_views[p],
+                                       None if bf16_views is None else bf16_views[p])
+        finally:
+            self._post_step(layer_idx)
         return loss
 
     @torch.no_grad()
@@ -201,15 +293,19 @@ class LayerAdam:
         group = self._group(layer_idx)
         if len(group["params"]) != 1:
             raise ValueError("step_rows: the unit must hold exactly one parameter")
-        group["step"] += 1
-        p = group["params"][0]
-        st = self.state[p]
-        beta1, beta2 = group["betas"]
-        shape = param_view.shape
-        self.cpu_adam.adam_update_rows(self.optimizer_id, group["step"], group["lr"], beta1, beta2, group["eps"],
-                                       group["weight_decay"], group["bias_correction"], param_view,
-                                       st["exp_avg"].view(shape), st["exp_avg_sq"].view(shape), row_slot, rows,
-                                       params_bf16=bf16_view)
+        self._pre_step(layer_idx)
+        try:
+            group["step"] += 1
+            p = group["params"][0]
+            st = self.state[p]
+            beta1, beta2 = group["betas"]
+            shape = param_view.shape
+            self.cpu_adam.adam_update_rows(self.optimizer_id, group["step"], group["lr"], beta1, beta2,
+                                           group["eps"], group["weight_decay"], group["bias_correction"],
+                                           param_view, st["exp_avg"].view(shape), st["exp_avg_sq"].view(shape),
+                                           row_slot, rows, params_bf16=bf16_view)
+        finally:
+            self._post_step(layer_idx)
 
     def update_learning_rate(self, new_lr):
         """Set the learning rate of every group (reference layer_adam.py:427-442)."""

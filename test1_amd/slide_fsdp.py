@@ -61,7 +61,7 @@ from .fused_ce import chunked_linear_cross_entropy
 from .layer_state import LayerRuntimeState, StreamingRuntime
 from .optimizer import LayerAdam
 from .pinned import pinned_empty
-from .sliding_checkpoint import ActivationRing, SlidingCheckpoint
+from .sliding_checkpoint import ActivationRing, SlidingCheckpoint, StorageSpill
 
 
 try:  # transformers >= 5: masks are built by a module-level function
@@ -188,8 +188,6 @@ class SlideFSDP(nn.Module):
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
         if config.dtype != torch.bfloat16:
             raise NotImplementedError("SlideFSDP stages parameters as bfloat16; dtype=float16 is not supported")
-        if config.ac_offload_mode == "nvme":
-            raise NotImplementedError("ac_offload_mode='nvme' (GPUDirect Storage) is not supported")
         if not config.enable_activation_checkpoint:
             raise NotImplementedError(
                 "enable_activation_checkpoint=False would keep every unit's weights saved for backward "
@@ -235,6 +233,18 @@ class SlideFSDP(nn.Module):
         self.layer_tensors: Optional[List[List[torch.Tensor]]] = None
         self.position_embeddings = None
         self._act_ring = ActivationRing(self.device)
+        self._spill: Optional[StorageSpill] = None
+        self._act_paths: Optional[List[List[str]]] = None
+        if config.ac_offload_mode == "nvme":
+            # Checkpoint inputs on local storage, one file per (layer, tensor)
+            # under ac_offload_dir.  The reference passes no file_paths in this
+            # mode (slide_fsdp.py:592-600), so its SlidingCheckpoint asserts;
+            # here they are made, and no per-layer pinned slots are allocated.
+            os.makedirs(config.ac_offload_dir, exist_ok=True)
+            tag = f"{os.getpid()}-{id(self)}"
+            self._act_paths = [[os.path.join(config.ac_offload_dir, f"act-{tag}-{i}-{c}.bin") for c in range(4)]
+                               for i in range(self.num_decoder_layers)]
+            self._spill = StorageSpill(n_slots=4)
         self._print_model_info()
 
     # ------------------------------------------------------------------
@@ -477,7 +487,7 @@ class SlideFSDP(nn.Module):
         """One training step (reference slide_fsdp.py:507-640)."""
         batch_size, seq_length = input_ids.shape
         hidden_size = self.model_config.hidden_size
-        if self.config.ac_offload_mode != "none":
+        if self.config.ac_offload_mode == "cpu":
             if self.layer_tensors is None or self.layer_tensors[0][0].shape != (batch_size, seq_length, hidden_size):
                 self._allocate_activation_tensors(batch_size, seq_length, hidden_size)
         self._act_ring.reset()
@@ -528,7 +538,9 @@ class SlideFSDP(nn.Module):
 
             ckpt_kw = dict(use_reentrant=False, preserve_rng_state=self._layer_uses_rng)
             if self.config.ac_offload_mode != "none":
-                with SlidingCheckpoint(layer_idx=i + 1, layer_tensors=self.layer_tensors, is_last_layer=is_last_decoder,
+                with SlidingCheckpoint(layer_idx=i + 1, layer_tensors=self.layer_tensors,
+                                       gds_offload=self._spill is not None, file_paths=self._act_paths,
+                                       spill=self._spill, is_last_layer=is_last_decoder,
                                        no_mask=attention_mask is None, device=str(self.device),
                                        prefetch_ring=self._act_ring, trace=trace,
                                        max_workgroups=self.runtime.d2h_workgroups,
@@ -633,6 +645,11 @@ class SlideFSDP(nn.Module):
                 h.remove()
             self._hook_handles = []
             self.runtime.shutdown()
+            if self._spill is not None:
+                self._spill.close()
+                self._spill = None
+            if self.layer_optimizer.offloader is not None:
+                self.layer_optimizer.offloader.flush()
 
     def __del__(self):
         rt = getattr(self, "runtime", None)

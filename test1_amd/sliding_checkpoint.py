@@ -27,18 +27,33 @@ What is different, and why:
     blocking copies;
   * 16-bit tensors are packed into their slot by a kernel with a capped grid
     instead of the runtime's full-device copy kernel.
-  * NVMe/GPUDirect mode (``gds_offload=True``) is not part of this build.
+
+Storage mode (``gds_offload=True``, reference sliding_checkpoint.py:133-202):
+the reference writes each checkpoint input from device memory straight to
+``file_paths[layer][counter]`` with kvikio (GPUDirect Storage) and reads layer
+j-1 back into a new device buffer when layer j is first unpacked.  This
+platform has no GPU-to-storage DMA, so a ``StorageSpill`` stages through a few
+pinned bounce slots instead: pack copies the tensor into a slot on the
+offload stream, and a worker thread writes the slot to the file once the copy
+has landed; the prefetch of layer j-1 waits for that layer's writes, reads
+each file into a slot and copies it to the device on the prefetch stream.
+The consumer waits for the prefetch on its stream, as in host mode.  Files
+are opened through the native storage engine (O_DIRECT where available) and
+unlinked at once, so no file outlives the process.
 """
 
 from __future__ import annotations
 
+import threading
+import time
 from collections import deque
-from typing import Any, List, Optional, Tuple
+from concurrent.futures import Future, ThreadPoolExecutor
+from typing import Any, Dict, List, Optional, Tuple
 
 import torch
 from torch.autograd.graph import saved_tensors_hooks
 
-from . import kernels
+from . import kernels, storage
 from .pinned import pinned_empty
 
 _offload_streams = {}
@@ -47,6 +62,8 @@ _offload_streams = {}
 fifo_prefetch_queue: deque = deque()
 # Number of tensors packed per (layer_tensors, layer), for instances without a ring.
 _packed_counts = {}
+# Storage mode: (path, shape, dtype) of each tensor packed per (file_paths, layer).
+_packed_meta = {}
 
 
 def offload_stream(device) -> torch.cuda.Stream:
@@ -75,6 +92,7 @@ class ActivationRing:
         self.next = 0
         self.fifo: deque = deque()
         self.packed_counts = {}
+        self.packed_meta = {}
 
     def buffers_like(self, host_tensors: List[torch.Tensor]) -> List[torch.Tensor]:
         i = self.next
@@ -89,6 +107,167 @@ class ActivationRing:
 
     def reset(self) -> None:
         self.fifo.clear()
+
+
+class _OnStorage:
+    """What pack returns for a tensor written to storage."""
+
+    __slots__ = ("path", "shape", "dtype")
+
+    def __init__(self, path: str, shape, dtype):
+        self.path, self.shape, self.dtype = path, shape, dtype
+
+
+class _BounceSlot:
+    __slots__ = ("buf", "held", "pending")
+
+    def __init__(self, nbytes: int):
+        self.buf = pinned_empty((storage.align_up(nbytes),), torch.uint8)
+        if self.buf.data_ptr() % storage.ALIGN:
+            raise RuntimeError("StorageSpill: pinned slot not aligned for direct I/O")
+        self.held = False
+        self.pending: List[Any] = []   # waitables that must finish before reuse
+
+    def idle(self) -> bool:
+        for w in self.pending:
+            if isinstance(w, Future):
+                if not w.done() or (w.exception() is None and not w.result().done()):
+                    return False
+            elif not w.query():
+                return False
+        self.pending = []
+        return True
+
+
+class StorageSpill:
+    """Checkpoint inputs on local storage: pinned bounce slots, one file per
+    (layer, tensor) path, and one worker thread that turns finished device
+    copies into file writes and file reads into device copies (storage mode
+    of ``SlidingCheckpoint``)."""
+
+    def __init__(self, n_slots: int = 4, engine: Optional[storage.IoEngine] = None, direct: bool = True):
+        if n_slots < 2:
+            raise ValueError("StorageSpill: at least 2 bounce slots")
+        self.engine = engine or storage.default_engine()
+        self.direct = direct
+        self.n_slots = n_slots
+        self._slots: List[_BounceSlot] = []
+        self._files: Dict[str, storage.OffloadFile] = {}
+        self._writes: Dict[str, Future] = {}
+        self._lock = threading.Lock()
+        self._worker = ThreadPoolExecutor(max_workers=1, thread_name_prefix="act-spill")
+        self.bytes_written = 0
+        self.bytes_read = 0
+        self.slot_wait_s = 0.0
+
+    def _file(self, path: str) -> storage.OffloadFile:
+        with self._lock:
+            f = self._files.get(path)
+            if f is None:
+                f = self.engine.open(path, direct=self.direct, unlink=True)
+                self._files[path] = f
+            return f
+
+    def take_slot(self, nbytes: int) -> _BounceSlot:
+        """A bounce slot of at least ``nbytes``, waiting for one to drain."""
+        t0 = time.perf_counter()
+        while True:
+            with self._lock:
+                for sl in self._slots:
+                    if not sl.held and sl.idle():
+                        if sl.buf.numel() < nbytes:
+                            sl.buf = _BounceSlot(nbytes).buf
+                        sl.held = True
+                        break
+                else:
+                    sl = None
+                    if len(self._slots) < self.n_slots:
+                        sl = _BounceSlot(nbytes)
+                        sl.held = True
+                        self._slots.append(sl)
+            if sl is not None:
+                self.slot_wait_s += time.perf_counter() - t0
+                return sl
+            time.sleep(200e-6)
+
+    def write_after(self, path: str, slot: _BounceSlot, copied: torch.cuda.Event, nbytes: int) -> None:
+        """Write ``nbytes`` of ``slot`` to ``path`` once ``copied`` (the
+        device-to-slot copy) has completed; the slot is free after the write."""
+        f = self._file(path)
+        padded = storage.align_up(nbytes)
+
+        def task():
+            copied.synchronize()
+            return f.write(slot.buf, 0, padded)
+
+        fut = self._worker.submit(task)
+        with self._lock:
+            self._writes[path] = fut
+            slot.pending = [fut]
+            slot.held = False
+        self.bytes_written += padded
+
+    def prefetch(self, items: List[Tuple[str, torch.Tensor]], after: torch.cuda.Event,
+                 stream: torch.cuda.Stream) -> Future:
+        """Read each ``(path, device_buffer)`` back into its buffer: on the
+        worker, wait for the file's write, read it into a slot, then copy the
+        slot to the buffer on ``stream`` after ``after``.  The future gives
+        the event recorded after the last copy."""
+
+        def task():
+            with torch.cuda.device(stream.device):
+                return copy_back()
+
+        def copy_back():
+            ev = None
+            for path, dst in items:
+                nbytes = dst.numel() * dst.element_size()
+                padded = storage.align_up(nbytes)
+                w = self._writes.get(path)
+                if w is None:
+                    raise RuntimeError(f"StorageSpill: {path} was never written")
+                w.result().wait()
+                slot = self.take_slot(padded)
+                try:
+                    self._file(path).read(slot.buf, 0, padded).wait()
+                    stream.wait_event(after)
+                    kernels.memcpy_async(dst.view(-1).view(torch.uint8), slot.buf, stream, nbytes=nbytes)
+                    ev = torch.cuda.Event()
+                    ev.record(stream)
+                finally:
+                    with self._lock:
+                        if ev is not None:
+                            slot.pending = [ev]
+                        slot.held = False
+                self.bytes_read += padded
+            return ev
+
+        return self._worker.submit(task)
+
+    def flush(self) -> None:
+        """Wait for every queued write (re-raising its error)."""
+        for fut in list(self._writes.values()):
+            fut.result().wait()
+
+    def close(self) -> None:
+        self.flush()
+        self._worker.shutdown(wait=True)
+        for f in self._files.values():
+            f.close()
+        self._files.clear()
+        self._slots.clear()
+
+
+_default_spill: Optional[StorageSpill] = None
+
+
+def default_spill() -> StorageSpill:
+    """The process's spill for ``SlidingCheckpoint``s given none (the
+    reference keeps its storage-mode state in module globals too)."""
+    global _default_spill
+    if _default_spill is None:
+        _default_spill = StorageSpill()
+    return _default_spill
 
 
 class SlidingCheckpoint(saved_tensors_hooks):
@@ -110,11 +289,16 @@ class SlidingCheckpoint(saved_tensors_hooks):
         max_workgroups: int = 8,
         prefetch_stream: Optional[torch.cuda.Stream] = None,
         pack_fence=None,
+        spill: Optional[StorageSpill] = None,
     ):
         if gds_offload:
-            raise NotImplementedError("SlidingCheckpoint: NVMe (GPUDirect Storage) offload is not supported")
-        if layer_tensors is None:
+            if file_paths is None:
+                raise ValueError("SlidingCheckpoint: file_paths is required for storage offload")
+            self.spill = spill or default_spill()
+        elif layer_tensors is None:
             raise ValueError("SlidingCheckpoint: layer_tensors is required for host offload")
+        self.gds_offload = gds_offload
+        self.file_paths = file_paths
         self.layer_idx = layer_idx - 1  # decoder index; units count the embedding as 0
         self.device = device
         self.stream = stream or offload_stream(device)
@@ -128,7 +312,8 @@ class SlidingCheckpoint(saved_tensors_hooks):
         self.ring = prefetch_ring
         self.fifo = prefetch_ring.fifo if prefetch_ring is not None else fifo_prefetch_queue
         self._counts = prefetch_ring.packed_counts if prefetch_ring is not None else _packed_counts
-        self._key = id(layer_tensors)
+        self._meta = prefetch_ring.packed_meta if prefetch_ring is not None else _packed_meta
+        self._key = id(file_paths) if gds_offload else id(layer_tensors)
         self.pack_counter = 0
         self.unpack_counter = 0
         self.pre_pack_event = torch.cuda.Event()
@@ -150,15 +335,20 @@ class SlidingCheckpoint(saved_tensors_hooks):
                 return (tensor.device, tensor.cpu())
             if self.is_last_layer:
                 return (tensor.device, tensor)
-            slots = self.layer_tensors[self.layer_idx]
-            while len(slots) <= self.pack_counter:
-                slots.append(None)
-            slot = slots[self.pack_counter]
-            if slot is None or slot.shape != tensor.shape or slot.dtype != tensor.dtype:
-                # First use of this slot (the mask slot is created on demand)
-                # or a new batch shape: (re)allocate it, pinned and exact-size.
-                slot = pinned_empty(tensor.shape, tensor.dtype)
-                slots[self.pack_counter] = slot
+            nbytes = tensor.numel() * tensor.element_size()
+            if self.gds_offload:
+                bounce = self.spill.take_slot(nbytes)
+                slot = bounce.buf[:nbytes].view(tensor.dtype).view(tensor.shape)
+            else:
+                slots = self.layer_tensors[self.layer_idx]
+                while len(slots) <= self.pack_counter:
+                    slots.append(None)
+                slot = slots[self.pack_counter]
+                if slot is None or slot.shape != tensor.shape or slot.dtype != tensor.dtype:
+                    # First use of this slot (the mask slot is created on demand)
+                    # or a new batch shape: (re)allocate it, pinned and exact-size.
+                    slot = pinned_empty(tensor.shape, tensor.dtype)
+                    slots[self.pack_counter] = slot
             cur = torch.cuda.current_stream()
             if self.pack_counter == 0:
                 self.pre_pack_event.record(cur)
@@ -181,11 +371,20 @@ class SlidingCheckpoint(saved_tensors_hooks):
             src.record_stream(self.stream)
             self.pack_counter += 1
             self._counts[(self._key, self.layer_idx)] = self.pack_counter
+            if self.gds_offload:
+                path = self.file_paths[self.layer_idx][self.pack_counter - 1]
+                copied = torch.cuda.Event()
+                copied.record(self.stream)
+                self.spill.write_after(path, bounce, copied, nbytes)
+                meta = self._meta.setdefault((self._key, self.layer_idx), [])
+                del meta[self.pack_counter - 1:]
+                meta.append((path, tuple(tensor.shape), tensor.dtype))
+                return (tensor.device, _OnStorage(path, tuple(tensor.shape), tensor.dtype))
             return (tensor.device, slot)
 
         def unpack_hook(packed: Tuple[torch.device, Any]) -> torch.Tensor:
             device, tensor = packed
-            if tensor.size() == torch.Size([0]):
+            if isinstance(tensor, torch.Tensor) and tensor.size() == torch.Size([0]):
                 return torch.empty(tensor.shape, dtype=tensor.dtype, device=device)
             if not pin_memory:
                 return tensor.to(device, non_blocking=pin_memory)
@@ -193,7 +392,24 @@ class SlidingCheckpoint(saved_tensors_hooks):
             if self.unpack_counter == 0:
                 self.pre_unpack_event.record(cur)
                 nxt = self.layer_idx - 1
-                if nxt >= 0:
+                if nxt >= 0 and self.gds_offload:
+                    meta = self._meta.get((self._key, nxt), [])[: self._slots_used(nxt)]
+                    if meta:
+                        like = [torch.empty(shape, dtype=dt, device="meta") for _, shape, dt in meta]
+                        if self.ring is not None:
+                            bufs = self.ring.buffers_like(like)
+                        else:
+                            bufs = [torch.empty(shape, dtype=dt, device=self.device) for _, shape, dt in meta]
+                        ps = self.prefetch_stream
+                        fut = self.spill.prefetch([(path, b) for (path, _, _), b in zip(meta, bufs)],
+                                                  self.pre_unpack_event, ps)
+                        if self.ring is None:
+                            for b in bufs:
+                                b.record_stream(ps)
+                        self.fifo.append((bufs, fut))
+                        if self._trace is not None:
+                            self._trace("act_h2d", nxt + 1)
+                elif nxt >= 0:
                     host = self.layer_tensors[nxt][: self._slots_used(nxt)]
                     if self.ring is not None:
                         bufs = self.ring.buffers_like(host)
@@ -216,9 +432,13 @@ class SlidingCheckpoint(saved_tensors_hooks):
             if not self.fifo:
                 # Nothing was prefetched for this layer (e.g. a first-layer
                 # recompute outside the sliding order): synchronous fallback.
+                if isinstance(tensor, _OnStorage):
+                    raise RuntimeError("SlidingCheckpoint: a layer on storage was not prefetched")
                 return tensor.to(device, non_blocking=True)
             bufs, ev = self.fifo[0]
             if self.unpack_counter == 0:
+                if isinstance(ev, Future):
+                    ev = ev.result()
                 cur.wait_event(ev)
             result = bufs[self.unpack_counter]
             self.unpack_counter += 1

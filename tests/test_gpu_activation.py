@@ -7,64 +7,97 @@ import torch
 from torch.utils.checkpoint import checkpoint
 
 from test1_amd.pinned import pinned_empty
-from test1_amd.sliding_checkpoint import ActivationRing, SlidingCheckpoint
+from test1_amd.sliding_checkpoint import ActivationRing, SlidingCheckpoint, StorageSpill
 
 pytestmark = pytest.mark.gpu
 
 
-def run_layers(dev, L, shape, weights, offload, seen, use_ring=True):
+def run_layers(dev, L, shape, weights, offload, seen, use_ring=True, spill_dir=None, mask=None):
+    """``offload``: None (plain checkpointing), "host" (pinned slots) or
+    "storage" (files under ``spill_dir`` through a 3-slot StorageSpill)."""
     h = torch.randn(shape, generator=torch.Generator().manual_seed(0)).bfloat16().to(dev).requires_grad_(True)
-    slots = [[pinned_empty(shape, torch.bfloat16)] for _ in range(L)] if offload else None
+    slots = [[pinned_empty(shape, torch.bfloat16)] for _ in range(L)] if offload == "host" else None
+    paths = ([[f"{spill_dir}/act-{i}-{c}.bin" for c in range(4)] for i in range(L)]
+             if offload == "storage" else None)
+    spill = StorageSpill(n_slots=3) if offload == "storage" else None
     ring = ActivationRing(dev) if (offload and use_ring) else None
 
-    def layer_fn(x, w, i):
+    def layer_fn(x, w, i, m=None):
         seen.setdefault(i, []).append(x.detach().clone())
-        return torch.tanh(x) * w
+        y = torch.tanh(x) * w
+        return y if m is None else y.masked_fill(m, 0.0)
 
     x = h
     for i in range(L):
+        args = (x, weights[i], i) if mask is None else (x, weights[i], i, mask)
         if offload:
-            with SlidingCheckpoint(layer_idx=i + 1, layer_tensors=slots, is_last_layer=(i == L - 1),
-                                   no_mask=True, device=str(dev), prefetch_ring=ring):
-                x = checkpoint(layer_fn, x, weights[i], i, use_reentrant=False)
+            with SlidingCheckpoint(layer_idx=i + 1, layer_tensors=slots, gds_offload=offload == "storage",
+                                   file_paths=paths, is_last_layer=(i == L - 1), no_mask=mask is None,
+                                   device=str(dev), prefetch_ring=ring, spill=spill):
+                x = checkpoint(layer_fn, *args, use_reentrant=False)
         else:
-            x = checkpoint(layer_fn, x, weights[i], i, use_reentrant=False)
+            x = checkpoint(layer_fn, *args, use_reentrant=False)
     x.float().sum().backward()
     torch.cuda.synchronize()
+    if spill is not None:
+        spill.close()
     return [w.grad.clone() for w in weights], h.grad.clone(), slots
 
 
 @pytest.mark.parametrize("use_ring", [True, False])
-def test_round_trip_bit_exact_small(dev, use_ring):
+@pytest.mark.parametrize("mode", ["host", "storage"])
+def test_round_trip_bit_exact_small(dev, use_ring, mode, tmp_path):
     L, shape = 6, (2, 128, 256)
     ws = [torch.randn(shape[-1], generator=torch.Generator().manual_seed(10 + i)).bfloat16().to(dev).requires_grad_(True)
           for i in range(L)]
     seen = {}
-    g_off, hg_off, slots = run_layers(dev, L, shape, ws, True, seen, use_ring)
+    g_off, hg_off, slots = run_layers(dev, L, shape, ws, mode, seen, use_ring, spill_dir=str(tmp_path))
     for i in range(L):
         fwd, rec = seen[i]
         assert torch.equal(fwd.view(torch.int16), rec.view(torch.int16)), f"layer {i} input changed"
-        if i < L - 1:  # every layer but the last went through its host slot
+        if i < L - 1 and mode == "host":  # every layer but the last went through its host slot
             assert torch.equal(slots[i][0].view(torch.int16), fwd.cpu().view(torch.int16))
     for w in ws:
         w.grad = None
-    g_ref, hg_ref, _ = run_layers(dev, L, shape, ws, False, {})
+    g_ref, hg_ref, _ = run_layers(dev, L, shape, ws, None, {})
     for a, b in zip(g_off, g_ref):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     assert torch.equal(hg_off.view(torch.int16), hg_ref.view(torch.int16))
 
 
+def test_storage_two_tensors_per_layer(dev, tmp_path):
+    """Storage mode with a second, non-16-bit checkpoint input per layer (a
+    bool mask of an odd byte size, so files and slots are padded): inputs and
+    gradients equal plain checkpointing's."""
+    L, shape = 5, (3, 40, 72)
+    mask = (torch.rand(shape, generator=torch.Generator().manual_seed(4)) < 0.3).to(dev)
+    ws = [torch.randn(shape[-1], generator=torch.Generator().manual_seed(20 + i)).bfloat16().to(dev).requires_grad_(True)
+          for i in range(L)]
+    seen = {}
+    g_off, hg_off, _ = run_layers(dev, L, shape, ws, "storage", seen, spill_dir=str(tmp_path), mask=mask)
+    for i in range(L):
+        fwd, rec = seen[i]
+        assert torch.equal(fwd.view(torch.int16), rec.view(torch.int16)), f"layer {i} input changed"
+    for w in ws:
+        w.grad = None
+    g_ref, hg_ref, _ = run_layers(dev, L, shape, ws, None, {}, mask=mask)
+    for a, b in zip(g_off, g_ref):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(hg_off.view(torch.int16), hg_ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("mode", ["host", "storage"])
 @pytest.mark.parametrize("L,shape", [(32, (4, 1024, 4096)), (48, (2, 4096, 5120))],
                          ids=["llama3-8b", "qwen2.5-14b"])
-def test_round_trip_model_checkpoint_shapes(dev, L, shape):
-    """The models' checkpoints through the pinned slots and back, bit-exact:
-    32 layers of [4, 1024, 4096] bf16 (32 MiB each, Llama-3-8B at batch 4 x
-    1024) and 48 layers of [2, 4096, 5120] (80 MiB each, Qwen2.5-14B at batch
-    2 x 4096)."""
+def test_round_trip_model_checkpoint_shapes(dev, L, shape, mode, tmp_path):
+    """The models' checkpoints through the pinned slots (or through files on
+    local storage) and back, bit-exact: 32 layers of [4, 1024, 4096] bf16
+    (32 MiB each, Llama-3-8B at batch 4 x 1024) and 48 layers of
+    [2, 4096, 5120] (80 MiB each, Qwen2.5-14B at batch 2 x 4096)."""
     ws = [torch.full((shape[-1],), 1.0 + 1e-2 * i, dtype=torch.bfloat16, device=dev, requires_grad=True)
           for i in range(L)]
     seen = {}
-    run_layers(dev, L, shape, ws, True, seen)
+    run_layers(dev, L, shape, ws, mode, seen, spill_dir=str(tmp_path))
     for i in range(L):
         fwd, rec = seen[i]
         assert torch.equal(fwd.view(torch.int16), rec.view(torch.int16)), f"layer {i}"

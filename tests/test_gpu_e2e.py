@@ -87,19 +87,46 @@ def test_updates_match_oracle_bit_exact(dev, h2d_format, resident, d2h_engine, r
     host bf16 copy of every unit is the oracle cast of its master after each
     step, so both formats stage the same bits.  ``resident`` decoder layers
     keep their forward weights for the backward."""
+    check_updates_against_oracle(dev, arch, h2d_format, {}, dict(
+        resident_layers=resident, d2h_engine=d2h_engine, grad_ring_depth=ring, fused_cross_entropy=fused))
+
+
+# checkpoint offload mode, optimizer moments on storage (fraction), H2D format
+STORAGE_MODES = [("nvme", 0.0, "fp32"), ("cpu", 0.3, "fp32"), ("nvme", 0.8, "bf16")]
+
+
+def storage_config(tmp_path, ac_mode, fraction):
+    return dict(ac_offload_mode=ac_mode, ac_offload_dir=str(tmp_path / "ac"),
+                optimizer_nvme_offload_fraction=fraction, optimizer_offload_dir=str(tmp_path / "opt"))
+
+
+@pytest.mark.parametrize("ac_mode,fraction,h2d_format", STORAGE_MODES)
+def test_storage_offload_updates_match_oracle_bit_exact(dev, tmp_path, ac_mode, fraction, h2d_format):
+    """Checkpoint inputs on local storage (``ac_offload_mode="nvme"``) and/or
+    AdamW moments on local storage (``optimizer_nvme_offload_fraction``: the
+    first moment above 0, both above 0.5): the updates stay those of the
+    oracle AdamW, bit for bit, over 3 steps (2 moment buffers, so moments
+    are evicted and read back within every step)."""
+    check_updates_against_oracle(dev, "llama", h2d_format, storage_config(tmp_path, ac_mode, fraction), {},
+                                 nvme_buffers=2)
+
+
+def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, nvme_buffers=None):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model(arch)
-    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS),
-                   wait_timeout=120, h2d_format=h2d_format, resident_layers=resident, d2h_engine=d2h_engine,
-                   grad_ring_depth=ring, fused_cross_entropy=fused)
+    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS,
+                                          **cfg_kw),
+                   wait_timeout=120, h2d_format=h2d_format, **sf_kw)
+    if nvme_buffers is not None and sf.layer_optimizer.offloader is not None:
+        sf.layer_optimizer.offloader.n_buffers = nvme_buffers
     orc = oracle.LayerAdamOracle(lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
     ref_units = []
     for ps in units_of(model):
         arrs = [p.detach().numpy().copy() for p in ps]
         ref_units.append(arrs)
         orc.add_layer(arrs)
-    for ids in batches(3):
+    for ids in batches(steps):
         sf.runtime.capture = {}
         ids = ids.to(dev)
         sf(input_ids=ids, labels=ids)
@@ -127,6 +154,12 @@ def test_updates_match_oracle_bit_exact(dev, h2d_format, resident, d2h_engine, r
             if h2d_format == "bf16":
                 flat = np.concatenate([a.reshape(-1) for a in ref_units[u]])
                 assert np.array_equal(u16(sf.layer_states[u]._cpu_params_bf16), oracle.cast_f32_bf16(flat)), f"unit {u}"
+    opt = sf.layer_optimizer
+    for u in range(L + 2):
+        m, v = opt.layer_states(u)
+        om, ov = orc.moments(u)
+        assert np.array_equal(m.numpy().view(np.uint32), om.view(np.uint32)), f"unit {u} exp_avg"
+        assert np.array_equal(v.numpy().view(np.uint32), ov.view(np.uint32)), f"unit {u} exp_avg_sq"
     sf.close()
 
 
@@ -163,14 +196,27 @@ def reference_losses(model, steps_ids, dev):
 
 @pytest.mark.parametrize("h2d_format,resident,d2h_engine,ring,arch,fused", MODES)
 def test_loss_parity_with_non_offloaded_run(dev, h2d_format, resident, d2h_engine, ring, arch, fused):
+    check_loss_parity(dev, arch, fused, {}, dict(h2d_format=h2d_format, resident_layers=resident,
+                                                 d2h_engine=d2h_engine, grad_ring_depth=ring,
+                                                 fused_cross_entropy=fused))
+
+
+@pytest.mark.parametrize("ac_mode,fraction,h2d_format", STORAGE_MODES)
+def test_storage_offload_loss_parity(dev, tmp_path, ac_mode, fraction, h2d_format):
+    """The storage modes against the non-offloaded run: first-step gradients
+    (through checkpoints read back from files) and 10 losses."""
+    check_loss_parity(dev, "llama", False, storage_config(tmp_path, ac_mode, fraction), dict(h2d_format=h2d_format))
+
+
+def check_loss_parity(dev, arch, fused, cfg_kw, sf_kw):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model(arch)
     steps = batches(10)
     ref_losses, ref_grads = reference_losses(model, steps, dev)
-    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS),
-                   wait_timeout=120, h2d_format=h2d_format, resident_layers=resident, d2h_engine=d2h_engine,
-                   grad_ring_depth=ring, fused_cross_entropy=fused)
+    sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS,
+                                          **cfg_kw),
+                   wait_timeout=120, **sf_kw)
     losses = []
     for k, ids in enumerate(steps):
         if k == 0:

@@ -225,9 +225,14 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     t0 = time.time()
-    cfg = SlideFSDPConfig(device=dev, lr=1e-5, weight_decay=0.01, attention_implementation="sdpa")
+    cfg = SlideFSDPConfig(device=dev, lr=1e-5, weight_decay=0.01, attention_implementation="sdpa",
+                          ac_offload_mode=args.ac_offload,
+                          ac_offload_dir=os.path.join(args.offload_dir, "activations"),
+                          optimizer_nvme_offload_fraction=args.opt_nvme_fraction,
+                          optimizer_offload_dir=os.path.join(args.offload_dir, "optimizer"))
     sf = SlideFSDP(model, cfg, d2h_engine=d2h_engine, h2d_format=h2d_format, resident_layers=resident_layers,
                    fused_cross_entropy=args.fused_ce)
+    uses_storage = args.ac_offload == "nvme" or args.opt_nvme_fraction > 0
     log(f"[bench] SlideFSDP ({h2d_format} H2D, {sf.resident_layers} resident decoders, {d2h_engine} D2H) "
         f"ready in {time.time() - t0:.1f}s")
     B, S = w["batch"], w["seq"]
@@ -248,6 +253,7 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
         _k.dma_enable_timing(True)
     if timeline:
         rt.timeline = []
+    io0 = _storage_snapshot(sf) if uses_storage else None
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     losses = []
@@ -264,6 +270,15 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
             for t, th, what, unit in rt.timeline:
                 f.write(f"{(t - t_start) * 1e3:.3f} {th} {what} {unit}\n")
     log(f"[bench] timed {args.steps} steps in {elapsed:.2f}s, losses {losses}")
+    storage_stats = None
+    if uses_storage:
+        io1 = _storage_snapshot(sf)
+        storage_stats = {k: io1[k] - io0[k] for k in io1}
+        rd, wr, busy = storage_stats["bytes_read"], storage_stats["bytes_written"], storage_stats["busy_s"]
+        storage_stats.update({
+            "read_bytes_per_step": rd / args.steps, "write_bytes_per_step": wr / args.steps,
+            "busy_frac": busy / elapsed, "gbs_while_busy": (rd + wr) / busy / 1e9 if busy > 0 else None})
+        log(f"[bench] storage: {storage_stats}")
     r = {
         "elapsed": elapsed, "losses": losses, "tokens": B * S * args.steps,
         "cast": elapsed_stats(rt.stager.cast_timing), "ncast": len(rt.stager.cast_timing or []),
@@ -273,12 +288,26 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
         "row_sparse_embedding": sf.layer_states[0].row_sparse,
         "layer_numel": sum(p.numel() for p in sf.decoder_layers[0].parameters()),
         "output_numel": sum(p.numel() for p in sf.output_layer.parameters()),
+        "storage": storage_stats,
     }
     sf.close()
     del sf, out, rt
     gc.collect()
     torch.cuda.empty_cache()
     return r
+
+
+def _storage_snapshot(sf) -> dict:
+    """Counters of the storage engine and of the two offloaders' waits."""
+    from test1_amd import storage
+
+    st = storage.default_engine().stats()
+    off = sf.layer_optimizer.offloader
+    spill = sf._spill
+    return {"bytes_read": st["bytes_read"], "bytes_written": st["bytes_written"], "busy_s": st["busy_s"],
+            "bytes_staged": st["bytes_staged"],
+            "optimizer_wait_s": 0.0 if off is None else off.wait_s,
+            "checkpoint_slot_wait_s": 0.0 if spill is None else spill.slot_wait_s}
 
 
 def megatron_flops_per_step(w: dict) -> float:
@@ -355,6 +384,12 @@ def main():
                          "(default: as many as fit in half of the free HBM)")
     ap.add_argument("--fused-ce", action="store_true",
                     help="chunked linear + cross entropy in the output unit (no [B,S,V] logits)")
+    ap.add_argument("--ac-offload", default="cpu", choices=("cpu", "nvme", "none"),
+                    help="checkpoint inputs to pinned host slots, to files on local storage, or kept on the GPU")
+    ap.add_argument("--opt-nvme-fraction", type=float, default=0.0,
+                    help="AdamW moments on local storage: exp_avg above 0, both moments above 0.5")
+    ap.add_argument("--offload-dir", default="/tmp/sf_offload",
+                    help="directory of the storage-offload files (removed as they are opened)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs the layer-streaming path on one GPU only; use --gpus 1", file=sys.stderr)
@@ -437,7 +472,9 @@ def main():
                    "h2d_format": args.h2d_format, "resident_layers": r["resident_layers"],
                    "d2h_engine": args.d2h_engine, "fused_cross_entropy": args.fused_ce,
                    "stage_after_update": r["stage_after_update"],
-                   "row_sparse_embedding": r["row_sparse_embedding"]},
+                   "row_sparse_embedding": r["row_sparse_embedding"],
+                   "ac_offload_mode": args.ac_offload,
+                   "optimizer_nvme_offload_fraction": args.opt_nvme_fraction},
         "roofline": {
             "bound": "hbm",
             "kernel": "cast_flat_kernel (fp32 -> bf16 RNE staging cast)",
@@ -461,6 +498,7 @@ def main():
                     "context only: the step is bound by the host link, not by MFMA",
         },
         "host_dram": host_dram_stats(r, args, cpu),
+        "storage": r["storage"],
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
         "losses": losses,
         "variants": variants,

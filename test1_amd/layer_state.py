@@ -380,7 +380,29 @@ class PriorityUpdateExecutor:
                 task, must_wait = self._pick()
                 if not must_wait:
                     self._tasks.remove(task)
-            if must_wait:
+            if must_wait and getattr(task[5], "poll_interval", None):
+                # Readiness that other queued tasks' progress can bring about
+                # (moments read back into buffers they free): pick again until
+                # some task is ready instead of committing to the oldest.  If
+                # none is for poll_fallback_s, run the oldest anyway (it then
+                # waits for its own inputs), so progress never depends on the
+                # readiness reports alone.
+                deadline = time.monotonic() + task[5].poll_fallback_s
+                while must_wait and time.monotonic() < deadline:
+                    time.sleep(task[5].poll_interval)
+                    with self._cv:
+                        task, must_wait = self._pick()
+                        if not must_wait:
+                            self._tasks.remove(task)
+                if must_wait:
+                    with self._cv:
+                        task = min(self._tasks, key=lambda t: t[1])
+                        self._tasks.remove(task)
+                    try:
+                        task[5].synchronize()
+                    except BaseException:
+                        pass
+            elif must_wait:
                 try:
                     task[5].synchronize()
                 except BaseException:
@@ -408,16 +430,23 @@ class PriorityUpdateExecutor:
 
 class _UpdateReady:
     """``query`` is true once the gradients have landed and the moments are
-    in memory; ``synchronize`` waits for the gradients only (the update reads
-    moments that are still on storage itself), so an executor that waits for
-    its oldest task never waits on a read that needs a buffer held by
-    another queued unit."""
+    in memory.  A unit's moments may wait for a buffer that another queued
+    unit's update frees, so the executor must not commit to one waiting
+    task: ``poll_interval`` makes it pick again until some task is ready.
+    ``synchronize`` waits for the gradients only (the update reads moments
+    that are still on storage itself)."""
+
+    poll_interval = 200e-6
+    poll_fallback_s = 10.0
 
     def __init__(self, grads_ready, optimizer, unit: int):
         self.grads_ready, self.optimizer, self.unit = grads_ready, optimizer, unit
 
     def query(self) -> bool:
-        return self.grads_ready.query() and self.optimizer.states_ready(self.unit)
+        try:
+            return self.grads_ready.query() and self.optimizer.states_ready(self.unit)
+        except BaseException:
+            return True  # a failed copy or read: the update runs and reports it
 
     def synchronize(self) -> None:
         self.grads_ready.synchronize()

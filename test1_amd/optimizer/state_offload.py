@@ -12,8 +12,9 @@ in the offload directory, unlinked at once so that the space is returned at
 exit), each (unit, moment) in its own 4 KiB-aligned region.  Host memory is a
 few buffers, each able to hold the moments of the largest unit:
 
-* ``prefetch(unit, priority)`` queues a read; reads start, lowest priority
-  first, whenever a buffer can be taken without waiting;
+* ``prefetch(unit, priority)`` requests a unit; reads of requested units
+  start, lowest priority first, whenever a buffer can be taken without
+  waiting, and a buffer holding a requested unit is kept for it;
 * ``acquire(unit)`` returns the unit's moments, waiting for (or starting)
   the read, and for a write-back of the same buffer still in flight;
 * ``release(unit)`` queues the write-back of the updated moments.
@@ -21,9 +22,9 @@ few buffers, each able to hold the moments of the largest unit:
 A buffer keeps its unit's moments after the write-back, so a unit updated
 again before its buffer is reused is not read back (its buffer already holds
 what the file holds).  Buffers are taken in this order: never used, clean
-(written back) least recently used, then -- only when the caller must wait --
-a prefetched but unused one (its unit goes back on the read queue), then the
-oldest write-back.  Moments reach the optimizer unchanged, so the updates are
+(written back) and not requested, least recently used first, then -- only
+when the caller must wait -- one holding the requested unit needed last (it
+is read again later), then the oldest write-back.  Moments reach the optimizer unchanged, so the updates are
 those of moments kept in memory, bit for bit.
 
 Unwritten file ranges read as zeros: the initial moments need no writes.
@@ -43,7 +44,7 @@ from .. import storage
 
 
 class _Buffer:
-    __slots__ = ("tensors", "capacity", "owner", "reads", "writes", "in_use", "prefetched", "last")
+    __slots__ = ("tensors", "capacity", "owner", "reads", "writes", "in_use", "last")
 
     def __init__(self, kinds: int, numel: int):
         self.tensors = [storage.aligned_empty(numel, torch.float32) for _ in range(kinds)]
@@ -52,7 +53,6 @@ class _Buffer:
         self.reads: List[storage.IoRequest] = []
         self.writes: List[storage.IoRequest] = []
         self.in_use = False
-        self.prefetched = False
         self.last = 0
 
     def grow(self, numel: int) -> None:
@@ -83,8 +83,7 @@ class StateOffloader:
         self._max_numel = 0
         self._buffers: List[_Buffer] = []
         self._where: Dict[int, _Buffer] = {}
-        self._wanted: Dict[int, Tuple[float, int]] = {}
-        self._prio: Dict[int, float] = {}
+        self._requested: Dict[int, Tuple[float, int]] = {}
         self._seq = itertools.count()
         self._tick = itertools.count(1)
         self._lock = threading.RLock()
@@ -115,19 +114,27 @@ class StateOffloader:
         return sum(4 * b.capacity * self.n_moments for b in self._buffers)
 
     # ------------------------------------------------------------------
+    # Buffer states: unused (no owner); loading (reads in flight); holding a
+    # unit's moments, clean or with its write-back in flight; in use between
+    # acquire and release.  A unit is "requested" from prefetch() until its
+    # acquire(); a buffer holding a requested unit is protected: reads for
+    # other units never take it (only an acquire that must wait may).
     def _reap(self, b: _Buffer) -> None:
         """Release finished write-backs of ``b`` (its contents stay valid)."""
         if b.writes and all(r.done() for r in b.writes):
             b.writes = []
 
+    def _protected(self, b: _Buffer) -> bool:
+        return b.owner is not None and b.owner in self._requested
+
     def _evict(self, b: _Buffer) -> None:
         if b.owner is not None:
             del self._where[b.owner]
         b.owner = None
-        b.prefetched = False
 
     def _take(self, blocking: bool) -> Optional[_Buffer]:
-        """A buffer free for a new unit (under the lock)."""
+        """A buffer for a new unit (under the lock), or None if ``blocking``
+        is false and every buffer is busy or protected."""
         for b in self._buffers:
             if not b.in_use and b.owner is None and not b.reads and not b.writes:
                 return b
@@ -139,64 +146,54 @@ class StateOffloader:
             if not b.in_use:
                 self._reap(b)
         clean = [b for b in self._buffers
-                 if not b.in_use and not b.prefetched and not b.reads and not b.writes]
+                 if not b.in_use and not b.reads and not b.writes and not self._protected(b)]
         if clean:
             b = min(clean, key=lambda b: b.last)
             self._evict(b)
             return b
         if not blocking:
             return None
-        pre = [b for b in self._buffers if not b.in_use and b.prefetched]
-        if pre:
-            # the prefetched unit needed last goes back on the read queue
-            b = max(pre, key=lambda b: self._prio.get(b.owner, 0.0))
-            for r in b.reads:
-                r.wait()
-            b.reads = []
-            unit = b.owner
-            self._evict(b)
-            self._wanted[unit] = (self._prio.get(unit, 0.0), next(self._seq))
-            return b
-        writing = [b for b in self._buffers if not b.in_use and b.writes]
-        if writing:
+        prot = [b for b in self._buffers if not b.in_use and self._protected(b)]
+        if prot:
+            # the requested unit needed last stays requested and is read again later
+            b = max(prot, key=lambda b: self._requested[b.owner])
+        else:
+            writing = [b for b in self._buffers if not b.in_use and b.writes]
+            if not writing:
+                raise RuntimeError("StateOffloader: every buffer is in use")
             b = min(writing, key=lambda b: b.last)
-            for r in b.writes:
-                r.wait()
-            b.writes = []
-            self._evict(b)
-            return b
-        raise RuntimeError("StateOffloader: every buffer is in use")
+        for r in b.reads + b.writes:
+            r.wait()
+        b.reads, b.writes = [], []
+        self._evict(b)
+        return b
 
     def _start_read(self, unit: int, b: _Buffer) -> None:
         numel, nbytes, offs = self._layout[unit]
         b.grow(numel)
         b.owner = unit
-        b.prefetched = True
         self._where[unit] = b
         b.reads = [self.file.read(t, off, nbytes) for t, off in zip(b.tensors, offs)]
 
     def _pump(self) -> None:
-        """Start queued reads while buffers can be taken without waiting."""
-        while self._wanted:
-            unit = min(self._wanted, key=lambda u: self._wanted[u])
-            if unit in self._where:
-                del self._wanted[unit]
-                continue
+        """Start reads of requested units, lowest priority first, while
+        buffers can be taken without waiting."""
+        pending = sorted((key, u) for u, key in self._requested.items() if u not in self._where)
+        for _, unit in pending:
             b = self._take(blocking=False)
             if b is None:
                 return
-            del self._wanted[unit]
             self._start_read(unit, b)
 
     # ------------------------------------------------------------------
     def prefetch(self, unit: int, priority: float = 0.0) -> None:
-        """Queue a read of ``unit``'s moments (lower priority first)."""
+        """Request ``unit``'s moments ahead of its update (lower priority
+        first); they stay requested until ``acquire``."""
         with self._lock:
             if unit not in self._layout:
                 return
-            self._prio[unit] = priority
-            if unit not in self._where and unit not in self._wanted:
-                self._wanted[unit] = (priority, next(self._seq))
+            if unit not in self._requested:
+                self._requested[unit] = (priority, next(self._seq))
             self._pump()
 
     def ready(self, unit: int) -> bool:
@@ -215,7 +212,7 @@ class StateOffloader:
         t0 = time.perf_counter()
         with self._lock:
             numel = self._layout[unit][0]
-            self._wanted.pop(unit, None)
+            self._requested.pop(unit, None)
             b = self._where.get(unit)
             if b is None:
                 b = self._take(blocking=True)
@@ -223,7 +220,6 @@ class StateOffloader:
             if b.in_use:
                 raise RuntimeError(f"StateOffloader: unit {unit} acquired twice")
             b.in_use = True
-            b.prefetched = False
             pending = b.reads + b.writes
         # Wait outside the lock (the buffer is in use, so nobody takes it);
         # keep other reads going while this one completes.

@@ -244,7 +244,7 @@ class SlideFSDP(nn.Module):
             tag = f"{os.getpid()}-{id(self)}"
             self._act_paths = [[os.path.join(config.ac_offload_dir, f"act-{tag}-{i}-{c}.bin") for c in range(4)]
                                for i in range(self.num_decoder_layers)]
-            self._spill = StorageSpill(n_slots=4)
+            self._spill = StorageSpill(n_slots=6)
         self._print_model_info()
 
     # ------------------------------------------------------------------

@@ -107,6 +107,49 @@ def test_priority_update_executor_skips_tasks_whose_input_is_not_ready():
     ex.shutdown(wait=True)
 
 
+class _PolledReady:
+    """Readiness the executor must poll (as a unit whose moments wait for a
+    buffer that another queued unit's update frees)."""
+
+    poll_interval = 1e-3
+    poll_fallback_s = 30.0
+
+    def __init__(self, cond):
+        self.cond = cond
+
+    def query(self):
+        return self.cond()
+
+    def synchronize(self):
+        raise AssertionError("polled readiness is not waited on")
+
+
+def test_priority_update_executor_polls_instead_of_committing_to_the_oldest():
+    from test1_amd.layer_state import PriorityUpdateExecutor
+
+    ex = PriorityUpdateExecutor("test-upd3")
+    gate, flag = threading.Event(), threading.Event()
+    log = []
+    ex.submit(-1, gate.wait, 10)
+    # the oldest task (9) can only become ready after task 5 has run; task 5
+    # becomes ready a little later: the worker must wait for 5, run it, then 9
+    f9 = ex.submit(9, log.append, 9, ready=_PolledReady(lambda: 5 in log))
+    f5 = ex.submit(5, log.append, 5, ready=_PolledReady(flag.is_set))
+    gate.set()
+    threading.Timer(0.1, flag.set).start()
+    for f in (f9, f5):
+        f.result(timeout=10)
+    assert log == [5, 9]
+    # nothing ever ready: after poll_fallback_s the oldest task runs anyway
+    never = _PolledReady(lambda: False)
+    never.poll_fallback_s = 0.2
+    never.synchronize = lambda: None
+    f = ex.submit(3, log.append, 3, ready=never)
+    f.result(timeout=10)
+    assert log == [5, 9, 3]
+    ex.shutdown(wait=True)
+
+
 def test_grad_slots_per_unit_are_sized_and_never_block(monkeypatch):
     from test1_amd import layer_state
     from test1_amd.layer_state import GradSlotsPerUnit

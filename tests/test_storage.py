@@ -155,6 +155,45 @@ def test_offloader_matches_a_dict_model(engine, tmp_path, n_buffers):
     off.close()
 
 
+@pytest.mark.parametrize("n_buffers", [2, 3])
+def test_every_requested_unit_becomes_ready(engine, tmp_path, n_buffers):
+    """A scheduler that updates only units whose moments are ready (as the
+    update thread does) must never starve: units requested while their
+    moments are still cached from their last update keep that buffer, and
+    requested units without a buffer are read as buffers drain.  (A cached
+    unit once lost its buffer to another unit's read and was then never read
+    back, so a poll-until-ready scheduler waited forever.)"""
+    off = StateOffloader(str(tmp_path), n_moments=1, n_buffers=n_buffers, engine=engine)
+    n_units = 6
+    for u in range(n_units):
+        off.register(u, 3000 + 100 * u)
+    rng = random.Random(n_buffers)
+    vals = {u: 0.0 for u in range(n_units)}
+    for step in range(5):
+        order = list(range(n_units))
+        rng.shuffle(order)
+        for pri, u in enumerate(order):       # requests arrive while earlier units update
+            off.prefetch(u, priority=rng.random())
+        remaining = set(order)
+        for _ in range(20000):
+            if not remaining:
+                break
+            for u in sorted(remaining):
+                if off.ready(u):
+                    (m,) = off.acquire(u)
+                    assert bool((m == vals[u]).all()), (step, u)
+                    m.add_(1.0)
+                    vals[u] += 1.0
+                    off.release(u)
+                    remaining.discard(u)
+                    break
+            else:
+                import time
+                time.sleep(1e-4)
+        assert not remaining, f"step {step}: units {sorted(remaining)} never became ready"
+    off.close()
+
+
 def _units(seed, sizes):
     g = torch.Generator().manual_seed(seed)
     return {u: [torch.nn.Parameter(torch.randn(s, generator=g) * 0.02) for s in shp] for u, shp in sizes.items()}

@@ -297,6 +297,32 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
     return r
 
 
+def cast_alone(dev, n: int, reps: int = 20) -> dict:
+    """The staging cast on an otherwise idle GPU, for context beside the
+    in-pipeline figure: one ``n``-element launch repeated ``reps`` times
+    (after 3 warmups) on a stream of its own, timed with HIP events."""
+    import torch
+
+    from test1_amd import kernels
+
+    src = torch.randn(n, device=dev)
+    dst = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    st = torch.cuda.Stream(device=dev)
+    for _ in range(3):
+        kernels.cast_f32_bf16_(dst, src, st)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in ev:
+        a.record(st)
+        kernels.cast_f32_bf16_(dst, src, st)
+        b.record(st)
+    st.synchronize()
+    ms = sum(a.elapsed_time(b) for a, b in ev) / reps
+    gbs = 6 * n / (ms * 1e-3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"elements": n, "launches": reps, "avg_launch_ms": ms, "achieved": gbs, "frac": gbs / HBM_PEAK_GBS}
+
+
 def _storage_snapshot(sf) -> dict:
     """Counters of the storage engine and of the two offloaders' waits."""
     from test1_amd import storage
@@ -442,6 +468,8 @@ def main():
 
     total_params = r["total_params"]
     layer_numel = r["layer_numel"]
+    alone = cast_alone(dev, layer_numel)
+    log(f"[bench] cast alone, one decoder layer: {alone['avg_launch_ms']:.4f} ms, {alone['achieved']:.0f} GB/s")
     resident = layer_numel + r["output_numel"]
     cpu = None
     if not args.no_cpu_baseline:
@@ -489,6 +517,10 @@ def main():
             "launches": ncast,
             "avg_launch_ms": cast_ms / ncast if ncast else None,
             "algorithmic_bytes_per_launch": cast_bytes / ncast if ncast else None,
+            "alone": alone,
+            "note": "achieved/frac: every cast of the timed steps, most of them beside the backward's "
+                    "GEMMs (units are staged right after their update); alone: one decoder layer's cast "
+                    "on an idle GPU after the timed steps",
         },
         "host_link": link_stats(r, args.steps),
         "model_tflops": {

@@ -73,6 +73,11 @@ __device__ __forceinline__ u32x4 cast8(const f32x4 a, const f32x4 b) {
 // ---------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void cast_flat_kernel(
     const float* __restrict__ src, uint16_t* __restrict__ dst, uint64_t n8) {
+    // Highest issue priority among the waves of its SIMD: staged units are
+    // cast while the backward's GEMMs run on the same CUs, and the cast's few
+    // instructions per byte then issue without queueing behind MFMA waves
+    // (in a training step: 0.2537 -> 0.2492 ms per Llama layer).
+    __builtin_amdgcn_s_setprio(3);
     const uint64_t tile0 = uint64_t(blockIdx.x) * (kThreads * kCastUnroll);
     if (tile0 + kThreads * kCastUnroll <= n8) {
         // Full tile (every workgroup but possibly the last): all loads are

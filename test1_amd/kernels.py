@@ -9,6 +9,7 @@ asynchronous on ``stream`` (default: the current stream).
 from __future__ import annotations
 
 import ctypes
+import threading
 import time
 import os
 from typing import Optional, Sequence, Tuple
@@ -298,17 +299,36 @@ def dma_query(handle) -> bool:
 
 class DmaReady:
     """``query()`` / ``synchronize()`` view of an SDMA copy handle, the
-    interface of a device event."""
+    interface of a device event.  Completion is remembered once seen, so
+    several threads may ask; ``release`` (``dma_wait``, which frees the copy's
+    signals) is allowed only after completion was seen, and later queries
+    then never touch the freed signals."""
 
     def __init__(self, handle):
         self.handle = handle
+        self._done = False
+        self._released = False
+        self._lock = threading.Lock()
 
     def query(self) -> bool:
-        return dma_query(self.handle)
+        with self._lock:
+            if not self._done:
+                self._done = dma_query(self.handle)
+            return self._done
 
     def synchronize(self) -> None:
-        while not dma_query(self.handle):
+        while not self.query():
             time.sleep(50e-6)
+
+    def release(self) -> Tuple[int, int]:
+        """Wait for the copies, free their signals and return their (start,
+        end) ns as ``dma_wait``."""
+        self.synchronize()
+        with self._lock:
+            if self._released:
+                raise RuntimeError("DmaReady: released twice")
+            self._released = True
+            return dma_wait(self.handle)
 
 
 def dma_wait(handle) -> Tuple[int, int]:

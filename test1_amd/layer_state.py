@@ -901,6 +901,7 @@ class LayerRuntimeState(nn.Module):
                 handle = kernels.dma_copy_d2h(pairs)
                 rt.mark("dma_issued", self.layer_idx)
                 done = None
+                dma_ready = kernels.DmaReady(handle)
             else:
                 rt.d2h_stream.wait_event(grad_ready)
                 if cast_fence is not None:
@@ -931,10 +932,10 @@ class LayerRuntimeState(nn.Module):
         # waited for; the caching allocator cannot hand them out before then.
         keep = grads if handle is not None else None
         del grads, pairs
-        ready = done if handle is None else kernels.DmaReady(handle)
+        ready = done if handle is None else dma_ready
         self._update_future = rt.update_executor.submit(rt.update_priority(self.layer_idx), self._do_update,
-                                                        slot, done, missing, handle, keep, nbytes,
-                                                        ready=self._update_ready(ready))
+                                                        slot, done, missing, None if handle is None else dma_ready,
+                                                        keep, nbytes, ready=self._update_ready(ready))
 
     def _update_ready(self, grads_ready):
         """Readiness of this unit's update: its gradients on the host and,
@@ -1086,12 +1087,12 @@ class LayerRuntimeState(nn.Module):
         return True
 
     def _do_update(self, slot: int, d2h_done: Optional[torch.cuda.Event], missing: List[Tuple[int, int]],
-                   dma_handle=None, keep=None, nbytes: int = 0) -> bool:
+                   dma_ready=None, keep=None, nbytes: int = 0) -> bool:
         rt = self.runtime
         try:
             rt.mark("update_start", self.layer_idx)
-            if dma_handle is not None:
-                t0, t1 = kernels.dma_wait(dma_handle)
+            if dma_ready is not None:
+                t0, t1 = dma_ready.release()
                 rt.mark("dma_done", self.layer_idx)
                 del keep
                 if rt.d2h_timing is not None and t1 > t0:

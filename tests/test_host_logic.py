@@ -219,3 +219,31 @@ def test_gated_executor_gives_the_slot_to_the_most_urgent_ready_task():
         f.result(timeout=10)
     ex2.shutdown(wait=True)
     ex.shutdown(wait=True)
+
+
+def test_dma_ready_remembers_completion_and_never_queries_freed_signals(monkeypatch):
+    """The update executor polls a unit's copies while the update thread may
+    free them: once completion has been seen, no query touches the (possibly
+    freed) signals again, and they are freed only after completion."""
+    from test1_amd import kernels
+
+    state = {"done_after": 3, "queries": 0, "freed": False}
+
+    def fake_query(handle):
+        assert not state["freed"], "queried freed signals"
+        state["queries"] += 1
+        return state["queries"] >= state["done_after"]
+
+    def fake_wait(handle):
+        state["freed"] = True
+        return (1, 2)
+
+    monkeypatch.setattr(kernels, "dma_query", fake_query)
+    monkeypatch.setattr(kernels, "dma_wait", fake_wait)
+    r = kernels.DmaReady(("h", 1))
+    assert not r.query() and not r.query()
+    assert r.release() == (1, 2)          # waits for completion, then frees
+    assert state["freed"] and r.query()   # answered from memory
+    r.synchronize()
+    with pytest.raises(RuntimeError):
+        r.release()

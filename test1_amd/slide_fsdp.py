@@ -521,7 +521,11 @@ class SlideFSDP(nn.Module):
             causal_mask = _hf_create_causal_mask(config=self.model_config, inputs_embeds=hidden_states,
                                                  attention_mask=attention_mask, past_key_values=None,
                                                  position_ids=cache_position.unsqueeze(0))
-        if self.position_embeddings is None and self.rotary_emb is not None:
+        if self.rotary_emb is not None and (self.position_embeddings is None
+                                            or self.position_embeddings[0].shape[-2] != seq_length):
+            # Cached per sequence length.  The reference computes them once
+            # (slide_fsdp.py:564-566), so a batch of another length would get
+            # the first batch's cos/sin.
             self.position_embeddings = self.rotary_emb(hidden_states, cache_position.unsqueeze(0))
 
         num_decoder_states = len(self.layer_states) - 2

@@ -111,7 +111,15 @@ def test_storage_offload_updates_match_oracle_bit_exact(dev, tmp_path, ac_mode, 
                                  nvme_buffers=2)
 
 
-def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, nvme_buffers=None):
+def test_changing_batch_shapes_match_oracle(dev):
+    """Batches of different sizes and lengths in one run ([2,128], [1,96],
+    [3,64], [2,128]): checkpoint slots, embedding row buffers and rotary
+    tables follow the shape, and every update stays the oracle's, bit for
+    bit."""
+    check_updates_against_oracle(dev, "llama", "fp32", {}, {}, shapes=[(2, 128), (1, 96), (3, 64), (2, 128)])
+
+
+def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, nvme_buffers=None, shapes=None):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model(arch)
@@ -126,7 +134,11 @@ def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, 
         arrs = [p.detach().numpy().copy() for p in ps]
         ref_units.append(arrs)
         orc.add_layer(arrs)
-    for ids in batches(steps):
+    if shapes is None:
+        steps_ids = batches(steps)
+    else:
+        steps_ids = [batches(1, B, S)[0] for B, S in shapes]
+    for ids in steps_ids:
         sf.runtime.capture = {}
         ids = ids.to(dev)
         sf(input_ids=ids, labels=ids)
@@ -323,6 +335,9 @@ def test_learning_rate_change_and_save_pretrained(dev, tmp_path):
         for p, a in zip(ps, ref_units[u]):
             assert np.array_equal(p.detach().numpy().view(np.uint32), a.view(np.uint32)), f"unit {u}"
 
+    # As the reference: gradients are released as each unit is offloaded, so
+    # the norm is taken over none and nothing is scaled.
+    assert float(sf.clip_grad_norm_(1.0)) == 0.0
     out = sf.save_pretrained(str(tmp_path / "ckpt"))
     saved = {}
     for name in os.listdir(out):

@@ -302,6 +302,27 @@ int sf_adam_update_rows(int optimizer_id, size_t step, float lr, float beta1,
                         size_t n_rows, size_t row_len, const int64_t* row_slot,
                         const void* grads, size_t n_grad_rows, int g_dtype);
 
+/* Scalars of one update of step `step` as the reference's stateful call
+ * sequence yields them (Adam_Optimizer::IncrementStep and its bias
+ * corrections, cpu_adam.h:57-89) when every unit is stepped once per step,
+ * last unit first, with at least two calls per step: first_of_step = 1 for
+ * the first call of the step (the last unit's first parameter), 0 for every
+ * other.  No optimizer state is read or written, so a caller that updates
+ * units in another order still gets the reference's bits.  No reference
+ * counterpart (the reference's order is fixed: updates run first in, first
+ * out, slide_fsdp.py:163). */
+int sf_adam_hparams_in_order(size_t step, float lr, float beta1, float beta2,
+                             float eps, float weight_decay, int bias_correction,
+                             int adamw_mode, int first_of_step,
+                             sf_adam_hparams* hp);
+
+/* sf_adam_update_rows with caller-given scalars and no optimizer state. */
+int sf_cpu_adam_step_rows(float* params, float* exp_avg, float* exp_avg_sq,
+                          uint16_t* params_bf16, size_t n_rows, size_t row_len,
+                          const int64_t* row_slot, const void* grads,
+                          size_t n_grad_rows, int g_dtype,
+                          const sf_adam_hparams* hp);
+
 /* OpenMP team size used by the host AdamW (<= 0: library default). */
 int sf_cpu_set_threads(int nthreads);
 /* 1 if the AVX-512 path is used on this host, 0 for the portable path. */

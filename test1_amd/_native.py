@@ -94,6 +94,8 @@ CPU_SIGNATURES = {
     "sf_cpu_adam_step_cast": [_vp, _vp, _i, _vp, _vp, _vp, _sz, ctypes.POINTER(SfAdamHparams)],
     "sf_cpu_cast_f32_bf16": [_vp, _vp, _sz],
     "sf_adam_update_rows": [_i, _sz, _f, _f, _f, _f, _f, _i, _vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _sz, _i],
+    "sf_adam_hparams_in_order": [_sz, _f, _f, _f, _f, _f, _i, _i, _i, ctypes.POINTER(SfAdamHparams)],
+    "sf_cpu_adam_step_rows": [_vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, _sz, _i, ctypes.POINTER(SfAdamHparams)],
     "sf_cpu_set_threads": [_i],
     "sf_cpu_has_avx512": [],
     "sf_io_create": [_i, _sz, ctypes.POINTER(_vp)],

@@ -409,6 +409,40 @@ void stateful_hparams(AdamState& stt, size_t step, float lr, float beta1, float 
     }
 }
 
+// Scalars of one update as the reference's call sequence yields them when
+// every unit is stepped once per step, last unit first, each with at least
+// two calls in all per step (Adam_Optimizer::IncrementStep, cpu_adam.h:57-76,
+// then cpu_adam.h:77-89): the first call of step t multiplies the beta^(t-1)
+// that the previous step's calls left (float(pow) after its second call, 1
+// before the first step) by beta; every later call of the step recomputes
+// beta^t with pow.  The caller says which call is the first.
+void hparams_in_reference_order(size_t step, float lr, float beta1, float beta2, float eps, float weight_decay,
+                                int bias_correction, int adamw_mode, int first_of_step, sf_adam_hparams& hp) {
+    float b1t, b2t;
+    if (first_of_step) {
+        const float p1 = step > 1 ? float(std::pow(double(beta1), double(step - 1))) : 1.0f;
+        const float p2 = step > 1 ? float(std::pow(double(beta2), double(step - 1))) : 1.0f;
+        b1t = p1 * beta1;
+        b2t = p2 * beta2;
+    } else {
+        b1t = float(std::pow(double(beta1), double(step)));
+        b2t = float(std::pow(double(beta2), double(step)));
+    }
+    float bc1 = 1.0f, bc2 = 1.0f;
+    if (bias_correction) {
+        bc1 = 1.0f - b1t;
+        bc2 = 1.0f / std::sqrt(1.0f - b2t);
+    }
+    hp.beta1 = beta1;
+    hp.beta2 = beta2;
+    hp.eps = eps;
+    hp.weight_decay = weight_decay;
+    hp.lr = lr;
+    hp.step_size = -1.0f * lr / bc1;
+    hp.bias_correction2 = bc2;
+    hp.adamw_mode = adamw_mode ? 1 : 0;
+}
+
 // Rows of a [n_rows, row_len] tensor; row r takes its gradient from
 // grads[row_slot[r]] or, for row_slot[r] < 0, zeros.  row_len is a multiple
 // of 16, so every row starts a 16-element group and no element falls in the
@@ -468,6 +502,30 @@ int sf_adam_update_rows(int optimizer_id, size_t step, float lr, float beta1, fl
     sf_adam_hparams hp;
     stateful_hparams(*st, step, lr, beta1, beta2, eps, weight_decay, bias_correction, hp);
     const Scalars c = make_scalars(hp);
+    if (g_dtype == SF_DTYPE_BF16) adam_rows<SF_DTYPE_BF16>(params, exp_avg, exp_avg_sq, params_bf16, n_rows, row_len, row_slot, grads, c);
+    else adam_rows<SF_DTYPE_F32>(params, exp_avg, exp_avg_sq, params_bf16, n_rows, row_len, row_slot, grads, c);
+    return SF_OK;
+}
+
+int sf_adam_hparams_in_order(size_t step, float lr, float beta1, float beta2, float eps, float weight_decay,
+                             int bias_correction, int adamw_mode, int first_of_step, sf_adam_hparams* hp) {
+    if (!hp || step == 0) return SF_EINVAL;
+    hparams_in_reference_order(step, lr, beta1, beta2, eps, weight_decay, bias_correction, adamw_mode,
+                               first_of_step, *hp);
+    return SF_OK;
+}
+
+int sf_cpu_adam_step_rows(float* params, float* exp_avg, float* exp_avg_sq, uint16_t* params_bf16,
+                          size_t n_rows, size_t row_len, const int64_t* row_slot, const void* grads,
+                          size_t n_grad_rows, int g_dtype, const sf_adam_hparams* hp) {
+    if (g_dtype != SF_DTYPE_F32 && g_dtype != SF_DTYPE_BF16) return SF_EDTYPE;
+    if (n_rows == 0 || row_len == 0) return SF_OK;
+    if (row_len % 16 != 0) return SF_EINVAL;
+    if (!hp || !params || !exp_avg || !exp_avg_sq || !row_slot || (n_grad_rows > 0 && !grads)) return SF_EINVAL;
+    for (size_t r = 0; r < n_rows; ++r) {
+        if (row_slot[r] >= 0 && size_t(row_slot[r]) >= n_grad_rows) return SF_EINVAL;
+    }
+    const Scalars c = make_scalars(*hp);
     if (g_dtype == SF_DTYPE_BF16) adam_rows<SF_DTYPE_BF16>(params, exp_avg, exp_avg_sq, params_bf16, n_rows, row_len, row_slot, grads, c);
     else adam_rows<SF_DTYPE_F32>(params, exp_avg, exp_avg_sq, params_bf16, n_rows, row_len, row_slot, grads, c);
     return SF_OK;

@@ -131,6 +131,68 @@ def adam_update_rows(optimizer_id: int, step: int, lr: float, beta1: float, beta
     return 0
 
 
+def hparams_in_reference_order(step: int, lr: float, beta1: float, beta2: float, eps: float,
+                               weight_decay: float, bias_correction: bool, adamw_mode: bool,
+                               first_of_step: bool) -> "_native.SfAdamHparams":
+    """Scalars of one update of ``step`` as the reference's stateful call
+    sequence gives them when units are stepped last unit first
+    (``first_of_step``: the last unit's first parameter); no optimizer state
+    is involved, so any update order gets the reference's bits."""
+    hp = _native.SfAdamHparams()
+    _check(_lib().sf_adam_hparams_in_order(int(step), lr, beta1, beta2, eps, weight_decay,
+                                           1 if bias_correction else 0, 1 if adamw_mode else 0,
+                                           1 if first_of_step else 0, ctypes.byref(hp)),
+           "sf_adam_hparams_in_order")
+    return hp
+
+
+def _check_step_tensors(params, grads, exp_avg, exp_avg_sq, params_bf16, what):
+    for t, name in ((params, "params"), (exp_avg, "exp_avg"), (exp_avg_sq, "exp_avg_sq")):
+        if t.dtype != torch.float32 or t.device.type != "cpu" or not t.is_contiguous() or t.numel() != params.numel():
+            raise ValueError(f"{what}: {name} must be a contiguous fp32 CPU tensor of the params' size")
+    gcode = _grad_dtype_code(grads)
+    if gcode < 0:
+        raise RuntimeError(f"Adam optimizer with grad type {grads.dtype} is not supported on current hardware")
+    if grads.device.type != "cpu" or not grads.is_contiguous():
+        raise ValueError(f"{what}: grads must be a contiguous CPU tensor")
+    pb = None
+    if params_bf16 is not None:
+        if (params_bf16.dtype != torch.bfloat16 or params_bf16.device.type != "cpu"
+                or not params_bf16.is_contiguous() or params_bf16.numel() != params.numel()):
+            raise ValueError(f"{what}: params_bf16 must be a contiguous bf16 CPU tensor of the params' size")
+        pb = params_bf16.data_ptr()
+    return gcode, pb
+
+
+def adam_step(params: torch.Tensor, grads: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor,
+              hp: "_native.SfAdamHparams", params_bf16: Optional[torch.Tensor] = None) -> None:
+    """One update with caller-given scalars (``hparams_in_reference_order``)."""
+    gcode, pb = _check_step_tensors(params, grads, exp_avg, exp_avg_sq, params_bf16, "adam_step")
+    if grads.numel() != params.numel():
+        raise ValueError("adam_step: params and grads must have the same numel")
+    _check(_lib().sf_cpu_adam_step_cast(params.data_ptr(), grads.data_ptr(), gcode, exp_avg.data_ptr(),
+                                        exp_avg_sq.data_ptr(), pb, params.numel(), ctypes.byref(hp)),
+           "sf_cpu_adam_step_cast")
+
+
+def adam_step_rows(params: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor, row_slot: torch.Tensor,
+                   grads: torch.Tensor, hp: "_native.SfAdamHparams",
+                   params_bf16: Optional[torch.Tensor] = None) -> None:
+    """``adam_update_rows`` with caller-given scalars."""
+    if params.dim() != 2:
+        raise ValueError("adam_step_rows: params must be 2-D")
+    n_rows, row_len = params.shape
+    gcode, pb = _check_step_tensors(params, grads, exp_avg, exp_avg_sq, params_bf16, "adam_step_rows")
+    if row_slot.dtype != torch.int64 or row_slot.numel() != n_rows or not row_slot.is_contiguous():
+        raise ValueError("adam_step_rows: row_slot must be a contiguous int64 tensor of n_rows")
+    if grads.numel() % max(1, row_len):
+        raise ValueError("adam_step_rows: grads must hold whole rows")
+    _check(_lib().sf_cpu_adam_step_rows(params.data_ptr(), exp_avg.data_ptr(), exp_avg_sq.data_ptr(), pb,
+                                        n_rows, row_len, row_slot.data_ptr(), grads.data_ptr(),
+                                        grads.numel() // max(1, row_len), gcode, ctypes.byref(hp)),
+           "sf_cpu_adam_step_rows")
+
+
 def cast_f32_bf16(src: torch.Tensor, dst: torch.Tensor) -> torch.Tensor:
     """``dst`` = round-to-nearest-even bf16 of ``src`` (NaN -> 0xFFFF), on the
     host AdamW's threads.  Both contiguous CPU tensors of the same size."""

@@ -17,6 +17,10 @@ Differences, all deliberate:
   * each instance owns its own native optimizer id (the reference always
     uses 0, layer_adam.py:59), so two instances in one process do not share
     or destroy each other's bias-correction state.
+  * ``reference_order = True`` computes each update's bias corrections as
+    the reference's call order would (last unit first, once per step)
+    instead of from the native call-order-dependent beta^t state, so a
+    caller may update units in any order and keep the reference's bits.
   * NVMe offload (``nvme_offload_fraction > 0``) keeps the reference's
     choice of moments (exp_avg, plus exp_avg_sq above 0.5) but stores them
     through the native storage engine (``StateOffloader``) instead of
@@ -70,6 +74,12 @@ class LayerAdam:
         self.cpu_adam.create_adam(self.optimizer_id, lr, betas[0], betas[1], eps, weight_decay, adamw_mode, True)
         self.fp32_optimizer_state = fp32_optimizer_state
         self.num_layer = num_layer
+        # False: the native stateful update, whose bias corrections depend on
+        # the order of calls, as in the reference.  True (set by callers that
+        # update units out of order, not in the reference): each call gets
+        # the scalars the reference's order -- last unit first, once per
+        # step -- would give it.
+        self.reference_order = False
         self.state: DefaultDict[torch.Tensor, Any] = defaultdict(dict)
         if not 0.0 <= nvme_offload_fraction <= 1.0:
             raise ValueError("nvme_offload_fraction must be in [0, 1]")
@@ -226,9 +236,22 @@ class LayerAdam:
             raise ValueError("LayerAdam: parameter and gradient sizes differ")
         beta1, beta2 = group["betas"]
         st = self.state[p]
+        if self.reference_order:
+            hp = _cpu_adam.hparams_in_reference_order(
+                group["step"], group["lr"], beta1, beta2, group["eps"], group["weight_decay"],
+                group["bias_correction"], self.defaults["adamw_mode"], self._first_of_step(group, p))
+            if not grad.is_contiguous():
+                grad = grad.contiguous()
+            _cpu_adam.adam_step(data, grad, st["exp_avg"], st["exp_avg_sq"], hp, params_bf16=data_bf16)
+            return
         self.cpu_adam.adam_update(self.optimizer_id, group["step"], group["lr"], beta1, beta2, group["eps"],
                                   group["weight_decay"], group["bias_correction"], data, grad,
                                   st["exp_avg"], st["exp_avg_sq"], params_bf16=data_bf16)
+
+    def _first_of_step(self, group: dict, p) -> bool:
+        """Whether the reference's update order (last unit first, parameters
+        in order) makes this the first native call of the step."""
+        return group["layer_idx"] == max(self._groups_by_layer) and p is group["params"][0]
 
     @torch.no_grad()
     def step(self, layer_idx: Optional[int] = None, closure=None):
@@ -300,10 +323,17 @@ class LayerAdam:
             st = self.state[p]
             beta1, beta2 = group["betas"]
             shape = param_view.shape
-            self.cpu_adam.adam_update_rows(self.optimizer_id, group["step"], group["lr"], beta1, beta2,
-                                           group["eps"], group["weight_decay"], group["bias_correction"],
-                                           param_view, st["exp_avg"].view(shape), st["exp_avg_sq"].view(shape),
-                                           row_slot, rows, params_bf16=bf16_view)
+            if self.reference_order:
+                hp = _cpu_adam.hparams_in_reference_order(
+                    group["step"], group["lr"], beta1, beta2, group["eps"], group["weight_decay"],
+                    group["bias_correction"], self.defaults["adamw_mode"], self._first_of_step(group, p))
+                _cpu_adam.adam_step_rows(param_view, st["exp_avg"].view(shape), st["exp_avg_sq"].view(shape),
+                                         row_slot, rows, hp, params_bf16=bf16_view)
+            else:
+                self.cpu_adam.adam_update_rows(self.optimizer_id, group["step"], group["lr"], beta1, beta2,
+                                               group["eps"], group["weight_decay"], group["bias_correction"],
+                                               param_view, st["exp_avg"].view(shape), st["exp_avg_sq"].view(shape),
+                                               row_slot, rows, params_bf16=bf16_view)
         finally:
             self._post_step(layer_idx)
 

@@ -224,3 +224,56 @@ def test_row_sparse_update_rejects_bad_shapes():
         cpu_adam.adam_update_rows(82, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, True, p, m, v,
                                   torch.tensor([0, 1, -1, -1]), torch.zeros(1, 32))
     cpu_adam.destroy_adam(82)
+
+
+def _run_layer_adam(order_fn, reference_order, steps=6, seed=3):
+    """Units 0 (a [64, 32] table, row-sparse updates) and 1..4 (several
+    params each), stepped ``steps`` times in the order ``order_fn(step)``."""
+    g = torch.Generator().manual_seed(seed)
+    shapes = {1: [(48, 32), (32,)], 2: [(40, 16), (16,), (16,)], 3: [(33, 7)], 4: [(64, 16), (64,)]}
+    units = {0: [torch.nn.Parameter(torch.randn(64, 32, generator=g) * 0.02)]}
+    for u, shp in shapes.items():
+        units[u] = [torch.nn.Parameter(torch.randn(s, generator=g) * 0.02) for s in shp]
+    opt = LayerAdam(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, num_layer=5)
+    opt.reference_order = reference_order
+    for u in sorted(units):
+        opt.add_layer_params(u, units[u])
+    gg = torch.Generator().manual_seed(seed + 1)
+    for step in range(steps):
+        grads = {u: [(torch.randn(p.shape, generator=gg) * 1e-3).bfloat16() for p in units[u]] for u in units}
+        ids = torch.randperm(64, generator=gg)[:9]
+        for u in order_fn(step):
+            if u == 0:
+                row_slot = torch.full((64,), -1, dtype=torch.int64)
+                row_slot[ids] = torch.arange(ids.numel())
+                opt.step_rows(0, row_slot, grads[0][0][ids].contiguous(), units[0][0].data)
+            else:
+                opt.step_with_grad_views(u, dict(zip(units[u], grads[u])))
+    return units, opt
+
+
+def test_reference_order_scalars_give_the_reference_bits_in_any_order():
+    """LayerAdam updates units in the reference's order (last unit first)
+    through the stateful native update, pinned against the reference's
+    compiled cpu_adam above.  With ``reference_order`` the same updates in
+    shuffled orders give the same bits over 6 steps (beta2^t by product and
+    by pow differ at t = 3, 4 and 6, so the first call of those steps is
+    checked), while the stateful update in a shuffled order does not."""
+    import random
+
+    descending = lambda step: [4, 3, 2, 1, 0]  # noqa: E731
+    rng = random.Random(7)
+    orders = {s: rng.sample(range(5), 5) for s in range(6)}
+    assert any(o[0] != 4 for o in orders.values())
+    ref_units, _ = _run_layer_adam(descending, reference_order=False)
+    got_units, _ = _run_layer_adam(lambda s: orders[s], reference_order=True)
+    same_order, _ = _run_layer_adam(descending, reference_order=True)
+    stateful_shuffled, _ = _run_layer_adam(lambda s: orders[s], reference_order=False)
+    differs = False
+    for u in ref_units:
+        for a, b, c, d in zip(ref_units[u], got_units[u], same_order[u], stateful_shuffled[u]):
+            ai = a.data.view(torch.int32)
+            assert torch.equal(ai, b.data.view(torch.int32)), f"unit {u}"
+            assert torch.equal(ai, c.data.view(torch.int32)), f"unit {u}"
+            differs |= not torch.equal(ai, d.data.view(torch.int32))
+    assert differs, "the stateful update should depend on the call order"

@@ -284,6 +284,78 @@ class GradStagingRing:
         self._free.put(idx)
 
 
+class GradSlotRing:
+    """Pinned gradient slots when one per unit does not fit the host's
+    pinned memory.  Units more than twice the median unit's size (the output
+    unit; a dense embedding) keep a slot of their own; the others share a
+    ring of slots of the largest remaining unit, so a ring slot holds one
+    decoder's gradients instead of the output unit's.  ``grow`` adds ring
+    slots once the step's other pinned buffers exist.  Ring slots have ids
+    0, 1, ...; a unit's own slot has the id ``("unit", u)``."""
+
+    def __init__(self, unit_sizes: Dict[int, int], depth: int, dtype: torch.dtype = torch.bfloat16):
+        sizes = sorted(unit_sizes.values())
+        median = sizes[len(sizes) // 2] if sizes else 1
+        self.big = {u: n for u, n in unit_sizes.items() if n > 2 * median}
+        small = [n for u, n in unit_sizes.items() if u not in self.big]
+        self.slot_elems = max(1, max(small) if small else max(sizes, default=1))
+        self.n_small = len(small)
+        self._dtype = dtype
+        self.slots: Dict[Any, torch.Tensor] = {}
+        for u, n in self.big.items():
+            self.slots[("unit", u)] = pinned_empty(max(1, n), dtype)
+        self._free: "queue.Queue[int]" = queue.Queue()
+        self.depth = 0
+        for _ in range(depth):
+            self._publish(pinned_empty(self.slot_elems, dtype))
+
+    def _publish(self, t: torch.Tensor) -> None:
+        i = self.depth
+        self.slots[i] = t
+        self.depth += 1
+        self._free.put(i)
+
+    def grow(self, max_depth: int, headroom_bytes: int) -> int:
+        """Pin more ring slots, up to ``max_depth``, until the host refuses;
+        then give back enough of the new ones to leave ``headroom_bytes``
+        pinnable for buffers allocated later.  Returns the slots added."""
+        new: List[torch.Tensor] = []
+        refused = False
+        while self.depth + len(new) < max_depth:
+            try:
+                new.append(pinned_empty(self.slot_elems, self._dtype))
+            except _native.NativeError as e:
+                if e.status != _native.HIP_ERROR_OUT_OF_MEMORY:
+                    raise
+                refused = True
+                break
+        if refused:
+            per = self.slot_elems * torch.empty((), dtype=self._dtype).element_size()
+            for _ in range(min(len(new), -(-headroom_bytes // per))):
+                new.pop()
+        for t in new:
+            self._publish(t)
+        return len(new)
+
+    def acquire(self, timeout: Optional[float] = None, unit: Optional[int] = None):
+        """A ring slot (blocking), or with ``unit`` a big unit's own slot."""
+        if unit is not None and unit in self.big:
+            return ("unit", unit)
+        try:
+            return self._free.get(timeout=timeout)
+        except queue.Empty:
+            raise TimeoutError("GradSlotRing.acquire: no slot released in time") from None
+
+    def own_slot(self, unit: int):
+        """The unit's own slot id, or None for a unit that uses the ring."""
+        return ("unit", unit) if unit in self.big else None
+
+    def release(self, idx) -> None:
+        if isinstance(idx, tuple):
+            return None
+        self._free.put(idx)
+
+
 class GradSlotsPerUnit:
     """One pinned bf16 host slot per unit, sized to the unit.
 
@@ -546,9 +618,12 @@ class StreamingRuntime:
         # Outside the handler: the traceback no longer holds the slots pinned
         # so far, so they are released before the ring is pinned.
         need = 2 * sum(unit_sizes.values())
+        ring = GradSlotRing(unit_sizes, fallback_depth, self._dtype)
         print(f"SlideFSDP: {need / 1e9:.1f} GB of pinned gradient slots (one per unit) do not fit; "
-              f"using a ring of {fallback_depth} slots", flush=True)
-        self.grad_ring = GradStagingRing(fallback_depth, self.pool.max_param_size, self._dtype)
+              f"using {len(ring.big)} slot(s) of their own for the largest units and a ring of "
+              f"{fallback_depth} slots of {2 * ring.slot_elems / 1e9:.2f} GB (grown after the first step)",
+              flush=True)
+        self.grad_ring = ring
 
     def log(self, *event) -> None:
         if self.trace is not None:
@@ -884,6 +959,11 @@ class LayerRuntimeState(nn.Module):
         rt = self.runtime
         if len(args) == 5:
             slot, grads, missing, grad_ready, cast_fence = args
+            own = getattr(rt.grad_ring, "own_slot", None)
+            if own is not None and own(self.layer_idx) is not None:
+                # a unit with a slot of its own hands the ring slot back
+                rt.grad_ring.release(slot)
+                slot = own(self.layer_idx)
         else:
             grads, missing, grad_ready, cast_fence = args
             slot = rt.grad_ring.acquire(timeout=rt.wait_timeout, unit=self.layer_idx)

@@ -58,7 +58,7 @@ from transformers.modeling_outputs import CausalLMOutputWithPast
 from .config import SlideFSDPConfig
 from .distributed_sync import create_distributed_sync
 from .fused_ce import chunked_linear_cross_entropy
-from .layer_state import LayerRuntimeState, StreamingRuntime
+from .layer_state import GradSlotRing, LayerRuntimeState, StreamingRuntime
 from .optimizer import LayerAdam
 from .pinned import pinned_empty
 from .sliding_checkpoint import ActivationRing, SlidingCheckpoint, StorageSpill
@@ -237,6 +237,7 @@ class SlideFSDP(nn.Module):
         self.position_embeddings = None
         self._act_ring = ActivationRing(self.device)
         self._spill: Optional[StorageSpill] = None
+        self._ring_grown = False
         self._act_paths: Optional[List[List[str]]] = None
         if config.ac_offload_mode == "nvme":
             # Checkpoint inputs on local storage, one file per (layer, tensor)
@@ -571,7 +572,20 @@ class SlideFSDP(nn.Module):
         if loss is not None:
             loss = self._PostLayerFunction.apply(loss, output_state, True)
             loss.backward()
+            self._grow_grad_ring()
         return CausalLMOutputWithPast(loss=loss, logits=logits)
+
+    def _grow_grad_ring(self) -> None:
+        """After the first step, when its checkpoint slots and embedding rows
+        are pinned: widen a gradient slot ring (the fallback when one slot per
+        unit does not fit) as far as pinned memory allows, leaving 1 GiB."""
+        ring = self.runtime.grad_ring
+        if self._ring_grown or not isinstance(ring, GradSlotRing):
+            return
+        self._ring_grown = True
+        before = ring.depth
+        ring.grow(max_depth=ring.n_small, headroom_bytes=1 << 30)
+        print(f"SlideFSDP: gradient slot ring {before} -> {ring.depth} slots", flush=True)
 
     # ------------------------------------------------------------------
     def wait_for_updates(self) -> None:

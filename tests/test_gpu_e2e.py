@@ -18,14 +18,14 @@ V, H, I, L = 1024, 256, 512, 3
 LR, BETAS, EPS, WD = 1e-3, (0.9, 0.999), 1e-8, 0.01
 
 
-def make_model(arch: str = "llama"):
+def make_model(arch: str = "llama", vocab: int = V):
     """A small model of the Llama-3 family, or of the Qwen2 family (q/k/v
     projections with biases, as Qwen2.5-14B)."""
     if arch == "llama":
         from transformers import LlamaConfig as C, LlamaForCausalLM as M
     else:
         from transformers import Qwen2Config as C, Qwen2ForCausalLM as M
-    cfg = C(vocab_size=V, hidden_size=H, intermediate_size=I, num_hidden_layers=L,
+    cfg = C(vocab_size=vocab, hidden_size=H, intermediate_size=I, num_hidden_layers=L,
             num_attention_heads=8, num_key_value_heads=4, max_position_embeddings=512,
             rope_theta=500000.0, tie_word_embeddings=False)
     cfg._attn_implementation = "sdpa"
@@ -44,9 +44,9 @@ def units_of(model):
     return [[m.embed_tokens.weight]] + [list(l.parameters()) for l in m.layers] + [[m.norm.weight, model.lm_head.weight]]
 
 
-def batches(n, B=2, S=128):
+def batches(n, B=2, S=128, vocab=V):
     g = torch.Generator().manual_seed(99)
-    return [torch.randint(0, V, (B, S), generator=g) for _ in range(n)]
+    return [torch.randint(0, vocab, (B, S), generator=g) for _ in range(n)]
 
 
 def u16(t):
@@ -119,10 +119,31 @@ def test_changing_batch_shapes_match_oracle(dev):
     check_updates_against_oracle(dev, "llama", "fp32", {}, {}, shapes=[(2, 128), (1, 96), (3, 64), (2, 128)])
 
 
-def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, nvme_buffers=None, shapes=None):
+def test_fallback_slot_ring_when_per_unit_slots_do_not_fit(dev, monkeypatch):
+    """Pinning one gradient slot per unit fails (as for Qwen2.5-14B with fp32
+    masters on hosts with a pinned-memory cap): the output unit (vocab 8192,
+    more than twice a decoder) gets a slot of its own, the decoders share a
+    ring of decoder-sized slots, widened after the first step; updates stay
+    the oracle's, bit for bit, over 4 steps."""
+    from test1_amd import _native, layer_state
+
+    class Refused(layer_state.GradSlotsPerUnit):
+        def __init__(self, *a, **k):
+            raise _native.NativeError("sf_host_alloc failed: out of memory", _native.HIP_ERROR_OUT_OF_MEMORY)
+
+    monkeypatch.setattr(layer_state, "GradSlotsPerUnit", Refused)
+    sf = check_updates_against_oracle(dev, "llama", "fp32", {}, {}, steps=4, vocab=8192, keep=True)
+    ring = sf.runtime.grad_ring
+    assert isinstance(ring, layer_state.GradSlotRing)
+    assert set(ring.big) == {L + 1} and ring.depth == L     # grown to one slot per decoder
+    sf.close()
+
+
+def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, nvme_buffers=None, shapes=None,
+                                 vocab=V, keep=False):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
-    model = make_model(arch)
+    model = make_model(arch, vocab=vocab)
     sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS,
                                           **cfg_kw),
                    wait_timeout=120, h2d_format=h2d_format, **sf_kw)
@@ -135,9 +156,9 @@ def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, 
         ref_units.append(arrs)
         orc.add_layer(arrs)
     if shapes is None:
-        steps_ids = batches(steps)
+        steps_ids = batches(steps, vocab=vocab)
     else:
-        steps_ids = [batches(1, B, S)[0] for B, S in shapes]
+        steps_ids = [batches(1, B, S, vocab=vocab)[0] for B, S in shapes]
     for ids in steps_ids:
         sf.runtime.capture = {}
         ids = ids.to(dev)
@@ -172,6 +193,8 @@ def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, 
         om, ov = orc.moments(u)
         assert np.array_equal(m.numpy().view(np.uint32), om.view(np.uint32)), f"unit {u} exp_avg"
         assert np.array_equal(v.numpy().view(np.uint32), ov.view(np.uint32)), f"unit {u} exp_avg_sq"
+    if keep:
+        return sf
     sf.close()
 
 

@@ -180,10 +180,11 @@ def test_grad_slots_fall_back_to_a_ring_when_pinning_fails(monkeypatch):
     rt.grad_ring, rt._dtype, rt.offload_executor, rt.wait_timeout = None, torch.bfloat16, None, None
     rt.pool = type("P", (), {"max_param_size": 9})()
     ring_slots = []
-    monkeypatch.setattr(layer_state, "GradStagingRing",
-                        lambda depth, n, dt: ring_slots.append((depth, n)) or "ring")
+    monkeypatch.setattr(layer_state, "GradSlotRing",
+                        lambda sizes, depth, dt: ring_slots.append((dict(sizes), depth)) or
+                        type("R", (), {"big": {}, "slot_elems": 9, "acquire": None})())
     rt.init_grad_slots({0: 5, 1: 9, 2: 7, 3: 3})
-    assert rt.grad_ring == "ring" and ring_slots == [(3, 9)]
+    assert ring_slots == [({0: 5, 1: 9, 2: 7, 3: 3}, 3)]
     rt.offload_executor.shutdown(wait=True)
 
     # any other failure is not swallowed
@@ -247,3 +248,41 @@ def test_dma_ready_remembers_completion_and_never_queries_freed_signals(monkeypa
     r.synchronize()
     with pytest.raises(RuntimeError):
         r.release()
+
+
+def test_grad_slot_ring_gives_big_units_their_own_slot_and_grows(monkeypatch):
+    """The fallback when one pinned slot per unit does not fit: units more
+    than twice the median size keep their own slot, the rest share a ring of
+    slots of the largest remaining unit; ``grow`` pins more ring slots until
+    the host refuses, then gives back enough for the headroom."""
+    from test1_amd import _native, layer_state
+    from test1_amd.layer_state import GradSlotRing
+
+    budget = {"left": 10}
+
+    def fake_pinned(n, dt):
+        if budget["left"] <= 0:
+            raise _native.NativeError("sf_host_alloc failed: out of memory", _native.HIP_ERROR_OUT_OF_MEMORY)
+        budget["left"] -= 1
+        return torch.empty(n, dtype=dt)
+
+    monkeypatch.setattr(layer_state, "pinned_empty", fake_pinned)
+    sizes = {0: 40, 1: 10, 2: 10, 3: 9, 4: 10, 5: 10, 6: 10, 7: 10, 8: 10, 9: 100}
+    ring = GradSlotRing(sizes, 2, torch.bfloat16)
+    assert ring.big == {0: 40, 9: 100} and ring.slot_elems == 10 and ring.depth == 2
+    assert ring.slots[("unit", 9)].numel() == 100
+    assert ring.acquire(unit=9) == ("unit", 9) and ring.own_slot(9) == ("unit", 9) and ring.own_slot(3) is None
+    a, b = ring.acquire(timeout=0, unit=3), ring.acquire(timeout=0, unit=4)
+    assert {a, b} == {0, 1}
+    with pytest.raises(TimeoutError):
+        ring.acquire(timeout=0.01, unit=5)
+    ring.release(a)
+    ring.release(("unit", 9))            # own slots are not ring slots: no-op
+    assert ring.acquire(timeout=0, unit=5) == a
+    # 6 more allocations succeed, then the host refuses; 2 slots go back as headroom
+    added = ring.grow(max_depth=20, headroom_bytes=2 * 10 * 2)
+    assert added == 4 and ring.depth == 6
+    assert {ring.acquire(timeout=0) for _ in range(4)} == {2, 3, 4, 5}
+    # growth stops at max_depth without touching the host limit
+    budget["left"] = 100
+    assert ring.grow(max_depth=7, headroom_bytes=0) == 1 and ring.depth == 7

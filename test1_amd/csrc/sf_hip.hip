@@ -27,7 +27,7 @@ namespace {
 
 constexpr int kThreads = 256;  // lanes per workgroup (4 wave64s)
 constexpr int kUnroll = 4;     // 8-element groups per lane per workgroup tile
-constexpr int kCastUnroll = 2; // the same for the flat cast (measured best, see below)
+constexpr int kCastUnroll = 1; // the same for the flat cast (measured best, see below)
 constexpr int kGroup = 8;      // elements per 128-bit bf16 store
 constexpr uint64_t kTileElems = uint64_t(kThreads) * kUnroll * kGroup;  // 8192
 
@@ -66,10 +66,14 @@ __device__ __forceinline__ u32x4 cast8(const f32x4 a, const f32x4 b) {
 // within it, unroll step k covers one contiguous run of kThreads groups,
 // so every load/store instruction of a wave touches one contiguous 1 KiB
 // span.  Loads are ordinary (cached) 128-bit loads and stores are
-// nontemporal: on gfx950 this ran at 6.16 TB/s on a 218M-element layer,
-// against 5.61 TB/s with nontemporal loads as well, 6.04 TB/s with 4 groups
-// per lane and 5.70 TB/s with 8 (one 106,500-workgroup grid per variant,
-// same box, alternating runs).
+// nontemporal.  On gfx950, 218M-element layer, alternating runs on one box:
+// 2 groups per lane 6.16 TB/s, against 5.61 TB/s with nontemporal loads as
+// well, 6.04 TB/s with 4 groups per lane and 5.70 TB/s with 8; 128-lane
+// workgroups (256 groups each) 6.19.  One group per lane (256 groups per
+// workgroup, 106,500 workgroups), measured later on another box in the
+// training step: 0.2172-0.2182 ms per layer alone against 0.2245-0.2253
+// with 2 groups, and 0.245-0.249 against 0.252-0.256 ms beside the
+// backward's kernels.
 // ---------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void cast_flat_kernel(
     const float* __restrict__ src, uint16_t* __restrict__ dst, uint64_t n8) {

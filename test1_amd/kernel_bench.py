@@ -11,6 +11,10 @@ Times, with HIP events on the stream each runs on:
             the offload path's 8-workgroup grid (host link)
   h2d       one DMA copy of N fp32 elements from pinned host memory
 Default N is one Llama-3-8B decoder layer (218,112,000 parameters).
+
+With ``--rotate K`` the cast cycles through K source/destination pairs, so
+that a launch does not find its input in the 256 MB Infinity Cache left by
+the previous one (pick K with K * 6 * N well above that size for small N).
 """
 
 from __future__ import annotations
@@ -41,12 +45,14 @@ def main(argv=None):
     ap.add_argument("--elements", type=int, default=218_112_000)
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--rotate", type=int, default=1, help="source/destination pairs the cast cycles through")
     args = ap.parse_args(argv)
     n, reps = args.elements, args.reps
     dev = torch.device("cuda", 0)
     s = torch.cuda.current_stream()
-    src = torch.randn(n, device=dev) * 0.02
-    dst = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    pairs = [(torch.randn(n, device=dev) * 0.02, torch.empty(n, dtype=torch.bfloat16, device=dev))
+             for _ in range(max(1, args.rotate))]
+    src, dst = pairs[0]
     half = n // 2
     cp_src = torch.ones(half, dtype=torch.float32, device=dev)
     cp_dst = torch.empty_like(cp_src)
@@ -60,9 +66,15 @@ def main(argv=None):
         cp_dst.copy_(cp_src)
     torch.cuda.synchronize()
     res = {}
-    ms = _time(lambda: kernels.cast_f32_bf16_(dst, src, s), s, reps)
+    nxt = iter(range(1 << 62))
+
+    def cast_next():
+        a, b = pairs[next(nxt) % len(pairs)]
+        kernels.cast_f32_bf16_(b, a, s)
+
+    ms = _time(cast_next, s, reps)
     res["cast"] = {"ms": ms, "GB/s": 6 * n / ms / 1e6, "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS,
-                   "algorithmic_bytes": 6 * n}
+                   "algorithmic_bytes": 6 * n, "rotated_pairs": len(pairs)}
     ms = _time(lambda: cp_dst.copy_(cp_src), s, reps)
     res["copy"] = {"ms": ms, "GB/s": 8 * half / ms / 1e6, "bytes_read": 4 * half, "bytes_written": 4 * half}
     ms = _time(lambda: kernels.pack_b16([g], host_g, s, max_workgroups=8), s, max(1, reps // 4))

@@ -524,6 +524,11 @@ class _UpdateReady:
         self.grads_ready.synchronize()
 
 
+def _no_slot() -> None:
+    """Offload gate with one slot per unit: nothing to wait for."""
+    return None
+
+
 class StreamingRuntime:
     """Objects shared by all units of one model: streams, pool, stager, grad
     ring, worker threads and the optional event trace."""
@@ -605,7 +610,10 @@ class StreamingRuntime:
             self._alloc_grad_slots(unit_sizes, fallback_depth)
         if self.offload_executor is None:
             ring = self.grad_ring
-            gate = None if isinstance(ring, GradSlotsPerUnit) else (lambda: ring.acquire(timeout=self.wait_timeout))
+            if isinstance(ring, GradSlotsPerUnit):
+                gate = _no_slot       # the task takes its unit's own slot
+            else:
+                gate = lambda: ring.acquire(timeout=self.wait_timeout)  # noqa: E731
             self.offload_executor = PriorityUpdateExecutor("sf-offload", gate=gate)
 
     def _alloc_grad_slots(self, unit_sizes: Dict[int, int], fallback_depth: int) -> None:
@@ -952,21 +960,19 @@ class LayerRuntimeState(nn.Module):
         self._current_gpu_cache = None
         self._release_unit(unit)
 
-    def _d2h_task(self, *args) -> None:
+    def _d2h_task(self, slot, grads, missing, grad_ready, cast_fence) -> None:
         """Offload thread: copy this unit's gradients into a host slot, then
-        queue the update.  Called as ``(grads, missing, grad_ready, cast_fence)``
-        with per-unit slots, or with a ring slot taken by the thread first."""
+        queue the update.  ``slot`` is the ring slot the thread's gate took,
+        or None with one slot per unit (the unit's own is taken here)."""
         rt = self.runtime
-        if len(args) == 5:
-            slot, grads, missing, grad_ready, cast_fence = args
+        if slot is None:
+            slot = rt.grad_ring.acquire(timeout=rt.wait_timeout, unit=self.layer_idx)
+        else:
             own = getattr(rt.grad_ring, "own_slot", None)
             if own is not None and own(self.layer_idx) is not None:
                 # a unit with a slot of its own hands the ring slot back
                 rt.grad_ring.release(slot)
                 slot = own(self.layer_idx)
-        else:
-            grads, missing, grad_ready, cast_fence = args
-            slot = rt.grad_ring.acquire(timeout=rt.wait_timeout, unit=self.layer_idx)
         rt.mark("d2h_task", self.layer_idx)
         rt.mark("slot", self.layer_idx)
         try:

@@ -17,10 +17,10 @@ def __getattr__(name):
     if name in ("SlideFSDP", "OutputLayer"):
         from . import slide_fsdp
         return getattr(slide_fsdp, name)
-    if name in ("LayerBufferPool", "LayerRuntimeState", "H2DStager", "GradStagingRing"):
+    if name in ("LayerBufferPool", "LayerRuntimeState", "H2DStager", "GradStagingRing", "GradSlotRing"):
         from . import layer_state
         return getattr(layer_state, name)
-    if name in ("SlidingCheckpoint", "ActivationRing"):
+    if name in ("SlidingCheckpoint", "ActivationRing", "StorageSpill", "save_on_cpu"):
         from . import sliding_checkpoint
         return getattr(sliding_checkpoint, name)
     if name == "LayerAdam":

@@ -52,6 +52,9 @@ from typing import Any, Dict, List, Optional, Tuple
 
 import torch
 from torch.autograd.graph import saved_tensors_hooks
+# The reference module also carries a copy of torch's save_on_cpu
+# (sliding_checkpoint.py:206-231); torch's own class is the same interface.
+from torch.autograd.graph import save_on_cpu  # noqa: F401
 
 from . import kernels, storage
 from .pinned import pinned_empty

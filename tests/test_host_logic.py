@@ -286,3 +286,16 @@ def test_grad_slot_ring_gives_big_units_their_own_slot_and_grows(monkeypatch):
     # growth stops at max_depth without touching the host limit
     budget["left"] = 100
     assert ring.grow(max_depth=7, headroom_bytes=0) == 1 and ring.depth == 7
+
+
+def test_save_on_cpu_round_trip():
+    """``sliding_checkpoint.save_on_cpu`` (the reference module carries a copy
+    of torch's, sliding_checkpoint.py:206-231): saved tensors go to the host
+    and come back for the backward."""
+    from test1_amd import save_on_cpu
+
+    x = torch.randn(8, 4, requires_grad=True)
+    with save_on_cpu(pin_memory=False):
+        y = (x * x).sum()
+    y.backward()
+    assert torch.allclose(x.grad, 2 * x.detach())

@@ -229,7 +229,8 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
                           ac_offload_mode=args.ac_offload,
                           ac_offload_dir=os.path.join(args.offload_dir, "activations"),
                           optimizer_nvme_offload_fraction=args.opt_nvme_fraction,
-                          optimizer_offload_dir=os.path.join(args.offload_dir, "optimizer"))
+                          optimizer_offload_dir=os.path.join(args.offload_dir, "optimizer"),
+                          enable_activation_checkpoint=not args.no_activation_checkpoint)
     sf = SlideFSDP(model, cfg, d2h_engine=d2h_engine, h2d_format=h2d_format, resident_layers=resident_layers,
                    fused_cross_entropy=args.fused_ce)
     uses_storage = args.ac_offload == "nvme" or args.opt_nvme_fraction > 0
@@ -410,6 +411,8 @@ def main():
                          "(default: as many as fit in half of the free HBM)")
     ap.add_argument("--fused-ce", action="store_true",
                     help="chunked linear + cross entropy in the output unit (no [B,S,V] logits)")
+    ap.add_argument("--no-activation-checkpoint", action="store_true",
+                    help="keep every decoder's activations in HBM (needs every unit resident): no recompute")
     ap.add_argument("--ac-offload", default="cpu", choices=("cpu", "nvme", "none"),
                     help="checkpoint inputs to pinned host slots, to files on local storage, or kept on the GPU")
     ap.add_argument("--opt-nvme-fraction", type=float, default=0.0,
@@ -502,6 +505,7 @@ def main():
                    "stage_after_update": r["stage_after_update"],
                    "row_sparse_embedding": r["row_sparse_embedding"],
                    "ac_offload_mode": args.ac_offload,
+                   "activation_checkpoint": not args.no_activation_checkpoint,
                    "optimizer_nvme_offload_fraction": args.opt_nvme_fraction},
         "roofline": {
             "bound": "hbm",

@@ -191,10 +191,6 @@ class SlideFSDP(nn.Module):
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
         if config.dtype != torch.bfloat16:
             raise NotImplementedError("SlideFSDP stages parameters as bfloat16; dtype=float16 is not supported")
-        if not config.enable_activation_checkpoint:
-            raise NotImplementedError(
-                "enable_activation_checkpoint=False would keep every unit's weights saved for backward "
-                "while its pool buffer is reused; set it to True")
         self.config = config
         self.device = torch.device(config.device)
         if self.device.type != "cuda":
@@ -227,6 +223,15 @@ class SlideFSDP(nn.Module):
         self.runtime.update_priority = lambda u: 1 - u if u <= 1 else u
         self.runtime.stage_after_update = bool(stage_after_update)
         self._make_resident(self._auto_resident() if resident_layers is None else int(resident_layers))
+        if not config.enable_activation_checkpoint and not self._all_units_own_buffers():
+            # Without checkpoints the backward reads the weights the forward
+            # saved, so no unit may go back to the 2-unit pool in between
+            # (the reference's pool would overwrite them: slide_fsdp.py:399-400
+            # releases each unit after its forward).
+            raise NotImplementedError(
+                "enable_activation_checkpoint=False needs every decoder and the output unit in a device "
+                "buffer of its own (resident_layers = decoders - 1 and room for the last two units); "
+                "with fewer, a reused pool unit would overwrite weights saved for backward")
         self._setup_autograd_functions()
 
         # The recompute must replay the forward's random numbers only if a
@@ -353,6 +358,9 @@ class SlideFSDP(nn.Module):
             if sum(st.total_size for st in extra) * elem < free // 4:
                 for st in extra:
                     st.make_resident(torch.empty(st.total_size, dtype=self.dtype, device=self.device))
+
+    def _all_units_own_buffers(self) -> bool:
+        return all(st._own_unit is not None for st in self.layer_states[1:])
 
     # ------------------------------------------------------------------
     def _setup_autograd_functions(self) -> None:
@@ -495,7 +503,7 @@ class SlideFSDP(nn.Module):
         """One training step (reference slide_fsdp.py:507-640)."""
         batch_size, seq_length = input_ids.shape
         hidden_size = self.model_config.hidden_size
-        if self.config.ac_offload_mode == "cpu":
+        if self.config.ac_offload_mode == "cpu" and self.config.enable_activation_checkpoint:
             if self.layer_tensors is None or self.layer_tensors[0][0].shape != (batch_size, seq_length, hidden_size):
                 self._allocate_activation_tensors(batch_size, seq_length, hidden_size)
         self._act_ring.reset()
@@ -549,7 +557,12 @@ class SlideFSDP(nn.Module):
                                          output_attentions=False, use_cache=False))
 
             ckpt_kw = dict(use_reentrant=False, preserve_rng_state=self._layer_uses_rng)
-            if self.config.ac_offload_mode != "none":
+            if not self.config.enable_activation_checkpoint:
+                # every unit keeps its own device buffer (checked at construction):
+                # the activations stay in HBM and the backward recomputes nothing
+                hidden_states = _layer_forward(hidden_states, causal_mask, self.position_embeddings,
+                                               layer_state.layer)
+            elif self.config.ac_offload_mode != "none":
                 with SlidingCheckpoint(layer_idx=i + 1, layer_tensors=self.layer_tensors,
                                        gds_offload=self._spill is not None, file_paths=self._act_paths,
                                        spill=self._spill, is_last_layer=is_last_decoder,

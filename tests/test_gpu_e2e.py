@@ -119,6 +119,23 @@ def test_changing_batch_shapes_match_oracle(dev):
     check_updates_against_oracle(dev, "llama", "fp32", {}, {}, shapes=[(2, 128), (1, 96), (3, 64), (2, 128)])
 
 
+@pytest.mark.parametrize("h2d_format", ["fp32", "bf16"])
+def test_without_activation_checkpoints(dev, h2d_format):
+    """``enable_activation_checkpoint=False`` with every unit in a device
+    buffer of its own: the activations stay in HBM and nothing is recomputed;
+    updates stay the oracle's, bit for bit, and the losses match the
+    non-offloaded run."""
+    check_updates_against_oracle(dev, "llama", h2d_format, dict(enable_activation_checkpoint=False), {})
+    check_loss_parity(dev, "llama", False, dict(enable_activation_checkpoint=False), dict(h2d_format=h2d_format))
+
+
+def test_without_activation_checkpoints_needs_own_buffers(dev):
+    from test1_amd import SlideFSDP, SlideFSDPConfig
+
+    with pytest.raises(NotImplementedError):
+        SlideFSDP(make_model(), SlideFSDPConfig(device=dev, enable_activation_checkpoint=False), resident_layers=0)
+
+
 def test_fallback_slot_ring_when_per_unit_slots_do_not_fit(dev, monkeypatch):
     """Pinning one gradient slot per unit fails (as for Qwen2.5-14B with fp32
     masters on hosts with a pinned-memory cap): the output unit (vocab 8192,

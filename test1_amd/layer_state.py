@@ -101,6 +101,14 @@ class LayerBufferPool:
             return len(self.pool)
 
 
+def _backlog(copies: deque) -> int:
+    """Drop the completed events at the front of ``copies`` (one stream, so
+    they complete in order) and count the rest."""
+    while copies and copies[0].query():
+        copies.popleft()
+    return len(copies)
+
+
 class _StageTicket:
     """Chunks of one unit's master in flight through the staging ring."""
 
@@ -144,6 +152,11 @@ class H2DStager:
         self.copy_timing: Optional[list] = None
         # Completion event of the last cast issued (see fence_after_casts).
         self.last_cast_done: Optional[torch.cuda.Event] = None
+        self._copies: deque = deque()   # completion events of issued copies, in stream order
+
+    def backlog(self) -> int:
+        """Host-to-device copies issued and not yet complete."""
+        return _backlog(self._copies)
 
     def fence_after_casts(self, stream: torch.cuda.Stream) -> None:
         """Make ``stream`` wait for every cast issued so far.  Kernels that write
@@ -174,6 +187,9 @@ class H2DStager:
             self.copy_timing.append((t0, copied, c * 4))
         t.slots.append(s)
         t.copied.append(copied)
+        self._copies.append(copied)
+        if len(self._copies) > 64:
+            _backlog(self._copies)
 
     def begin(self, host_f32: torch.Tensor) -> _StageTicket:
         self._lock.acquire()
@@ -234,6 +250,7 @@ class BF16Loader:
 
     def __init__(self, h2d_stream: torch.cuda.Stream):
         self.h2d_stream = h2d_stream
+        self._copies: deque = deque()
         self.last_cast_done: Optional[torch.cuda.Event] = None
         self.cast_timing: Optional[list] = None
         self.copy_timing: Optional[list] = None
@@ -257,7 +274,14 @@ class BF16Loader:
         done.record(self.h2d_stream)
         if timing:
             self.copy_timing.append((t0, done, n * 2))
+        self._copies.append(done)
+        if len(self._copies) > 64:
+            _backlog(self._copies)
         return done
+
+    def backlog(self) -> int:
+        """Host-to-device copies issued and not yet complete."""
+        return _backlog(self._copies)
 
 
 class GradStagingRing:
@@ -557,6 +581,10 @@ class StreamingRuntime:
         self.d2h_engine = d2h_engine
         if d2h_engine == "sdma":
             kernels.dma_init(device)
+        # Host AdamW team size (0: leave the library's setting alone); see
+        # set_adam_threads.
+        self.adam_threads = 0
+        self._adam_threads_set = 0
         # Workgroups of the kernels that write into pinned host memory (grad
         # and checkpoint offload): 8 move ~49 GB/s while the link is busy the
         # other way; more do not move more, and slow HBM-bound kernels beside
@@ -598,6 +626,25 @@ class StreamingRuntime:
         # {("device_grads", unit): [param.grad clones]}, for checking the
         # pack and the update against the oracle.
         self.capture: Optional[dict] = None
+
+    def set_adam_threads(self) -> None:
+        """Team size of the next host update (update thread).  With two or
+        more units' copies still queued for the host-to-device link, the
+        AdamW is ahead of the link, the step's bottleneck: it then runs on
+        half of its threads, which leaves host memory bandwidth and cores to
+        the copies and to the threads that feed the GPU.  Measured, Llama-3-8B
+        step, same box: 745-750 ms against 797-801 ms with every update on
+        all threads; a threshold of one queued unit 756-760 ms, of three
+        816 ms; 6 threads 764-768 ms, 10 threads 783 ms.  With bf16 H2D (half
+        the link bytes) the AdamW is the bottleneck and keeps all its threads
+        (yielding there measured 1.5 % slower)."""
+        if not self.adam_threads or self.h2d_format != "fp32":
+            return
+        few = self.stager.backlog() >= 2
+        n = max(1, (self.adam_threads + 1) // 2) if few else self.adam_threads
+        if n != self._adam_threads_set:
+            _cpu_adam.set_num_threads(n)
+            self._adam_threads_set = n
 
     def init_grad_slots(self, unit_sizes: Dict[int, int], fallback_depth: int = 3) -> None:
         """One pinned slot per unit; if the host cannot pin that much (the
@@ -1161,6 +1208,7 @@ class LayerRuntimeState(nn.Module):
                 dense = torch.zeros(V, H, dtype=rows.dtype)
                 dense[ids] = rows
                 rt.capture[self.layer_idx] = (dense.view(-1), self._cpu_params_flat.clone())
+            rt.set_adam_threads()
             with self.update_lock:
                 if self.layer_optimizer is not None:
                     self.layer_optimizer.step_rows(self.layer_idx, row_slot, rows,
@@ -1192,6 +1240,7 @@ class LayerRuntimeState(nn.Module):
             if rt.capture is not None:
                 rt.capture[self.layer_idx] = (rt.grad_ring.slots[slot][:self.total_size].clone(),
                                               self._cpu_params_flat.clone())
+            rt.set_adam_threads()
             with self.update_lock:
                 if self.layer_optimizer is not None:
                     # The fp32 masters are passed explicitly: this thread never

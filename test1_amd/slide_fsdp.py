@@ -294,6 +294,8 @@ class SlideFSDP(nn.Module):
                         nvme_offload_fraction=config.optimizer_nvme_offload_fraction,
                         offload_dir=config.optimizer_offload_dir, prefetch=True)
         opt.cpu_adam.set_num_threads(adam_threads())
+        self.runtime.adam_threads = adam_threads()
+        self.runtime._adam_threads_set = self.runtime.adam_threads
         # Updates run in next-forward order as gradients land, not in the
         # reference's backward order: take each update's bias corrections as
         # the reference's order gives them.

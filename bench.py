@@ -232,7 +232,7 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
                           optimizer_offload_dir=os.path.join(args.offload_dir, "optimizer"),
                           enable_activation_checkpoint=not args.no_activation_checkpoint)
     sf = SlideFSDP(model, cfg, d2h_engine=d2h_engine, h2d_format=h2d_format, resident_layers=resident_layers,
-                   fused_cross_entropy=args.fused_ce)
+                   fused_cross_entropy=args.fused_ce, update_piece_elems=args.piece_elems)
     uses_storage = args.ac_offload == "nvme" or args.opt_nvme_fraction > 0
     log(f"[bench] SlideFSDP ({h2d_format} H2D, {sf.resident_layers} resident decoders, {d2h_engine} D2H) "
         f"ready in {time.time() - t0:.1f}s")
@@ -417,6 +417,9 @@ def main():
                     help="checkpoint inputs to pinned host slots, to files on local storage, or kept on the GPU")
     ap.add_argument("--opt-nvme-fraction", type=float, default=0.0,
                     help="AdamW moments on local storage: exp_avg above 0, both moments above 0.5")
+    ap.add_argument("--piece-elems", type=int, default=0,
+                    help="elements per piece of a unit's update (gradients back, AdamW and copy to the device "
+                         "run piece by piece, one cast per unit), e.g. 67108864; 0: whole units")
     ap.add_argument("--offload-dir", default="/tmp/sf_offload",
                     help="directory of the storage-offload files (removed as they are opened)")
     args = ap.parse_args()
@@ -503,6 +506,7 @@ def main():
                    "h2d_format": args.h2d_format, "resident_layers": r["resident_layers"],
                    "d2h_engine": args.d2h_engine, "fused_cross_entropy": args.fused_ce,
                    "stage_after_update": r["stage_after_update"],
+                   "update_piece_elems": args.piece_elems,
                    "row_sparse_embedding": r["row_sparse_embedding"],
                    "ac_offload_mode": args.ac_offload,
                    "activation_checkpoint": not args.no_activation_checkpoint,

@@ -39,13 +39,15 @@ plus the fp32 staging ring (``depth`` chunks of ``chunk_elems``) with fp32 H2D.
 
 from __future__ import annotations
 
+import bisect
 import heapq
+import itertools
 import queue
 import threading
 import time
 from collections import OrderedDict, deque
 from concurrent.futures import Future
-from typing import Any, Callable, Dict, List, Optional, Tuple
+from typing import Any, Callable, Dict, List, Optional, Sequence, Tuple
 
 import torch
 import torch.nn as nn
@@ -109,6 +111,39 @@ def _backlog(copies: deque) -> int:
     return len(copies)
 
 
+def split_into_pieces(sizes: Sequence[int], piece_elems: int) -> List[Tuple[int, int]]:
+    """Flat ``[a, b)`` ranges of about ``piece_elems`` elements covering
+    tensors of ``sizes`` laid out back to back.  A boundary inside a tensor
+    falls a multiple of 16 elements after that tensor's start, so a host
+    AdamW call per piece gives every element the arithmetic of the
+    whole-tensor call (16-wide vector body, scalar tail at the end)."""
+    total = int(sum(sizes))
+    if total == 0:
+        return []
+    n = max(1, -(-total // int(piece_elems))) if piece_elems and piece_elems > 0 else 1
+    starts = list(itertools.accumulate([0] + [int(s) for s in sizes[:-1]]))
+    bounds = [0]
+    for k in range(1, n):
+        c = total * k // n
+        i = bisect.bisect_right(starts, c) - 1
+        c = starts[i] + (c - starts[i]) // 16 * 16
+        if c > bounds[-1]:
+            bounds.append(c)
+    bounds.append(total)
+    return list(zip(bounds[:-1], bounds[1:]))
+
+
+def overlap_ranges(spans: Sequence[Tuple[int, int]], a: int, b: int) -> List[Tuple[int, int, int]]:
+    """``(index, lo, hi)`` for each span ``(offset, size)`` that overlaps the
+    flat range ``[a, b)``; ``lo``/``hi`` are relative to the span's offset."""
+    out = []
+    for i, (off, size) in enumerate(spans):
+        lo, hi = max(a, off) - off, min(b, off + size) - off
+        if hi > lo:
+            out.append((i, lo, hi))
+    return out
+
+
 class _StageTicket:
     """Chunks of one unit's master in flight through the staging ring."""
 
@@ -153,6 +188,12 @@ class H2DStager:
         # Completion event of the last cast issued (see fence_after_casts).
         self.last_cast_done: Optional[torch.cuda.Event] = None
         self._copies: deque = deque()   # completion events of issued copies, in stream order
+        # Piece streams (``open_pieces``): two device slots used in turn and
+        # the completion of the cast that last read each.
+        self._piece_lock = threading.Lock()
+        self._piece_bufs: List[Optional[torch.Tensor]] = [None, None]
+        self._piece_free: List[Optional[torch.cuda.Event]] = [None, None]
+        self._piece_next = 0
 
     def backlog(self) -> int:
         """Host-to-device copies issued and not yet complete."""
@@ -237,6 +278,117 @@ class H2DStager:
         """``begin`` and ``finish`` in one call."""
         return self.finish(self.begin(host_f32), dst_bf16, wait_event)
 
+    def open_pieces(self, host_f32: torch.Tensor, dst_bf16: torch.Tensor, wait_event: Optional[torch.cuda.Event],
+                    pieces: Sequence[Tuple[int, int]]) -> "_StagerPieces":
+        """Stage ``host_f32`` into ``dst_bf16`` with its copy issued one flat
+        piece ``[a, b)`` at a time, each when the caller ``push``-es it (after
+        writing it), so the copy of the first pieces runs while later ones are
+        still being produced; ``close`` casts the unit in one launch once its
+        last piece has landed.  The pieces land in one of two device slots of
+        their own (allocated on first use, used in turn), not in the ring, so
+        ring stagings run between pushes.  One piece stream is open at a
+        time."""
+        self._piece_lock.acquire()
+        try:
+            return _StagerPieces(self, host_f32, dst_bf16, wait_event, pieces)
+        except BaseException:
+            self._piece_lock.release()
+            raise
+
+    def _piece_slot(self, n: int) -> Tuple[int, torch.Tensor]:
+        k = self._piece_next
+        self._piece_next ^= 1
+        if self._piece_bufs[k] is None or self._piece_bufs[k].numel() < n:
+            if self._piece_bufs[k] is not None:
+                # growing: nothing may still copy into or cast from the old slot
+                self.h2d_stream.synchronize()
+                self.cast_stream.synchronize()
+            self._piece_bufs[k] = None
+            self._piece_bufs[k] = torch.empty(max(n, self.chunk), dtype=torch.float32, device=self.buf.device)
+            self._piece_free[k] = None
+        return k, self._piece_bufs[k]
+
+
+class _StagerPieces:
+    """One unit staged by an ``H2DStager``: copies piece by piece, one cast."""
+
+    def __init__(self, stager: H2DStager, host: torch.Tensor, dst: torch.Tensor,
+                 wait_event: Optional[torch.cuda.Event], pieces: Sequence[Tuple[int, int]]):
+        n = host.numel()
+        if dst.numel() < n:
+            raise ValueError("H2DStager.open_pieces: destination smaller than source")
+        bounds = [0] + [b for _, b in pieces]
+        if not pieces or any(pieces[i][0] != bounds[i] or pieces[i][1] <= pieces[i][0]
+                             for i in range(len(pieces))) or bounds[-1] != n:
+            raise ValueError("H2DStager.open_pieces: the pieces must cover the source in order")
+        self.stager, self.host, self.dst, self.wait_event = stager, host, dst, wait_event
+        self.pieces = list(pieces)
+        self.k, self.buf = stager._piece_slot(n)
+        self.pushed = 0
+        self.last_copy: Optional[torch.cuda.Event] = None
+        self.open = True
+
+    def push(self, j: int) -> None:
+        if not self.open or j != self.pushed:
+            raise RuntimeError(f"H2DStager pieces: piece {j} pushed out of order (next is {self.pushed})")
+        st = self.stager
+        a, b = self.pieces[j]
+        if j == 0 and st._piece_free[self.k] is not None:
+            st.h2d_stream.wait_event(st._piece_free[self.k])   # the slot's previous cast has read it
+        timing = st.copy_timing is not None
+        if timing:
+            t0 = torch.cuda.Event(enable_timing=True)
+            t0.record(st.h2d_stream)
+        kernels.memcpy_async(self.buf[a:b], self.host[a:b], st.h2d_stream)
+        copied = torch.cuda.Event(enable_timing=True) if timing else _new_event()
+        copied.record(st.h2d_stream)
+        if timing:
+            st.copy_timing.append((t0, copied, (b - a) * 4))
+        self.pushed += 1
+        if self.pushed == len(self.pieces):
+            self.last_copy = copied
+            # the backlog counts units: queued until the unit's last copy is done
+            st._copies.append(copied)
+            if len(st._copies) > 64:
+                _backlog(st._copies)
+
+    def close(self) -> torch.cuda.Event:
+        """Cast the unit (after its last copy and the unit's ``ready`` event);
+        returns the cast's completion event."""
+        if not self.open or self.pushed != len(self.pieces):
+            raise RuntimeError(f"H2DStager pieces: {self.pushed} of {len(self.pieces)} pieces pushed")
+        st = self.stager
+        try:
+            n = self.host.numel()
+            if self.wait_event is not None:
+                st.cast_stream.wait_event(self.wait_event)
+            st.cast_stream.wait_event(self.last_copy)
+            timing = st.cast_timing is not None
+            if timing:
+                c0 = torch.cuda.Event(enable_timing=True)
+                c0.record(st.cast_stream)
+            kernels.cast_f32_bf16_(self.dst[:n], self.buf[:n], st.cast_stream)
+            freed = torch.cuda.Event(enable_timing=True) if timing else _new_event()
+            freed.record(st.cast_stream)
+            if timing:
+                st.cast_timing.append((c0, freed, n))
+            st._piece_free[self.k] = freed
+            st.last_cast_done = freed
+            return freed
+        finally:
+            self._release()
+
+    def abort(self) -> None:
+        """Give the stream up without casting (the unit is staged whole later);
+        copies already issued finish into the slot, ahead of its next user's on
+        the same stream."""
+        if self.open:
+            self._release()
+
+    def _release(self) -> None:
+        self.open = False
+        self.stager._piece_lock.release()
+
 
 class BF16Loader:
     """Pinned bf16 host copy -> device bf16 unit: one DMA per unit, no cast.
@@ -282,6 +434,57 @@ class BF16Loader:
     def backlog(self) -> int:
         """Host-to-device copies issued and not yet complete."""
         return _backlog(self._copies)
+
+    def open_pieces(self, host_bf16: torch.Tensor, dst_bf16: torch.Tensor, wait_event: Optional[torch.cuda.Event],
+                    pieces: Sequence[Tuple[int, int]]) -> "_LoaderPieces":
+        """``load`` one flat piece ``[a, b)`` at a time, each when pushed."""
+        return _LoaderPieces(self, host_bf16, dst_bf16, wait_event, pieces)
+
+
+class _LoaderPieces:
+    """One unit loaded piece by piece by a ``BF16Loader``."""
+
+    def __init__(self, loader: BF16Loader, host: torch.Tensor, dst: torch.Tensor,
+                 wait_event: Optional[torch.cuda.Event], pieces: Sequence[Tuple[int, int]]):
+        if dst.numel() < host.numel():
+            raise ValueError("BF16Loader.open_pieces: destination smaller than source")
+        if any(b <= a for a, b in pieces) or (pieces and pieces[-1][1] > host.numel()):
+            raise ValueError("BF16Loader.open_pieces: a piece is empty or outside the source")
+        self.loader, self.host, self.dst, self.wait_event = loader, host, dst, wait_event
+        self.pieces = list(pieces)
+        self.pushed = 0
+        self.done: Optional[torch.cuda.Event] = None
+
+    def push(self, j: int) -> None:
+        if j != self.pushed:
+            raise RuntimeError(f"BF16Loader pieces: piece {j} pushed out of order (next is {self.pushed})")
+        ld = self.loader
+        a, b = self.pieces[j]
+        if j == 0 and self.wait_event is not None:
+            ld.h2d_stream.wait_event(self.wait_event)
+        timing = ld.copy_timing is not None
+        if timing:
+            t0 = torch.cuda.Event(enable_timing=True)
+            t0.record(ld.h2d_stream)
+        kernels.memcpy_async(self.dst[a:b], self.host[a:b], ld.h2d_stream)
+        ev = torch.cuda.Event(enable_timing=True) if timing else _new_event()
+        ev.record(ld.h2d_stream)
+        if timing:
+            ld.copy_timing.append((t0, ev, (b - a) * 2))
+        if j == len(self.pieces) - 1:
+            ld._copies.append(ev)
+            if len(ld._copies) > 64:
+                _backlog(ld._copies)
+            self.done = ev
+        self.pushed += 1
+
+    def close(self) -> torch.cuda.Event:
+        if self.pushed != len(self.pieces) or self.done is None:
+            raise RuntimeError(f"BF16Loader pieces: {self.pushed} of {len(self.pieces)} pieces pushed")
+        return self.done
+
+    def abort(self) -> None:
+        """Nothing to give back: the unit is loaded whole later."""
 
 
 class GradStagingRing:
@@ -540,12 +743,14 @@ class _UpdateReady:
 
     def query(self) -> bool:
         try:
-            return self.grads_ready.query() and self.optimizer.states_ready(self.unit)
+            return ((self.grads_ready is None or self.grads_ready.query())
+                    and self.optimizer.states_ready(self.unit))
         except BaseException:
             return True  # a failed copy or read: the update runs and reports it
 
     def synchronize(self) -> None:
-        self.grads_ready.synchronize()
+        if self.grads_ready is not None:
+            self.grads_ready.synchronize()
 
 
 def _no_slot() -> None:
@@ -615,6 +820,11 @@ class StreamingRuntime:
         # Queue priority of a unit's update (lower runs first); the model sets
         # it to the unit's position in the next forward.
         self.update_priority: Callable[[int], int] = lambda unit: unit
+        # Elements per piece of a unit's update (0: whole units).  Gradients
+        # come back in pieces, the host AdamW starts on the first piece that
+        # has landed, and each updated piece is copied to the device while
+        # the next one is being updated.
+        self.piece_elems = 0
         self.wait_timeout = wait_timeout
         self.trace: Optional[List[Tuple]] = None
         self._trace_lock = threading.Lock()
@@ -732,6 +942,8 @@ class LayerRuntimeState(nn.Module):
         # thread (``stage_for_next_forward``): (unit, copy-and-cast event).
         self._prefetched: Optional[Tuple[Dict[str, Any], torch.cuda.Event]] = None
         self._prefetch_lock = threading.Lock()
+        self._plan_key: Optional[int] = None
+        self._plan = None
         self._post_called = False
         self._bwd_armed = False
         self._bwd_compute_done = False
@@ -1007,6 +1219,42 @@ class LayerRuntimeState(nn.Module):
         self._current_gpu_cache = None
         self._release_unit(unit)
 
+    def _piece_plan(self):
+        """``(bounds, param_ranges)``: the flat ``[a, b)`` pieces this unit's
+        update runs in and, per piece, its ``(param, lo, hi)`` ranges; None
+        when the unit is one piece."""
+        pe = int(self.runtime.piece_elems or 0)
+        if self._plan_key != pe:
+            named = list(self._named())
+            spans = [(off, size) for (_, (off, _, size)), _ in named]
+            plan = None
+            if pe > 0 and all(off == sum(sz for _, sz in spans[:i]) for i, (off, _) in enumerate(spans)):
+                bounds = split_into_pieces([sz for _, sz in spans], pe)
+                if len(bounds) > 1:
+                    params = [p for _, p in named]
+                    plan = (bounds, [[(params[i], lo, hi) for i, lo, hi in overlap_ranges(spans, a, b)]
+                                     for a, b in bounds])
+            self._plan_key, self._plan = pe, plan
+        return self._plan
+
+    def _open_staging_pieces(self, bounds):
+        """``(unit, piece stream)`` to stage the unit's own buffer piece by
+        piece during its update, or None where ``stage_for_next_forward``
+        would not stage it."""
+        unit = self._own_unit
+        if unit is None or self._current_gpu_cache is not None or self.row_sparse:
+            return None
+        stager = self.runtime.stager
+        if getattr(stager, "pieces_disabled", False):
+            return None
+        host = self._cpu_params_bf16 if self._cpu_params_bf16 is not None else self._cpu_params_flat
+        try:
+            return unit, stager.open_pieces(host, unit["param"], unit["ready"], bounds)
+        except torch.cuda.OutOfMemoryError:
+            # no room for the piece slots: stage whole units after their update
+            stager.pieces_disabled = True
+            return None
+
     def _d2h_task(self, slot, grads, missing, grad_ready, cast_fence) -> None:
         """Offload thread: copy this unit's gradients into a host slot, then
         queue the update.  ``slot`` is the ring slot the thread's gate took,
@@ -1031,10 +1279,22 @@ class LayerRuntimeState(nn.Module):
                 # worker thread, then hand the copy to the engine.
                 grad_ready.synchronize()
                 rt.mark("grad_ready", self.layer_idx)
-                handle = kernels.dma_copy_d2h(pairs)
+                plan = self._piece_plan()
+                if plan is None:
+                    handles = [kernels.dma_copy_d2h(pairs)]
+                else:
+                    # one copy per piece, in update order: the update starts
+                    # once the first has landed
+                    spans = [(off, g.numel()) for g, off in grads]
+                    handles = []
+                    for a, b in plan[0]:
+                        sub = [(grads[i][0][lo:hi], host[grads[i][1] + lo:grads[i][1] + hi])
+                               for i, lo, hi in overlap_ranges(spans, a, b)]
+                        handles.append(kernels.dma_copy_d2h(sub) if sub else None)
                 rt.mark("dma_issued", self.layer_idx)
                 done = None
-                dma_ready = kernels.DmaReady(handle)
+                dma_ready = [None if h is None else kernels.DmaReady(h) for h in handles]
+                handle = handles
             else:
                 rt.d2h_stream.wait_event(grad_ready)
                 if cast_fence is not None:
@@ -1065,7 +1325,10 @@ class LayerRuntimeState(nn.Module):
         # waited for; the caching allocator cannot hand them out before then.
         keep = grads if handle is not None else None
         del grads, pairs
-        ready = done if handle is None else dma_ready
+        if handle is None:
+            ready = done
+        else:
+            ready = next((d for d in dma_ready if d is not None), None)
         self._update_future = rt.update_executor.submit(rt.update_priority(self.layer_idx), self._do_update,
                                                         slot, done, missing, None if handle is None else dma_ready,
                                                         keep, nbytes, ready=self._update_ready(ready))
@@ -1222,39 +1485,81 @@ class LayerRuntimeState(nn.Module):
 
     def _do_update(self, slot: int, d2h_done: Optional[torch.cuda.Event], missing: List[Tuple[int, int]],
                    dma_ready=None, keep=None, nbytes: int = 0) -> bool:
+        """Update thread: the unit's AdamW from its host gradient slot, then
+        (own units) its staging for the next forward.  ``dma_ready`` holds the
+        SDMA copies of the gradients, one per piece of ``_piece_plan`` (or one
+        for the unit); piece ``j`` is updated once copy ``j`` has landed, and
+        its new weights are copied to the device while piece ``j + 1`` is
+        updated (the cast follows the unit's last piece)."""
         rt = self.runtime
+        chunks = list(dma_ready) if dma_ready is not None else []
+        state = {"waited": 0, "t0": None, "t1": None}
+
+        def wait_chunks(upto: int) -> None:
+            while state["waited"] < len(chunks) and state["waited"] <= upto:
+                ch = chunks[state["waited"]]
+                state["waited"] += 1
+                if ch is None:
+                    continue
+                t0, t1 = ch.release()
+                if t1 > t0:
+                    state["t0"] = t0 if state["t0"] is None else min(state["t0"], t0)
+                    state["t1"] = t1 if state["t1"] is None else max(state["t1"], t1)
+                if state["waited"] == 1:
+                    rt.mark("dma_done", self.layer_idx)
+
         try:
             rt.mark("update_start", self.layer_idx)
-            if dma_ready is not None:
-                t0, t1 = dma_ready.release()
-                rt.mark("dma_done", self.layer_idx)
-                del keep
-                if rt.d2h_timing is not None and t1 > t0:
-                    rt.d2h_timing.append(("interval_ns", t0, t1, nbytes))
-            else:
+            if d2h_done is not None:
                 d2h_done.synchronize()
+            plan = self._piece_plan() if self.layer_optimizer is not None else None
+            if plan is None or len(chunks) not in (0, len(plan[0])):
+                wait_chunks(len(chunks))
             for off, size in missing:
                 # a parameter that received no gradient: zeros, as the zeroed
-                # grad buffer of the reference gives it (layer_state.py:297)
+                # grad buffer of the reference gives it (layer_state.py:297);
+                # no copy writes these ranges
                 rt.grad_ring.slots[slot][off:off + size].zero_()
-            if rt.capture is not None:
-                rt.capture[self.layer_idx] = (rt.grad_ring.slots[slot][:self.total_size].clone(),
-                                              self._cpu_params_flat.clone())
-            rt.set_adam_threads()
-            with self.update_lock:
-                if self.layer_optimizer is not None:
-                    # The fp32 masters are passed explicitly: this thread never
-                    # reads param.data, which the autograd thread may be
-                    # rebinding at the same time.
-                    self.layer_optimizer.step_with_grad_views(self.layer_idx, self._grad_views(rt.grad_ring.slots[slot]),
-                                                              param_views=self._master_views(),
-                                                              bf16_views=self._bf16_views())
+            master_before = self._cpu_params_flat.clone() if rt.capture is not None else None
+            staging = self._open_staging_pieces(plan[0]) if plan is not None and rt.stage_after_update else None
+            try:
+                rt.set_adam_threads()
+                with self.update_lock:
+                    if self.layer_optimizer is not None:
+                        # The fp32 masters are passed explicitly: this thread
+                        # never reads param.data, which the autograd thread may
+                        # be rebinding at the same time.
+                        self.layer_optimizer.step_with_grad_views(
+                            self.layer_idx, self._grad_views(rt.grad_ring.slots[slot]),
+                            param_views=self._master_views(), bf16_views=self._bf16_views(),
+                            pieces=None if plan is None else plan[1],
+                            before_piece=None if plan is None else wait_chunks,
+                            after_piece=None if staging is None else staging[1].push)
+            except BaseException:
+                if staging is not None:
+                    staging[1].abort()
+                raise
             rt.mark("adam_done", self.layer_idx)
-            if rt.stage_after_update:
+            if staging is not None:
+                done = staging[1].close()
+                with self._prefetch_lock:
+                    self._prefetched = (staging[0], done)
+                rt.mark("staged_after_update", self.layer_idx)
+            elif rt.stage_after_update:
                 self.stage_for_next_forward()
+            if master_before is not None:
+                wait_chunks(len(chunks))
+                rt.capture[self.layer_idx] = (rt.grad_ring.slots[slot][:self.total_size].clone(), master_before)
         finally:
-            rt.grad_ring.release(slot)
-            self.update_finished.set()
+            try:
+                # every gradient copy has landed before the slot is handed back
+                wait_chunks(len(chunks))
+                del keep
+                if rt.d2h_timing is not None and state["t0"] is not None:
+                    rt.d2h_timing.append(("interval_ns", state["t0"], state["t1"], nbytes))
+                rt.grad_ring.release(slot)
+            finally:
+                self.update_finished.set()
         return True
 
     def update_params(self) -> None:

@@ -277,7 +277,8 @@ class LayerAdam:
     def step_with_grad_views(self, layer_idx: Optional[int] = None,
                              grad_views: Optional[Dict[torch.nn.Parameter, torch.Tensor]] = None, closure=None,
                              param_views: Optional[Dict[torch.nn.Parameter, torch.Tensor]] = None,
-                             bf16_views: Optional[Dict[torch.nn.Parameter, torch.Tensor]] = None):
+                             bf16_views: Optional[Dict[torch.nn.Parameter, torch.Tensor]] = None,
+                             pieces=None, before_piece=None, after_piece=None):
         """Update one unit from per-parameter grad views into a host staging
         buffer (reference layer_adam.py:358-425).  bf16 views are read in place.
 
@@ -285,7 +286,18 @@ class LayerAdam:
         update per parameter; without it ``p.data`` is updated, which must then
         be the host master, as in the reference.  ``bf16_views`` (not in the
         reference) names bf16 host tensors that receive the rounded params in
-        the same pass."""
+        the same pass.
+
+        ``pieces`` (not in the reference): a list of pieces, each a list of
+        ``(param, lo, hi)`` flat element ranges, together covering the unit
+        in order.  With ``reference_order`` the update runs piece by piece,
+        calling ``before_piece(j)`` before piece ``j`` (e.g. to wait for its
+        gradients) and ``after_piece(j)`` after it (e.g. to send its new
+        weights on).  Every ``lo`` that is not a parameter's start must be a
+        multiple of 16: each element then gets the same vector or tail
+        arithmetic as in the whole-tensor call, so the bits are the same.
+        Without ``reference_order`` the unit is updated at once, between all
+        ``before_piece`` and all ``after_piece`` calls."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -293,6 +305,15 @@ class LayerAdam:
         groups = self._groups_to_update(layer_idx)
         self._pre_step(layer_idx)
         try:
+            if pieces is not None and self.reference_order and len(groups) == 1:
+                groups[0]["step"] += 1
+                self._step_pieces(groups[0], grad_views, param_views, bf16_views, pieces,
+                                  before_piece, after_piece)
+                return loss
+            n_pieces = 0 if pieces is None else len(pieces)
+            if before_piece is not None:
+                for j in range(n_pieces):
+                    before_piece(j)
             for group in groups:
                 group["step"] += 1
                 for p in group["params"]:
@@ -302,9 +323,50 @@ class LayerAdam:
                         continue
                     self._update_param(group, p, grad, None if param_views is None else param_views[p],
                                        None if bf16_views is None else bf16_views[p])
+            if after_piece is not None:
+                for j in range(n_pieces):
+                    after_piece(j)
         finally:
             self._post_step(layer_idx)
         return loss
+
+    def _step_pieces(self, group, grad_views, param_views, bf16_views, pieces, before_piece, after_piece) -> None:
+        beta1, beta2 = group["betas"]
+        covered: Dict[Any, int] = {}
+        hps: Dict[Any, Any] = {}
+        for j, piece in enumerate(pieces):
+            if before_piece is not None:
+                before_piece(j)
+            for p, lo, hi in piece:
+                grad = grad_views.get(p) if grad_views else None
+                if grad is None:
+                    if lo == 0:
+                        print(f"Warning: no gradient view for a parameter of shape {tuple(p.shape)}; skipped")
+                    continue
+                if covered.get(p, 0) != lo or hi <= lo or hi > p.numel() or (hi < p.numel() and hi % 16):
+                    raise ValueError(f"LayerAdam: piece range [{lo}, {hi}) of a parameter of {p.numel()} "
+                                     "elements does not continue the previous one on a 16-element boundary")
+                covered[p] = hi
+                data = p.data if param_views is None else param_views[p]
+                if data.device.type != "cpu":
+                    raise RuntimeError(f"LayerAdam: unsupported device type {data.device.type}")
+                if data.numel() != grad.numel():
+                    raise ValueError("LayerAdam: parameter and gradient sizes differ")
+                hp = hps.get(p)
+                if hp is None:
+                    hp = hps[p] = _cpu_adam.hparams_in_reference_order(
+                        group["step"], group["lr"], beta1, beta2, group["eps"], group["weight_decay"],
+                        group["bias_correction"], self.defaults["adamw_mode"], self._first_of_step(group, p))
+                st = self.state[p]
+                pb = None if bf16_views is None else bf16_views[p].view(-1)[lo:hi]
+                _cpu_adam.adam_step(data.view(-1)[lo:hi], grad.reshape(-1)[lo:hi],
+                                    st["exp_avg"].view(-1)[lo:hi], st["exp_avg_sq"].view(-1)[lo:hi], hp,
+                                    params_bf16=pb)
+            if after_piece is not None:
+                after_piece(j)
+        for p in group["params"]:
+            if grad_views and grad_views.get(p) is not None and covered.get(p, 0) != p.numel():
+                raise ValueError(f"LayerAdam: the pieces leave part of a parameter of {p.numel()} elements out")
 
     @torch.no_grad()
     def step_rows(self, layer_idx: int, row_slot: torch.Tensor, rows: torch.Tensor,

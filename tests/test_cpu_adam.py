@@ -226,9 +226,11 @@ def test_row_sparse_update_rejects_bad_shapes():
     cpu_adam.destroy_adam(82)
 
 
-def _run_layer_adam(order_fn, reference_order, steps=6, seed=3):
+def _run_layer_adam(order_fn, reference_order, steps=6, seed=3, piece_elems=None, calls=None):
     """Units 0 (a [64, 32] table, row-sparse updates) and 1..4 (several
-    params each), stepped ``steps`` times in the order ``order_fn(step)``."""
+    params each), stepped ``steps`` times in the order ``order_fn(step)``.
+    With ``piece_elems``, units 1..4 are updated in pieces of that size (the
+    runtime's split), and ``calls`` collects the piece callbacks."""
     g = torch.Generator().manual_seed(seed)
     shapes = {1: [(48, 32), (32,)], 2: [(40, 16), (16,), (16,)], 3: [(33, 7)], 4: [(64, 16), (64,)]}
     units = {0: [torch.nn.Parameter(torch.randn(64, 32, generator=g) * 0.02)]}
@@ -247,9 +249,27 @@ def _run_layer_adam(order_fn, reference_order, steps=6, seed=3):
                 row_slot = torch.full((64,), -1, dtype=torch.int64)
                 row_slot[ids] = torch.arange(ids.numel())
                 opt.step_rows(0, row_slot, grads[0][0][ids].contiguous(), units[0][0].data)
-            else:
+            elif piece_elems is None:
                 opt.step_with_grad_views(u, dict(zip(units[u], grads[u])))
+            else:
+                pieces = _pieces_of(units[u], piece_elems)
+                log = []
+                opt.step_with_grad_views(u, dict(zip(units[u], grads[u])), pieces=pieces,
+                                         before_piece=lambda j: log.append(("before", j)),
+                                         after_piece=lambda j: log.append(("after", j)))
+                if calls is not None:
+                    calls.append((u, len(pieces), log))
     return units, opt
+
+
+def _pieces_of(params, piece_elems):
+    from test1_amd.layer_state import overlap_ranges, split_into_pieces
+
+    sizes = [p.numel() for p in params]
+    offs = [sum(sizes[:i]) for i in range(len(sizes))]
+    spans = list(zip(offs, sizes))
+    return [[(params[i], lo, hi) for i, lo, hi in overlap_ranges(spans, a, b)]
+            for a, b in split_into_pieces(sizes, piece_elems)]
 
 
 def test_reference_order_scalars_give_the_reference_bits_in_any_order():
@@ -277,3 +297,72 @@ def test_reference_order_scalars_give_the_reference_bits_in_any_order():
             assert torch.equal(ai, c.data.view(torch.int32)), f"unit {u}"
             differs |= not torch.equal(ai, d.data.view(torch.int32))
     assert differs, "the stateful update should depend on the call order"
+
+
+def test_split_into_pieces_covers_the_layout_on_vector_boundaries():
+    """The runtime's piece split: contiguous cover of [0, total), at most
+    piece_elems + 15 per piece, and every boundary inside a tensor a multiple
+    of 16 elements after that tensor's start (zero-size and tiny tensors,
+    one tensor larger than several pieces)."""
+    import random
+
+    from test1_amd.layer_state import split_into_pieces
+
+    rng = random.Random(11)
+    cases = [([4096, 16777216, 4194304, 4194304, 16777216, 58720256, 58720256, 58720256, 4096], 1 << 26),
+             ([525336576, 4096], 1 << 26), ([231], 64), ([0, 5, 0, 1000, 17], 100), ([10], 0), ([], 64)]
+    cases += [([rng.choice([0, 1, 7, 16, 33, rng.randrange(1, 5000)]) for _ in range(rng.randrange(1, 9))],
+               rng.choice([16, 48, 100, 1000])) for _ in range(200)]
+    for sizes, pe in cases:
+        total = sum(sizes)
+        pieces = split_into_pieces(sizes, pe)
+        if total == 0:
+            assert pieces == []
+            continue
+        assert pieces[0][0] == 0 and pieces[-1][1] == total
+        assert all(b > a for a, b in pieces) and all(pieces[k][1] == pieces[k + 1][0] for k in range(len(pieces) - 1))
+        if pe > 0:
+            assert max(b - a for a, b in pieces) <= pe + 15
+            assert len(pieces) <= -(-total // pe)
+        else:
+            assert len(pieces) == 1
+        starts = [sum(sizes[:i]) for i in range(len(sizes))]
+        for a, _ in pieces[1:]:
+            inside = [o for o, n in zip(starts, sizes) if o < a < o + n]
+            assert all((a - o) % 16 == 0 for o in inside), (sizes, pe, a)
+
+
+def test_piecewise_update_gives_the_reference_bits():
+    """A unit updated piece by piece (as the runtime overlaps its gradient
+    copies and its staging with the update) gives the bits of the whole-unit
+    update pinned against the reference's compiled cpu_adam above, with the
+    reference's first-of-step scalars, over 6 steps; the callbacks run
+    before and after each piece in order.  Pieces of 48 and 100 elements
+    cut every multi-piece parameter in its vector body and leave the odd
+    tails (33 x 7 = 231 elements: tail 7) at the parameter's end."""
+    descending = lambda step: [4, 3, 2, 1, 0]  # noqa: E731
+    ref_units, ref_opt = _run_layer_adam(descending, reference_order=False)
+    for pe in (48, 100, 1 << 20):
+        calls = []
+        got_units, got_opt = _run_layer_adam(descending, reference_order=True, piece_elems=pe, calls=calls)
+        assert any(n > 1 for _, n, _ in calls) == (pe < 1000)
+        for _, n, log in calls:
+            assert log == [(k, j) for j in range(n) for k in ("before", "after")]
+        for u in ref_units:
+            for a, b in zip(ref_units[u], got_units[u]):
+                assert torch.equal(a.data.view(torch.int32), b.data.view(torch.int32)), (pe, u)
+                sa, sb = ref_opt.state[a], got_opt.state[b]
+                for k in ("exp_avg", "exp_avg_sq"):
+                    assert torch.equal(sa[k].view(torch.int32), sb[k].view(torch.int32)), (pe, u, k)
+
+
+def test_piecewise_update_rejects_ranges_off_the_vector_boundary():
+    """A piece split inside a parameter at a position that is not a multiple
+    of 16 would change which elements take the scalar tail: refused."""
+    p = torch.nn.Parameter(torch.zeros(100))
+    opt = LayerAdam(lr=1e-3, num_layer=1)
+    opt.reference_order = True
+    opt.add_layer_params(0, [p])
+    g = torch.zeros(100, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="16-element boundary"):
+        opt.step_with_grad_views(0, {p: g}, pieces=[[(p, 0, 40)], [(p, 40, 100)]])

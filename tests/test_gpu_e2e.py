@@ -91,6 +91,52 @@ def test_updates_match_oracle_bit_exact(dev, h2d_format, resident, d2h_engine, r
         resident_layers=resident, d2h_engine=d2h_engine, grad_ring_depth=ring, fused_cross_entropy=fused))
 
 
+# Updates in pieces of 40,000 elements: a decoder (590,336 elements) comes back, is
+# updated and is staged in 15 pieces, the output unit in 7, cutting parameters
+# inside their vector body.  (H2D format, resident decoders, D2H engine, slot ring, family)
+PIECE = 40000
+PIECE_MODES = [("fp32", L - 1, "sdma", None, "llama"), ("bf16", L - 1, "sdma", None, "llama"),
+               ("fp32", 0, "sdma", None, "qwen2"), ("fp32", L - 1, "kernel", 2, "llama"),
+               ("bf16", 0, "copy", None, "llama")]
+
+
+@pytest.mark.parametrize("h2d_format,resident,d2h_engine,ring,arch", PIECE_MODES)
+def test_piecewise_updates_match_oracle_bit_exact(dev, h2d_format, resident, d2h_engine, ring, arch):
+    """Units updated in pieces: each piece's gradients are waited for just
+    before its AdamW (SDMA: one copy per piece), and own units are copied to
+    the device piece by piece right after each piece's update, then cast in
+    one launch.  The updates, the staged weights the next forward computes
+    with, and the moments stay the oracle's, bit for bit, over 3 steps; with
+    every unit in a buffer of its own the staging really ran in pieces (at
+    least two decoders' worth of piece copies; each fp32 cast one whole unit)."""
+    sf = check_updates_against_oracle(dev, arch, h2d_format, {}, dict(
+        resident_layers=resident, d2h_engine=d2h_engine, grad_ring_depth=ring, update_piece_elems=PIECE),
+        keep=True, timing=True)
+    plan = sf.layer_states[1]._piece_plan()
+    assert plan is not None and len(plan[0]) == 15
+    assert len(sf.layer_states[L + 1]._piece_plan()[0]) == 7
+    st = sf.runtime.stager
+    sizes = [n // (4 if h2d_format == "fp32" else 2) for _, _, n in st.copy_timing]
+    assert sizes
+    if resident == L - 1:
+        # the first forward stages the units whole, later stagings run in pieces
+        # (a unit whose backward still holds it when its update starts is
+        # staged whole by the next forward instead)
+        assert sum(1 for n in sizes if n <= PIECE + 15) >= 2 * 15, sizes
+        if h2d_format == "fp32":
+            unit_sizes = {s.total_size for s in sf.layer_states}
+            assert {n for _, _, n in st.cast_timing} <= unit_sizes
+    sf.close()
+
+
+def test_piecewise_updates_with_moments_on_storage(dev, tmp_path):
+    """Updates in pieces with the first moment on local storage (2 buffers,
+    so moments are evicted and read back within every step): bit-exact
+    against the oracle over 3 steps."""
+    check_updates_against_oracle(dev, "llama", "fp32", storage_config(tmp_path, "cpu", 0.3),
+                                 dict(update_piece_elems=PIECE), nvme_buffers=2)
+
+
 # checkpoint offload mode, optimizer moments on storage (fraction), H2D format
 STORAGE_MODES = [("nvme", 0.0, "fp32"), ("cpu", 0.3, "fp32"), ("nvme", 0.8, "bf16")]
 
@@ -157,13 +203,15 @@ def test_fallback_slot_ring_when_per_unit_slots_do_not_fit(dev, monkeypatch):
 
 
 def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, nvme_buffers=None, shapes=None,
-                                 vocab=V, keep=False):
+                                 vocab=V, keep=False, timing=False):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model(arch, vocab=vocab)
     sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS,
                                           **cfg_kw),
                    wait_timeout=120, h2d_format=h2d_format, **sf_kw)
+    if timing:
+        sf.runtime.stager.cast_timing, sf.runtime.stager.copy_timing = [], []
     if nvme_buffers is not None and sf.layer_optimizer.offloader is not None:
         sf.layer_optimizer.offloader.n_buffers = nvme_buffers
     orc = oracle.LayerAdamOracle(lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
@@ -251,6 +299,13 @@ def test_loss_parity_with_non_offloaded_run(dev, h2d_format, resident, d2h_engin
     check_loss_parity(dev, arch, fused, {}, dict(h2d_format=h2d_format, resident_layers=resident,
                                                  d2h_engine=d2h_engine, grad_ring_depth=ring,
                                                  fused_cross_entropy=fused))
+
+
+def test_piecewise_loss_parity(dev):
+    """Updates in pieces against the non-offloaded run: first-step gradients
+    and 10 losses (no capture after the first step: every piece's AdamW
+    starts as soon as its own gradient copy has landed)."""
+    check_loss_parity(dev, "llama", False, {}, dict(resident_layers=L - 1, update_piece_elems=PIECE))
 
 
 @pytest.mark.parametrize("ac_mode,fraction,h2d_format", STORAGE_MODES)

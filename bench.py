@@ -106,7 +106,8 @@ def traffic_factor():
 
 def elapsed_stats(records):
     """(busy ms, total bytes or elements) from (start_event, end_event, amount)
-    records (summed) or ("interval_ns", start, end, amount) records of copies
+    or (KernelTimer, None, amount) records (summed) or ("interval_ns", start,
+    end, amount) records of copies
     that may overlap one another (busy = union of the intervals)."""
     ms = amt = 0.0
     intervals = []
@@ -114,6 +115,9 @@ def elapsed_stats(records):
         if len(r) == 4:
             intervals.append((r[1], r[2]))
             amt += r[3]
+        elif r[1] is None:   # a KernelTimer: the kernels' own start and end
+            ms += r[0].elapsed_ms()
+            amt += r[2]
         else:
             ms += r[0].elapsed_time(r[1])
             amt += r[2]
@@ -232,7 +236,8 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
                           optimizer_offload_dir=os.path.join(args.offload_dir, "optimizer"),
                           enable_activation_checkpoint=not args.no_activation_checkpoint)
     sf = SlideFSDP(model, cfg, d2h_engine=d2h_engine, h2d_format=h2d_format, resident_layers=resident_layers,
-                   fused_cross_entropy=args.fused_ce, update_piece_elems=args.piece_elems)
+                   fused_cross_entropy=args.fused_ce, update_piece_elems=args.piece_elems,
+                   cast_at_use=not args.cast_on_copy)
     uses_storage = args.ac_offload == "nvme" or args.opt_nvme_fraction > 0
     log(f"[bench] SlideFSDP ({h2d_format} H2D, {sf.resident_layers} resident decoders, {d2h_engine} D2H) "
         f"ready in {time.time() - t0:.1f}s")
@@ -286,6 +291,7 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
         "h2d": elapsed_stats(rt.stager.copy_timing), "d2h": elapsed_stats(rt.d2h_timing),
         "total_params": sf.total_params, "resident_layers": sf.resident_layers,
         "stage_after_update": sf.runtime.stage_after_update,
+        "cast_at_use": sf.runtime.cast_at_use,
         "row_sparse_embedding": sf.layer_states[0].row_sparse,
         "layer_numel": sum(p.numel() for p in sf.decoder_layers[0].parameters()),
         "output_numel": sum(p.numel() for p in sf.output_layer.parameters()),
@@ -301,7 +307,8 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
 def cast_alone(dev, n: int, reps: int = 20) -> dict:
     """The staging cast on an otherwise idle GPU, for context beside the
     in-pipeline figure: one ``n``-element launch repeated ``reps`` times
-    (after 3 warmups) on a stream of its own, timed with HIP events."""
+    (after 3 warmups) on a stream of its own, timed with HIP events stamped
+    around the kernel as in the pipeline figure."""
     import torch
 
     from test1_amd import kernels
@@ -311,13 +318,11 @@ def cast_alone(dev, n: int, reps: int = 20) -> dict:
     st = torch.cuda.Stream(device=dev)
     for _ in range(3):
         kernels.cast_f32_bf16_(dst, src, st)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for a, b in ev:
-        a.record(st)
-        kernels.cast_f32_bf16_(dst, src, st)
-        b.record(st)
+    timers = [kernels.KernelTimer() for _ in range(reps)]
+    for t in timers:
+        kernels.cast_f32_bf16_(dst, src, st, timer=t)
     st.synchronize()
-    ms = sum(a.elapsed_time(b) for a, b in ev) / reps
+    ms = sum(t.elapsed_ms() for t in timers) / reps
     gbs = 6 * n / (ms * 1e-3) / 1e9
     del src, dst
     torch.cuda.empty_cache()
@@ -420,6 +425,9 @@ def main():
     ap.add_argument("--piece-elems", type=int, default=0,
                     help="elements per piece of a unit's update (gradients back, AdamW and copy to the device "
                          "run piece by piece, one cast per unit), e.g. 67108864; 0: whole units")
+    ap.add_argument("--cast-on-copy", action="store_true",
+                    help="cast a unit staged after its update on the cast stream as soon as its copy lands "
+                         "(default: where the unit is next used, between the forward's kernels)")
     ap.add_argument("--offload-dir", default="/tmp/sf_offload",
                     help="directory of the storage-offload files (removed as they are opened)")
     args = ap.parse_args()
@@ -507,6 +515,7 @@ def main():
                    "d2h_engine": args.d2h_engine, "fused_cross_entropy": args.fused_ce,
                    "stage_after_update": r["stage_after_update"],
                    "update_piece_elems": args.piece_elems,
+                   "cast_at_use": r["cast_at_use"],
                    "row_sparse_embedding": r["row_sparse_embedding"],
                    "ac_offload_mode": args.ac_offload,
                    "activation_checkpoint": not args.no_activation_checkpoint,
@@ -526,9 +535,13 @@ def main():
             "avg_launch_ms": cast_ms / ncast if ncast else None,
             "algorithmic_bytes_per_launch": cast_bytes / ncast if ncast else None,
             "alone": alone,
-            "note": "achieved/frac: every cast of the timed steps, most of them beside the backward's "
-                    "GEMMs (units are staged right after their update); alone: one decoder layer's cast "
-                    "on an idle GPU after the timed steps",
+            "note": ("achieved/frac: every cast of the timed steps, "
+                     + ("each on the forward's stream right before the unit's forward (units are copied "
+                        "right after their update and cast where they are next used)"
+                        if r["cast_at_use"] else
+                        "most of them beside the backward's GEMMs (units are staged right after their "
+                        "update)")
+                     + "; alone: one decoder layer's cast on an idle GPU after the timed steps"),
         },
         "host_link": link_stats(r, args.steps),
         "model_tflops": {

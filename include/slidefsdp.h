@@ -30,6 +30,8 @@ extern "C" {
 
 /* An opaque HIP stream handle (hipStream_t); 0 is the null stream. */
 typedef void* sf_stream_t;
+/* A HIP event (hipEvent_t), created by sf_event_create. */
+typedef void* sf_event_t;
 
 /* Library-specific status codes, disjoint from hipError_t values. */
 #define SF_OK 0
@@ -76,6 +78,22 @@ int sf_abi_version(void);
  * runs in HBM after the fp32 master has been copied to the device. */
 int sf_cast_f32_bf16(const float* src, uint16_t* dst, size_t n,
                      sf_stream_t stream);
+
+/* sf_cast_f32_bf16 with `start` and `stop` (both or neither) stamped by the
+ * runtime at the start and end of the cast kernels' own dispatch, so that
+ * their elapsed time is the kernels' alone, whatever the stream waited for
+ * before them.  No counterpart in the reference (it has no device cast);
+ * used to measure the cast's HBM rate inside a training step. */
+int sf_cast_f32_bf16_timed(const float* src, uint16_t* dst, size_t n,
+                           sf_stream_t stream, sf_event_t start,
+                           sf_event_t stop);
+
+/* Timing events for sf_cast_f32_bf16_timed: create, destroy, and the
+ * milliseconds between two completed events (a HIP status, e.g. not ready,
+ * while either is pending).  No counterpart in the reference. */
+int sf_event_create(sf_event_t* ev);
+int sf_event_destroy(sf_event_t ev);
+int sf_event_elapsed_ms(sf_event_t start, sf_event_t stop, float* ms);
 
 /* The same cast over a table of segments (src: fp32, dst: bf16), for a
  * device layer buffer whose per-parameter views are not offset-identical

@@ -62,6 +62,10 @@ HIP_SIGNATURES = {
     "sf_error_string": [_i],
     "sf_abi_version": [],
     "sf_cast_f32_bf16": [_vp, _vp, _sz, _vp],
+    "sf_cast_f32_bf16_timed": [_vp, _vp, _sz, _vp, _vp, _vp],
+    "sf_event_create": [ctypes.POINTER(ctypes.c_void_p)],
+    "sf_event_destroy": [_vp],
+    "sf_event_elapsed_ms": [_vp, _vp, ctypes.POINTER(ctypes.c_float)],
     "sf_cast_scatter_f32_bf16": [ctypes.POINTER(SfSeg), _i, _vp],
     "sf_pack_b16": [ctypes.POINTER(SfSeg), _i, _vp, _i, _vp],
     "sf_unpack_b16": [_vp, ctypes.POINTER(SfSeg), _i, _i, _vp],

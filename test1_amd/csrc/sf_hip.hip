@@ -11,6 +11,7 @@
 //
 // The C ABI is declared in include/slidefsdp.h.
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <hsa/hsa.h>
 #include <hsa/hsa_ext_amd.h>
@@ -352,33 +353,76 @@ const char* sf_error_string(int status) {
 
 int sf_abi_version(void) { return 1; }
 
-int sf_cast_f32_bf16(const float* src, uint16_t* dst, size_t n, sf_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// The flat cast's launches: the vector kernel over the 8-element groups (when
+// both pointers are 16-byte aligned), then the scalar kernel over the rest.
+// ``start`` / ``stop`` (may be null) are stamped by the runtime around the
+// first and the last launch's own dispatch, so they time the kernels alone,
+// not what the stream waited for before them.
+int cast_launch(const float* src, uint16_t* dst, size_t n, hipStream_t st, hipEvent_t start, hipEvent_t stop) {
     if (n == 0) return SF_OK;
     if (src == nullptr || dst == nullptr) return SF_EINVAL;
     const uintptr_t s = reinterpret_cast<uintptr_t>(src), d = reinterpret_cast<uintptr_t>(dst);
     // fp32 source [s, s+4n) and bf16 destination [d, d+2n) must not overlap:
     // workgroups run in no particular order.
     if (s < d + 2 * n && d < s + 4 * n) return SF_EOVERLAP;
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const uint64_t n8 = ((s | d) & 15) == 0 ? n / kGroup : 0;
+    const uint64_t done = n8 * kGroup;
+    const bool tail = done < n;
     if (n8 > 0) {
         const uint64_t blocks = ceil_div(n8, uint64_t(kThreads) * kCastUnroll);
         if (blocks > kMaxBlocks) return SF_EINVAL;
-        hipLaunchKernelGGL(cast_flat_kernel, dim3(uint32_t(blocks)), dim3(kThreads), 0, st, src, dst, n8);
+        hipExtLaunchKernelGGL(cast_flat_kernel, dim3(uint32_t(blocks)), dim3(kThreads), 0, st, start,
+                              tail ? nullptr : stop, 0, src, dst, n8);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return int(e);
     }
-    const uint64_t done = n8 * kGroup;
-    if (done < n) {
+    if (tail) {
         const uint64_t rest = n - done;
         uint64_t blocks = ceil_div(rest, kThreads);
         if (blocks > 65536) blocks = 65536;
-        hipLaunchKernelGGL(cast_scalar_kernel, dim3(uint32_t(blocks)), dim3(kThreads), 0, st,
-                           src + done, dst + done, rest);
+        hipExtLaunchKernelGGL(cast_scalar_kernel, dim3(uint32_t(blocks)), dim3(kThreads), 0, st,
+                              n8 > 0 ? nullptr : start, stop, 0, src + done, dst + done, rest);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return int(e);
     }
     return SF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sf_cast_f32_bf16(const float* src, uint16_t* dst, size_t n, sf_stream_t stream) {
+    return cast_launch(src, dst, n, reinterpret_cast<hipStream_t>(stream), nullptr, nullptr);
+}
+
+int sf_cast_f32_bf16_timed(const float* src, uint16_t* dst, size_t n, sf_stream_t stream, sf_event_t start,
+                           sf_event_t stop) {
+    if ((start == nullptr) != (stop == nullptr)) return SF_EINVAL;
+    return cast_launch(src, dst, n, reinterpret_cast<hipStream_t>(stream), reinterpret_cast<hipEvent_t>(start),
+                       reinterpret_cast<hipEvent_t>(stop));
+}
+
+int sf_event_create(sf_event_t* ev) {
+    if (ev == nullptr) return SF_EINVAL;
+    hipEvent_t e = nullptr;
+    const int rc = hip_status(hipEventCreate(&e));
+    *ev = rc == SF_OK ? reinterpret_cast<sf_event_t>(e) : nullptr;
+    return rc;
+}
+
+int sf_event_destroy(sf_event_t ev) {
+    if (ev == nullptr) return SF_OK;
+    return hip_status(hipEventDestroy(reinterpret_cast<hipEvent_t>(ev)));
+}
+
+int sf_event_elapsed_ms(sf_event_t start, sf_event_t stop, float* ms) {
+    if (start == nullptr || stop == nullptr || ms == nullptr) return SF_EINVAL;
+    return hip_status(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(stop)));
 }
 
 int sf_cast_scatter_f32_bf16(const sf_seg* segs, int nsegs, sf_stream_t stream) {

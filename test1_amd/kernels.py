@@ -36,8 +36,41 @@ def _require_contig(t: torch.Tensor, what: str) -> None:
         raise ValueError(f"{what} must be contiguous")
 
 
-def cast_f32_bf16_(dst: torch.Tensor, src: torch.Tensor, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
-    """dst[:] = RNE-bf16(src), both flat-contiguous GPU tensors of equal numel."""
+class KernelTimer:
+    """A pair of HIP timing events that a launch stamps around its kernels'
+    own dispatch (``cast_f32_bf16_(..., timer=t)``): ``elapsed_ms`` is then
+    the kernels' duration alone, not what the stream waited for first."""
+
+    def __init__(self):
+        lib = _native.hip()
+        self._lib = lib
+        self.start, self.stop = ctypes.c_void_p(), ctypes.c_void_p()
+        _native.check(lib.sf_event_create(ctypes.byref(self.start)), "sf_event_create")
+        try:
+            _native.check(lib.sf_event_create(ctypes.byref(self.stop)), "sf_event_create")
+        except BaseException:
+            lib.sf_event_destroy(self.start)
+            raise
+
+    def elapsed_ms(self) -> float:
+        """Milliseconds from the first kernel's start to the last one's end
+        (the launch must have completed)."""
+        ms = ctypes.c_float(0.0)
+        _native.check(self._lib.sf_event_elapsed_ms(self.start, self.stop, ctypes.byref(ms)), "sf_event_elapsed_ms")
+        return float(ms.value)
+
+    def __del__(self):
+        lib = getattr(self, "_lib", None)
+        if lib is not None:
+            for ev in (getattr(self, "start", None), getattr(self, "stop", None)):
+                if ev is not None and ev.value:
+                    lib.sf_event_destroy(ev)
+
+
+def cast_f32_bf16_(dst: torch.Tensor, src: torch.Tensor, stream: Optional[torch.cuda.Stream] = None,
+                   timer: Optional[KernelTimer] = None) -> torch.Tensor:
+    """dst[:] = RNE-bf16(src), both flat-contiguous GPU tensors of equal numel.
+    With ``timer``, its events are stamped around the cast kernels."""
     if src.dtype != torch.float32 or dst.dtype != torch.bfloat16:
         raise TypeError(f"cast_f32_bf16_: need float32 -> bfloat16, got {src.dtype} -> {dst.dtype}")
     _require_cuda(src, "src")
@@ -46,10 +79,17 @@ def cast_f32_bf16_(dst: torch.Tensor, src: torch.Tensor, stream: Optional[torch.
     _require_contig(dst, "dst")
     if src.numel() != dst.numel():
         raise ValueError(f"cast_f32_bf16_: numel mismatch {src.numel()} vs {dst.numel()}")
-    _native.check(
-        _native.hip().sf_cast_f32_bf16(src.data_ptr(), dst.data_ptr(), src.numel(), _stream_ptr(stream)),
-        "sf_cast_f32_bf16",
-    )
+    if timer is None:
+        _native.check(
+            _native.hip().sf_cast_f32_bf16(src.data_ptr(), dst.data_ptr(), src.numel(), _stream_ptr(stream)),
+            "sf_cast_f32_bf16",
+        )
+    else:
+        _native.check(
+            _native.hip().sf_cast_f32_bf16_timed(src.data_ptr(), dst.data_ptr(), src.numel(), _stream_ptr(stream),
+                                                 timer.start, timer.stop),
+            "sf_cast_f32_bf16_timed",
+        )
     return dst
 
 

@@ -154,6 +154,51 @@ class _StageTicket:
         self.copied: List[torch.cuda.Event] = []
 
 
+class PendingCast:
+    """A unit's fp32 weights copied into a device slot, not yet cast: the
+    cast runs where the unit is next used (``H2DStager.cast_pending``)."""
+
+    __slots__ = ("slot", "copied", "n", "wait_event")
+
+    def __init__(self, slot: torch.Tensor, copied: torch.cuda.Event, n: int,
+                 wait_event: Optional[torch.cuda.Event]):
+        self.slot, self.copied, self.n, self.wait_event = slot, copied, n, wait_event
+
+
+class _SlotPool:
+    """Device fp32 buffers of whole units, keyed by size and reused.  A
+    buffer comes back with the event after which it may be overwritten.
+    Allocation stops at ``cap_bytes`` or at the first out-of-memory error;
+    callers then stage through the ring."""
+
+    def __init__(self, device: torch.device, cap_bytes: int):
+        self.device = device
+        self.cap_bytes = int(cap_bytes)
+        self.bytes = 0
+        self.disabled = False
+        self._free: Dict[int, List[Tuple[torch.Tensor, Optional[torch.cuda.Event]]]] = {}
+        self._lock = threading.Lock()
+
+    def take(self, n: int) -> Optional[Tuple[torch.Tensor, Optional[torch.cuda.Event]]]:
+        with self._lock:
+            free = self._free.get(n)
+            if free:
+                return free.pop()
+            if self.disabled or self.bytes + 4 * n > self.cap_bytes:
+                return None
+            try:
+                t = torch.empty(n, dtype=torch.float32, device=self.device)
+            except torch.cuda.OutOfMemoryError:
+                self.disabled = True
+                return None
+            self.bytes += 4 * n
+            return t, None
+
+    def give(self, t: torch.Tensor, free_event: Optional[torch.cuda.Event]) -> None:
+        with self._lock:
+            self._free.setdefault(t.numel(), []).append((t, free_event))
+
+
 class H2DStager:
     """Pinned fp32 master -> device bf16 unit, through a device fp32 ring.
 
@@ -166,10 +211,17 @@ class H2DStager:
                   chunk's copy) and issues the remaining copies as slots free.
     One unit is staged at a time: ``begin`` takes a lock that ``finish``
     releases.
+
+    Units staged right after their update (``copy_for_later``, ``open_pieces``)
+    instead land whole in a device fp32 slot of their own size, and their cast
+    can wait until the unit is next used (``cast_pending``, on the stream that
+    uses it): the cast then runs between that stream's kernels, with the HBM
+    to itself, instead of beside the backward's GEMMs.
     """
 
     def __init__(self, device: torch.device, chunk_elems: int, depth: int,
-                 h2d_stream: torch.cuda.Stream, cast_stream: torch.cuda.Stream):
+                 h2d_stream: torch.cuda.Stream, cast_stream: torch.cuda.Stream,
+                 slot_cap_bytes: int = 0):
         if depth < 1 or chunk_elems < 1:
             raise ValueError("H2DStager: depth and chunk_elems must be positive")
         self.chunk = int(chunk_elems)
@@ -181,19 +233,16 @@ class H2DStager:
         self.cast_stream = cast_stream
         self._lock = threading.Lock()
         # Optional instrumentation: when a list, each cast appends
-        # (start_event, end_event, n_elements); each copy appends
-        # (start_event, end_event, bytes) to copy_timing.
+        # (KernelTimer, None, n_elements), timed around the cast kernels
+        # themselves; each copy appends (start_event, end_event, bytes) to
+        # copy_timing.
         self.cast_timing: Optional[list] = None
         self.copy_timing: Optional[list] = None
         # Completion event of the last cast issued (see fence_after_casts).
         self.last_cast_done: Optional[torch.cuda.Event] = None
         self._copies: deque = deque()   # completion events of issued copies, in stream order
-        # Piece streams (``open_pieces``): two device slots used in turn and
-        # the completion of the cast that last read each.
-        self._piece_lock = threading.Lock()
-        self._piece_bufs: List[Optional[torch.Tensor]] = [None, None]
-        self._piece_free: List[Optional[torch.cuda.Event]] = [None, None]
-        self._piece_next = 0
+        # Whole-unit device slots of ``copy_for_later`` and ``open_pieces``.
+        self.slots = _SlotPool(device, slot_cap_bytes)
 
     def backlog(self) -> int:
         """Host-to-device copies issued and not yet complete."""
@@ -255,14 +304,12 @@ class H2DStager:
             for j, (off, c) in enumerate(t.chunks):
                 s = t.slots[j]
                 self.cast_stream.wait_event(t.copied[j])
-                if timing:
-                    c0 = torch.cuda.Event(enable_timing=True)
-                    c0.record(self.cast_stream)
-                kernels.cast_f32_bf16_(dst_bf16[off:off + c], self._slot(s, c), self.cast_stream)
-                freed = torch.cuda.Event(enable_timing=True) if timing else _new_event()
+                timer = kernels.KernelTimer() if timing else None
+                kernels.cast_f32_bf16_(dst_bf16[off:off + c], self._slot(s, c), self.cast_stream, timer=timer)
+                freed = _new_event()
                 freed.record(self.cast_stream)
                 if timing:
-                    self.cast_timing.append((c0, freed, c))
+                    self.cast_timing.append((timer, None, c))
                 self.slot_free[s] = freed
                 if j + self.depth < len(t.chunks):
                     self._issue_copy(t, j + self.depth)  # reuses slot s, after this cast
@@ -278,42 +325,79 @@ class H2DStager:
         """``begin`` and ``finish`` in one call."""
         return self.finish(self.begin(host_f32), dst_bf16, wait_event)
 
-    def open_pieces(self, host_f32: torch.Tensor, dst_bf16: torch.Tensor, wait_event: Optional[torch.cuda.Event],
-                    pieces: Sequence[Tuple[int, int]]) -> "_StagerPieces":
-        """Stage ``host_f32`` into ``dst_bf16`` with its copy issued one flat
-        piece ``[a, b)`` at a time, each when the caller ``push``-es it (after
-        writing it), so the copy of the first pieces runs while later ones are
-        still being produced; ``close`` casts the unit in one launch once its
-        last piece has landed.  The pieces land in one of two device slots of
-        their own (allocated on first use, used in turn), not in the ring, so
-        ring stagings run between pushes.  One piece stream is open at a
-        time."""
-        self._piece_lock.acquire()
-        try:
-            return _StagerPieces(self, host_f32, dst_bf16, wait_event, pieces)
-        except BaseException:
-            self._piece_lock.release()
-            raise
+    def copy_for_later(self, host_f32: torch.Tensor,
+                       wait_event: Optional[torch.cuda.Event]) -> Optional[PendingCast]:
+        """Copy the whole unit into a device slot of its size on ``h2d_stream``
+        (after that slot's last cast); the cast is left to ``cast_pending``.
+        ``wait_event`` is what the cast must wait for besides the copy (the
+        destination's last reader).  None when no slot can be had."""
+        n = host_f32.numel()
+        got = self.slots.take(n)
+        if got is None:
+            return None
+        slot, free_ev = got
+        if free_ev is not None:
+            self.h2d_stream.wait_event(free_ev)
+        timing = self.copy_timing is not None
+        if timing:
+            t0 = torch.cuda.Event(enable_timing=True)
+            t0.record(self.h2d_stream)
+        kernels.memcpy_async(slot[:n], host_f32, self.h2d_stream)
+        copied = torch.cuda.Event(enable_timing=True) if timing else _new_event()
+        copied.record(self.h2d_stream)
+        if timing:
+            self.copy_timing.append((t0, copied, n * 4))
+        self._copies.append(copied)
+        if len(self._copies) > 64:
+            _backlog(self._copies)
+        return PendingCast(slot, copied, n, wait_event)
 
-    def _piece_slot(self, n: int) -> Tuple[int, torch.Tensor]:
-        k = self._piece_next
-        self._piece_next ^= 1
-        if self._piece_bufs[k] is None or self._piece_bufs[k].numel() < n:
-            if self._piece_bufs[k] is not None:
-                # growing: nothing may still copy into or cast from the old slot
-                self.h2d_stream.synchronize()
-                self.cast_stream.synchronize()
-            self._piece_bufs[k] = None
-            self._piece_bufs[k] = torch.empty(max(n, self.chunk), dtype=torch.float32, device=self.buf.device)
-            self._piece_free[k] = None
-        return k, self._piece_bufs[k]
+    def cast_pending(self, p: PendingCast, dst_bf16: torch.Tensor, stream: torch.cuda.Stream) -> torch.cuda.Event:
+        """Cast a copied unit into ``dst_bf16`` on ``stream`` (after its copy and
+        its ``wait_event``); the slot goes back to the pool behind the cast."""
+        if dst_bf16.numel() < p.n:
+            raise ValueError("H2DStager.cast_pending: destination smaller than the unit")
+        if p.wait_event is not None:
+            stream.wait_event(p.wait_event)
+        stream.wait_event(p.copied)
+        timer = kernels.KernelTimer() if self.cast_timing is not None else None
+        kernels.cast_f32_bf16_(dst_bf16[:p.n], p.slot[:p.n], stream, timer=timer)
+        freed = _new_event()
+        freed.record(stream)
+        if timer is not None:
+            self.cast_timing.append((timer, None, p.n))
+        self.slots.give(p.slot, freed)
+        self.last_cast_done = freed
+        return freed
+
+    def drop_pending(self, p: PendingCast) -> None:
+        """Give a copied unit's slot back without casting it."""
+        self.slots.give(p.slot, p.copied)
+
+    def open_pieces(self, host_f32: torch.Tensor, dst_bf16: torch.Tensor, wait_event: Optional[torch.cuda.Event],
+                    pieces: Sequence[Tuple[int, int]]) -> Optional["_StagerPieces"]:
+        """Copy ``host_f32`` to the device one flat piece ``[a, b)`` at a time,
+        each when the caller ``push``-es it (after writing it), so the copy of
+        the first pieces runs while later ones are still being produced.  The
+        pieces land in a device slot of the unit's size; ``close`` casts the
+        unit into ``dst_bf16`` or leaves the cast to ``cast_pending``.  None
+        when no slot can be had."""
+        got = self.slots.take(host_f32.numel())
+        if got is None:
+            return None
+        try:
+            return _StagerPieces(self, host_f32, dst_bf16, wait_event, pieces, got)
+        except BaseException:
+            self.slots.give(*got)
+            raise
 
 
 class _StagerPieces:
-    """One unit staged by an ``H2DStager``: copies piece by piece, one cast."""
+    """One unit's copy, piece by piece, into a whole-unit slot of an ``H2DStager``."""
 
     def __init__(self, stager: H2DStager, host: torch.Tensor, dst: torch.Tensor,
-                 wait_event: Optional[torch.cuda.Event], pieces: Sequence[Tuple[int, int]]):
+                 wait_event: Optional[torch.cuda.Event], pieces: Sequence[Tuple[int, int]],
+                 slot: Tuple[torch.Tensor, Optional[torch.cuda.Event]]):
         n = host.numel()
         if dst.numel() < n:
             raise ValueError("H2DStager.open_pieces: destination smaller than source")
@@ -323,7 +407,7 @@ class _StagerPieces:
             raise ValueError("H2DStager.open_pieces: the pieces must cover the source in order")
         self.stager, self.host, self.dst, self.wait_event = stager, host, dst, wait_event
         self.pieces = list(pieces)
-        self.k, self.buf = stager._piece_slot(n)
+        self.buf, self.slot_free = slot
         self.pushed = 0
         self.last_copy: Optional[torch.cuda.Event] = None
         self.open = True
@@ -333,8 +417,8 @@ class _StagerPieces:
             raise RuntimeError(f"H2DStager pieces: piece {j} pushed out of order (next is {self.pushed})")
         st = self.stager
         a, b = self.pieces[j]
-        if j == 0 and st._piece_free[self.k] is not None:
-            st.h2d_stream.wait_event(st._piece_free[self.k])   # the slot's previous cast has read it
+        if j == 0 and self.slot_free is not None:
+            st.h2d_stream.wait_event(self.slot_free)   # the slot's last cast has read it
         timing = st.copy_timing is not None
         if timing:
             t0 = torch.cuda.Event(enable_timing=True)
@@ -352,42 +436,24 @@ class _StagerPieces:
             if len(st._copies) > 64:
                 _backlog(st._copies)
 
-    def close(self) -> torch.cuda.Event:
-        """Cast the unit (after its last copy and the unit's ``ready`` event);
-        returns the cast's completion event."""
+    def close(self, cast_later: bool = False):
+        """After the last piece: a ``PendingCast`` (``cast_later``) or the
+        completion event of the unit's cast on the stager's cast stream."""
         if not self.open or self.pushed != len(self.pieces):
             raise RuntimeError(f"H2DStager pieces: {self.pushed} of {len(self.pieces)} pieces pushed")
-        st = self.stager
-        try:
-            n = self.host.numel()
-            if self.wait_event is not None:
-                st.cast_stream.wait_event(self.wait_event)
-            st.cast_stream.wait_event(self.last_copy)
-            timing = st.cast_timing is not None
-            if timing:
-                c0 = torch.cuda.Event(enable_timing=True)
-                c0.record(st.cast_stream)
-            kernels.cast_f32_bf16_(self.dst[:n], self.buf[:n], st.cast_stream)
-            freed = torch.cuda.Event(enable_timing=True) if timing else _new_event()
-            freed.record(st.cast_stream)
-            if timing:
-                st.cast_timing.append((c0, freed, n))
-            st._piece_free[self.k] = freed
-            st.last_cast_done = freed
-            return freed
-        finally:
-            self._release()
+        self.open = False
+        p = PendingCast(self.buf, self.last_copy, self.host.numel(), self.wait_event)
+        if cast_later:
+            return p
+        return self.stager.cast_pending(p, self.dst, self.stager.cast_stream)
 
     def abort(self) -> None:
-        """Give the stream up without casting (the unit is staged whole later);
-        copies already issued finish into the slot, ahead of its next user's on
-        the same stream."""
+        """Give the slot back without casting (the unit is staged whole later);
+        copies already issued finish into it ahead of its next user's copies
+        on the same stream."""
         if self.open:
-            self._release()
-
-    def _release(self) -> None:
-        self.open = False
-        self.stager._piece_lock.release()
+            self.open = False
+            self.stager.slots.give(self.buf, None)
 
 
 class BF16Loader:
@@ -478,7 +544,8 @@ class _LoaderPieces:
             self.done = ev
         self.pushed += 1
 
-    def close(self) -> torch.cuda.Event:
+    def close(self, cast_later: bool = False) -> torch.cuda.Event:
+        """The last piece's copy event (there is no cast to leave for later)."""
         if self.pushed != len(self.pieces) or self.done is None:
             raise RuntimeError(f"BF16Loader pieces: {self.pushed} of {len(self.pieces)} pieces pushed")
         return self.done
@@ -802,7 +869,11 @@ class StreamingRuntime:
         if h2d_format == "bf16":
             self.stager = BF16Loader(self.h2d_stream)
         else:
-            self.stager = H2DStager(device, stage_chunk_elems, stage_depth, self.h2d_stream, self.cast_stream)
+            # whole-unit slots of units staged after their update: at most a
+            # quarter of the device memory
+            cap = torch.cuda.get_device_properties(device).total_memory // 4
+            self.stager = H2DStager(device, stage_chunk_elems, stage_depth, self.h2d_stream, self.cast_stream,
+                                    slot_cap_bytes=cap)
         # Gradient host slots: a ring of ``grad_ring_depth`` max-size slots,
         # or (None) one slot per unit, set up by ``init_grad_slots``.
         self.grad_ring = None if grad_ring_depth is None else GradStagingRing(grad_ring_depth, max_param_size, dtype)
@@ -825,6 +896,10 @@ class StreamingRuntime:
         # has landed, and each updated piece is copied to the device while
         # the next one is being updated.
         self.piece_elems = 0
+        # Units staged after their update (fp32 H2D) are cast where they are
+        # next used, on that stream between its kernels, instead of on the
+        # cast stream as soon as their copy lands.
+        self.cast_at_use = False
         self.wait_timeout = wait_timeout
         self.trace: Optional[List[Tuple]] = None
         self._trace_lock = threading.Lock()
@@ -944,6 +1019,9 @@ class LayerRuntimeState(nn.Module):
         self._prefetch_lock = threading.Lock()
         self._plan_key: Optional[int] = None
         self._plan = None
+        # Own unit bound with its weights copied but not cast yet: cast by
+        # ``wait_for_h2d`` on the stream about to use the unit.
+        self._pending_cast: Optional[PendingCast] = None
         self._post_called = False
         self._bwd_armed = False
         self._bwd_compute_done = False
@@ -1011,7 +1089,9 @@ class LayerRuntimeState(nn.Module):
         and drop a staging made for the next forward.  Updates keep both
         current; call this after writing the master directly."""
         with self._prefetch_lock:
-            self._prefetched = None
+            old, self._prefetched = self._prefetched, None
+        if old is not None and isinstance(old[1], PendingCast):
+            self.runtime.stager.drop_pending(old[1])
         if self._cpu_params_bf16 is not None and self.total_size:
             _cpu_adam.cast_f32_bf16(self._cpu_params_flat, self._cpu_params_bf16)
 
@@ -1026,13 +1106,28 @@ class LayerRuntimeState(nn.Module):
         if unit is None or self._current_gpu_cache is not None or self.row_sparse:
             return
         stager = self.runtime.stager
+        done = None
         if self._cpu_params_bf16 is not None:
             done = stager.load(self._cpu_params_bf16, unit["param"], unit["ready"])
-        else:
+        elif self.runtime.cast_at_use:
+            done = stager.copy_for_later(self._cpu_params_flat, unit["ready"])
+        if done is None:
             done = stager.finish(stager.begin(self._cpu_params_flat), unit["param"], unit["ready"])
-        with self._prefetch_lock:
-            self._prefetched = (unit, done)
+        self._set_prefetched(unit, done)
         self.runtime.mark("staged_after_update", self.layer_idx)
+
+    def _set_prefetched(self, unit: Dict[str, Any], done) -> None:
+        """Record the staging of the own unit for the next forward: its cast's
+        completion event, or a ``PendingCast``."""
+        with self._prefetch_lock:
+            old, self._prefetched = self._prefetched, (unit, done)
+        if old is not None and isinstance(old[1], PendingCast):
+            self.runtime.stager.drop_pending(old[1])
+
+    def _drop_pending_cast(self) -> None:
+        pc, self._pending_cast = self._pending_cast, None
+        if pc is not None:
+            self.runtime.stager.drop_pending(pc)
 
     def _bind_device_views(self, unit: Dict[str, Any]) -> None:
         buf = unit["param"]
@@ -1067,7 +1162,12 @@ class LayerRuntimeState(nn.Module):
         with self._prefetch_lock:
             pre, self._prefetched = self._prefetched, None
         if pre is not None:
-            unit, self._h2d_done = pre
+            unit, done = pre
+            self._drop_pending_cast()
+            if isinstance(done, PendingCast):
+                self._pending_cast, self._h2d_done = done, None
+            else:
+                self._h2d_done = done
             self._bind_unit(unit, is_backward)
             return
         stager = self.runtime.stager
@@ -1133,7 +1233,16 @@ class LayerRuntimeState(nn.Module):
         return torch.empty(self.total_size, dtype=torch.bfloat16, device=self.runtime.device)
 
     def wait_for_h2d(self, timeout: Optional[float] = None) -> None:
-        """Make the current stream wait for this unit's load (no host block)."""
+        """Make the current stream wait for this unit's load (no host block).
+        A unit whose weights were copied but not cast is cast here, on the
+        current stream, after its copy."""
+        pc = self._pending_cast
+        if pc is not None:
+            unit = self._current_gpu_cache
+            if unit is None:
+                raise RuntimeError(f"unit {self.layer_idx}: a pending cast without a bound unit")
+            self._pending_cast = None
+            self._h2d_done = self.runtime.stager.cast_pending(pc, unit["param"], torch.cuda.current_stream())
         if self._h2d_done is not None:
             torch.cuda.current_stream().wait_event(self._h2d_done)
 
@@ -1245,15 +1354,9 @@ class LayerRuntimeState(nn.Module):
         if unit is None or self._current_gpu_cache is not None or self.row_sparse:
             return None
         stager = self.runtime.stager
-        if getattr(stager, "pieces_disabled", False):
-            return None
         host = self._cpu_params_bf16 if self._cpu_params_bf16 is not None else self._cpu_params_flat
-        try:
-            return unit, stager.open_pieces(host, unit["param"], unit["ready"], bounds)
-        except torch.cuda.OutOfMemoryError:
-            # no room for the piece slots: stage whole units after their update
-            stager.pieces_disabled = True
-            return None
+        stream = stager.open_pieces(host, unit["param"], unit["ready"], bounds)
+        return None if stream is None else (unit, stream)
 
     def _d2h_task(self, slot, grads, missing, grad_ready, cast_fence) -> None:
         """Offload thread: copy this unit's gradients into a host slot, then
@@ -1541,9 +1644,7 @@ class LayerRuntimeState(nn.Module):
                 raise
             rt.mark("adam_done", self.layer_idx)
             if staging is not None:
-                done = staging[1].close()
-                with self._prefetch_lock:
-                    self._prefetched = (staging[0], done)
+                self._set_prefetched(staging[0], staging[1].close(cast_later=rt.cast_at_use))
                 rt.mark("staged_after_update", self.layer_idx)
             elif rt.stage_after_update:
                 self.stage_for_next_forward()

@@ -192,6 +192,15 @@ class SlideFSDP(nn.Module):
                          per Llama-3-8B step instead of 51), but where host
                          memory bandwidth bounds the step it does not raise
                          the rate (measured within noise on a 16-core host).
+      cast_at_use        True (default): with fp32 H2D, a unit staged right
+                         after its update is copied into a device fp32 slot
+                         of its own size, and its cast to bf16 runs where the
+                         unit is next used, on the forward's stream between
+                         its kernels, with the HBM to itself.  False: the cast
+                         runs on a stream of its own as soon as the copy has
+                         landed, mostly beside the backward's GEMMs.  Same
+                         bits; costs up to 4 bytes of HBM per parameter (at
+                         most a quarter of the device memory, else the ring).
     """
 
     def __init__(self, model, config: SlideFSDPConfig, *, stage_chunk_elems: Optional[int] = None,
@@ -199,7 +208,7 @@ class SlideFSDP(nn.Module):
                  d2h_engine: str = "sdma", h2d_format: str = "fp32",
                  resident_layers: Optional[int] = None, row_sparse_embedding: bool = True,
                  fused_cross_entropy: bool = False, stage_after_update: bool = True,
-                 update_piece_elems: int = 0):
+                 update_piece_elems: int = 0, cast_at_use: bool = True):
         super().__init__()
         if config.param_transfer_mode != "full":
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
@@ -228,6 +237,7 @@ class SlideFSDP(nn.Module):
         if update_piece_elems < 0:
             raise ValueError("update_piece_elems must be >= 0")
         self.runtime.piece_elems = int(update_piece_elems)
+        self.runtime.cast_at_use = bool(cast_at_use) and h2d_format == "fp32"
         self.buffer_pool = self.runtime.pool
         self.layer_optimizer = self._create_optimizer(config)
         self.layer_states: List[LayerRuntimeState] = []

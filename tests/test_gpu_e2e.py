@@ -137,6 +137,36 @@ def test_piecewise_updates_with_moments_on_storage(dev, tmp_path):
                                  dict(update_piece_elems=PIECE), nvme_buffers=2)
 
 
+# (cast where the unit is next used, byte cap of the whole-unit slots: None = default)
+CAST_PLACEMENTS = [(True, None), (False, None), (True, 0)]
+
+
+@pytest.mark.parametrize("cast_at_use,slot_cap", CAST_PLACEMENTS)
+def test_cast_placement_matches_oracle(dev, cast_at_use, slot_cap):
+    """Units staged after their update (every unit resident, fp32 H2D): copied
+    into a whole-unit device slot and cast on the forward's stream right
+    before the unit's forward (default), cast on the cast stream as soon as
+    the copy lands (``cast_at_use=False``), or, with no slot to be had, staged
+    through the ring.  Updates, staged weights and moments stay the oracle's,
+    bit for bit, over 3 steps, and the slots are used only by the first."""
+    def setup(sf):
+        if slot_cap is not None:
+            sf.runtime.stager.slots.cap_bytes = slot_cap
+
+    sf = check_updates_against_oracle(dev, "llama", "fp32", {}, dict(resident_layers=L - 1, cast_at_use=cast_at_use),
+                                      keep=True, setup=setup)
+    assert sf.runtime.cast_at_use == cast_at_use
+    used = sf.runtime.stager.slots.bytes
+    assert (used > 0) == (cast_at_use and slot_cap is None), used
+    sf.close()
+
+
+def test_cast_at_use_loss_parity(dev):
+    """Casts where the unit is next used, against the non-offloaded run:
+    first-step gradients and 10 losses."""
+    check_loss_parity(dev, "llama", False, {}, dict(resident_layers=L - 1, cast_at_use=True))
+
+
 # checkpoint offload mode, optimizer moments on storage (fraction), H2D format
 STORAGE_MODES = [("nvme", 0.0, "fp32"), ("cpu", 0.3, "fp32"), ("nvme", 0.8, "bf16")]
 
@@ -203,13 +233,15 @@ def test_fallback_slot_ring_when_per_unit_slots_do_not_fit(dev, monkeypatch):
 
 
 def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, nvme_buffers=None, shapes=None,
-                                 vocab=V, keep=False, timing=False):
+                                 vocab=V, keep=False, timing=False, setup=None):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model(arch, vocab=vocab)
     sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS,
                                           **cfg_kw),
                    wait_timeout=120, h2d_format=h2d_format, **sf_kw)
+    if setup is not None:
+        setup(sf)
     if timing:
         sf.runtime.stager.cast_timing, sf.runtime.stager.copy_timing = [], []
     if nvme_buffers is not None and sf.layer_optimizer.offloader is not None:

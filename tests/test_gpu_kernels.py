@@ -59,6 +59,36 @@ def test_cast_unaligned_views(dev, src_off, dst_off):
     assert np.array_equal(bits16(out), exp)
 
 
+@pytest.mark.parametrize("n,src_off", [(1 << 20, 0), ((1 << 20) + 5, 0), (4099, 1), (7, 0)])
+def test_timed_cast_times_the_kernel_alone(dev, n, src_off):
+    """The timed cast (vector kernel, vector + tail, scalar only) gives the
+    oracle's bits, and its events time the kernels alone: on a stream that
+    first waits for a long matmul on another stream, events recorded around
+    the launch include the wait, the kernel-stamped events do not."""
+    x = rand_f32(n + src_off, 17)
+    xs = x.to(dev)[src_off:]
+    out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    a = torch.randn(4096, 4096, device=dev)
+    busy, st = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(busy):
+        for _ in range(8):
+            a = (a @ a).clamp_(-1, 1)
+        long_done = torch.cuda.Event()
+        long_done.record(busy)
+    outer0, outer1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    timer = kernels.KernelTimer()
+    outer0.record(st)
+    st.wait_event(long_done)
+    kernels.cast_f32_bf16_(out, xs, st, timer=timer)
+    outer1.record(st)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(out), oracle.cast_f32_bf16(x.numpy()[src_off:]))
+    kernel_ms, outer_ms = timer.elapsed_ms(), outer0.elapsed_time(outer1)
+    print(f"n={n}: kernel {kernel_ms:.4f} ms, around the wait {outer_ms:.4f} ms")
+    assert 0.0 < kernel_ms < 0.5 * outer_ms
+
+
 def test_cast_full_llama_layer(dev):
     # one Llama-3-8B decoder layer: 218,112,000 elements, the staged unit size
     n = 218_112_000

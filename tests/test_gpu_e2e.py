@@ -161,6 +161,34 @@ def test_cast_placement_matches_oracle(dev, cast_at_use, slot_cap):
     sf.close()
 
 
+def test_dropped_stagings_restage_from_the_master(dev):
+    """Stagings for the next forward dropped between steps (``refresh_host_copy``,
+    as after writing a master directly): units copied but not cast give their
+    slot back, and the next forward stages them from the master through the
+    ring; every update stays the oracle's, bit for bit, and no slot is lost
+    (free slots plus those still held by a staging add up to the pool)."""
+    from test1_amd.layer_state import PendingCast
+
+    dropped = []
+
+    def between(sf, k):
+        if k == 1:
+            held = [s for s in sf.layer_states if s._prefetched is not None and isinstance(s._prefetched[1], PendingCast)]
+            dropped.append(len(held))
+            for s in sf.layer_states:
+                s.refresh_host_copy()
+
+    sf = check_updates_against_oracle(dev, "llama", "fp32", {}, dict(resident_layers=L - 1), keep=True, between=between)
+    assert dropped and dropped[0] > 0
+    pool = sf.runtime.stager.slots
+    free = sum(t.numel() * 4 for lst in pool._free.values() for t, _ in lst)
+    held = sum(4 * s._prefetched[1].n for s in sf.layer_states
+               if s._prefetched is not None and isinstance(s._prefetched[1], PendingCast))
+    held += sum(4 * s._pending_cast.n for s in sf.layer_states if s._pending_cast is not None)
+    assert free + held == pool.bytes, (free, held, pool.bytes)
+    sf.close()
+
+
 def test_cast_at_use_loss_parity(dev):
     """Casts where the unit is next used, against the non-offloaded run:
     first-step gradients and 10 losses."""
@@ -233,7 +261,7 @@ def test_fallback_slot_ring_when_per_unit_slots_do_not_fit(dev, monkeypatch):
 
 
 def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, nvme_buffers=None, shapes=None,
-                                 vocab=V, keep=False, timing=False, setup=None):
+                                 vocab=V, keep=False, timing=False, setup=None, between=None):
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model(arch, vocab=vocab)
@@ -256,7 +284,9 @@ def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, 
         steps_ids = batches(steps, vocab=vocab)
     else:
         steps_ids = [batches(1, B, S, vocab=vocab)[0] for B, S in shapes]
-    for ids in steps_ids:
+    for k, ids in enumerate(steps_ids):
+        if between is not None and k > 0:
+            between(sf, k)
         sf.runtime.capture = {}
         ids = ids.to(dev)
         sf(input_ids=ids, labels=ids)

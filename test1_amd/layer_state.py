@@ -40,7 +40,6 @@ plus the fp32 staging ring (``depth`` chunks of ``chunk_elems``) with fp32 H2D.
 from __future__ import annotations
 
 import bisect
-import heapq
 import itertools
 import queue
 import threading

@@ -48,7 +48,7 @@ row-sparse embedding, bf16 H2D, SDMA gradient copies) change no bits.
 from __future__ import annotations
 
 import os
-from typing import Any, List, Optional
+from typing import List, Optional
 
 import torch
 import torch.nn as nn

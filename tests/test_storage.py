@@ -7,7 +7,6 @@ with moments in memory (which the LayerAdam tests pin against the reference's
 compiled cpu_adam).  The reference's tensornvme / kvikio back ends are not
 installed anywhere here, so their own behaviour is not compared."""
 
-import ctypes
 import random
 
 import pytest

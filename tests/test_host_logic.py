@@ -299,3 +299,19 @@ def test_save_on_cpu_round_trip():
         y = (x * x).sum()
     y.backward()
     assert torch.allclose(x.grad, 2 * x.detach())
+
+
+@pytest.mark.parametrize("args,env", [(["--gpus", "2"], {}), (["--gpus", "1"], {"WORLD_SIZE": "2"})])
+def test_bench_refuses_more_than_one_gpu(args, env):
+    """The path runs on one GPU: bench.py with --gpus above 1, or launched as
+    one of several ranks, exits with status 2 and says so, before touching a
+    GPU."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py")] + args, capture_output=True, text=True,
+                       env={**os.environ, **env}, timeout=120)
+    assert r.returncode == 2, (r.returncode, r.stderr[-500:])
+    assert "one GPU only" in r.stderr

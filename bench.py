@@ -392,6 +392,11 @@ def link_stats(r: dict, steps: int) -> dict:
         "h2d_bytes_per_step": h2d_bytes / steps,
         "d2h_bytes_per_step": d2h_bytes / steps,
         "h2d_busy_frac": (h2d_ms * 1e-3) / r["elapsed"],
+        "note": "h2d: the parameter copies' bytes over the sum of HIP-event durations around each copy on "
+                "its stream, which also count the copy's wait for a copy engine and the events' own latency "
+                "(profiles/host_link__llama3_8b_train_step.md: 52-53 GB/s over the union of the copy "
+                "engines' busy intervals); d2h: the SDMA gradient copies over the union of their engine "
+                "timestamps",
     }
 
 

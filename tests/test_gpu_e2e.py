@@ -189,6 +189,26 @@ def test_dropped_stagings_restage_from_the_master(dev):
     sf.close()
 
 
+@pytest.mark.parametrize("grad", [False, True])
+def test_evaluation_forwards_between_steps(dev, grad):
+    """Forwards without labels between training steps, under ``no_grad`` or
+    with autograd on and no backward (checkpoints packed, nothing unpacked):
+    two such forwards give identical logits, and every update of the
+    training that follows stays the oracle's, bit for bit."""
+    seen = []
+
+    def between(sf, k):
+        ids = batches(1)[0].to(dev)
+        with torch.set_grad_enabled(grad):
+            a = sf(input_ids=ids).logits.detach().float().clone()
+            b = sf(input_ids=ids).logits.detach().float().clone()
+        assert torch.equal(a, b), f"step {k}"
+        seen.append(a)
+
+    check_updates_against_oracle(dev, "llama", "fp32", {}, dict(resident_layers=L - 1), between=between)
+    assert len(seen) == 2
+
+
 def test_cast_at_use_loss_parity(dev):
     """Casts where the unit is next used, against the non-offloaded run:
     first-step gradients and 10 losses."""

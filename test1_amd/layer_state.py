@@ -197,6 +197,14 @@ class _SlotPool:
         with self._lock:
             self._free.setdefault(t.numel(), []).append((t, free_event))
 
+    def release(self) -> None:
+        """Drop the free buffers (the caller has made sure nothing still copies
+        into or reads from them); buffers still out stay with their holders."""
+        with self._lock:
+            for lst in self._free.values():
+                self.bytes -= sum(4 * t.numel() for t, _ in lst)
+            self._free.clear()
+
 
 class H2DStager:
     """Pinned fp32 master -> device bf16 unit, through a device fp32 ring.
@@ -977,6 +985,27 @@ class StreamingRuntime:
         if self.offload_executor is not None:
             self.offload_executor.shutdown(wait=True)
         self.update_executor.shutdown(wait=True)
+
+    def release_slots(self, states) -> None:
+        """Give back the whole-unit slots of stagings not yet cast (their units
+        are then staged from the master if used again) and free the pool's
+        buffers once the copy and cast streams have drained."""
+        slots = getattr(self.stager, "slots", None)
+        if slots is None:
+            return
+        for st in states:
+            with st._prefetch_lock:
+                pre = st._prefetched
+                if pre is not None and isinstance(pre[1], PendingCast):
+                    st._prefetched = None
+                else:
+                    pre = None
+            if pre is not None:
+                self.stager.drop_pending(pre[1])
+            st._drop_pending_cast()
+        self.h2d_stream.synchronize()
+        self.cast_stream.synchronize()
+        slots.release()
 
 
 class LayerRuntimeState(nn.Module):

@@ -712,6 +712,7 @@ class SlideFSDP(nn.Module):
                 h.remove()
             self._hook_handles = []
             self.runtime.shutdown()
+            self.runtime.release_slots(self.layer_states)
             if self._spill is not None:
                 self._spill.close()
                 self._spill = None

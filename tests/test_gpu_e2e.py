@@ -187,6 +187,7 @@ def test_dropped_stagings_restage_from_the_master(dev):
     held += sum(4 * s._pending_cast.n for s in sf.layer_states if s._pending_cast is not None)
     assert free + held == pool.bytes, (free, held, pool.bytes)
     sf.close()
+    assert pool.bytes == 0 and not pool._free     # close gives every slot back
 
 
 @pytest.mark.parametrize("grad", [False, True])

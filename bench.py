@@ -236,7 +236,7 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
                           enable_activation_checkpoint=not args.no_activation_checkpoint)
     sf = SlideFSDP(model, cfg, d2h_engine=d2h_engine, h2d_format=h2d_format, resident_layers=resident_layers,
                    fused_cross_entropy=args.fused_ce, update_piece_elems=args.piece_elems,
-                   cast_at_use=not args.cast_on_copy)
+                   cast_at_use=not args.cast_on_copy, early_embedding_update=not args.no_early_embedding)
     uses_storage = args.ac_offload == "nvme" or args.opt_nvme_fraction > 0
     log(f"[bench] SlideFSDP ({h2d_format} H2D, {sf.resident_layers} resident decoders, {d2h_engine} D2H) "
         f"ready in {time.time() - t0:.1f}s")
@@ -429,6 +429,9 @@ def main():
     ap.add_argument("--piece-elems", type=int, default=0,
                     help="elements per piece of a unit's update (gradients back, AdamW and copy to the device "
                          "run piece by piece, one cast per unit), e.g. 67108864; 0: whole units")
+    ap.add_argument("--no-early-embedding", action="store_true",
+                    help="update the embedding's untouched rows with its batch rows, after the backward, "
+                         "instead of as the backward starts")
     ap.add_argument("--cast-on-copy", action="store_true",
                     help="cast a unit staged after its update on the cast stream as soon as its copy lands "
                          "(default: where the unit is next used, between the forward's kernels)")
@@ -520,6 +523,7 @@ def main():
                    "stage_after_update": r["stage_after_update"],
                    "update_piece_elems": args.piece_elems,
                    "cast_at_use": r["cast_at_use"],
+                   "early_embedding_update": not args.no_early_embedding,
                    "row_sparse_embedding": r["row_sparse_embedding"],
                    "ac_offload_mode": args.ac_offload,
                    "activation_checkpoint": not args.no_activation_checkpoint,

@@ -308,11 +308,16 @@ int sf_adam_update_cast(int optimizer_id, size_t step, float lr, float beta1,
 
 /* sf_adam_update_cast over a [n_rows, row_len] tensor whose gradient is
  * zero except in some rows: row r takes its gradient from row row_slot[r]
- * of grads ([n_grad_rows, row_len], g_dtype), or zeros when row_slot[r] < 0.
- * Every element gets exactly the dense update (row_len must be a multiple
- * of 16, so no element falls in the scalar tail).  Replaces adam_update on
- * the embedding unit's dense `grad.float()` (layer_adam.py:404) when only
- * the batch's rows were offloaded. */
+ * of grads ([n_grad_rows, row_len], g_dtype), zeros when row_slot[r] is
+ * SF_ROW_ZERO, and is left as it is when row_slot[r] is SF_ROW_SKIP (so an
+ * update can be split over rows: the rows of one call skipped by the other).
+ * Other negative values are an error.  Every element gets exactly the dense
+ * update (row_len must be a multiple of 16, so no element falls in the
+ * scalar tail).  Replaces adam_update on the embedding unit's dense
+ * `grad.float()` (layer_adam.py:404) when only the batch's rows were
+ * offloaded. */
+#define SF_ROW_ZERO (-1)
+#define SF_ROW_SKIP (-2)
 int sf_adam_update_rows(int optimizer_id, size_t step, float lr, float beta1,
                         float beta2, float eps, float weight_decay,
                         int bias_correction, float* params, float* exp_avg,

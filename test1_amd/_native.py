@@ -33,6 +33,9 @@ SF_IO_READ = 0
 SF_IO_WRITE = 1
 SF_IO_ALIGN = 4096
 SF_EALIGN = 9007
+# row_slot markers of the row-wise AdamW: a zero-gradient row, a row left as it is
+SF_ROW_ZERO = -1
+SF_ROW_SKIP = -2
 
 
 class SfSeg(ctypes.Structure):

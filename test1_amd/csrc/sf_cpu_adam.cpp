@@ -461,6 +461,7 @@ void adam_rows(float* p, float* m, float* v, uint16_t* pb, size_t n_rows, size_t
     for (long k = 0; k < nchunks; ++k) {
         const size_t r0 = size_t(k) * rows_per_chunk, r1 = std::min(n_rows, r0 + size_t(rows_per_chunk));
         for (size_t r = r0; r < r1; ++r) {
+            if (row_slot[r] == SF_ROW_SKIP) continue;
             const size_t o = r * row_len;
             const G* gr = row_slot[r] >= 0 ? g + size_t(row_slot[r]) * row_len : zeros.data();
             uint16_t* pbr = pb ? pb + o : nullptr;
@@ -497,7 +498,7 @@ int sf_adam_update_rows(int optimizer_id, size_t step, float lr, float beta1, fl
     if (row_len % 16 != 0) return SF_EINVAL;
     if (!params || !exp_avg || !exp_avg_sq || !row_slot || (n_grad_rows > 0 && !grads)) return SF_EINVAL;
     for (size_t r = 0; r < n_rows; ++r) {
-        if (row_slot[r] >= 0 && size_t(row_slot[r]) >= n_grad_rows) return SF_EINVAL;
+        if (row_slot[r] < SF_ROW_SKIP || (row_slot[r] >= 0 && size_t(row_slot[r]) >= n_grad_rows)) return SF_EINVAL;
     }
     sf_adam_hparams hp;
     stateful_hparams(*st, step, lr, beta1, beta2, eps, weight_decay, bias_correction, hp);
@@ -523,7 +524,7 @@ int sf_cpu_adam_step_rows(float* params, float* exp_avg, float* exp_avg_sq, uint
     if (row_len % 16 != 0) return SF_EINVAL;
     if (!hp || !params || !exp_avg || !exp_avg_sq || !row_slot || (n_grad_rows > 0 && !grads)) return SF_EINVAL;
     for (size_t r = 0; r < n_rows; ++r) {
-        if (row_slot[r] >= 0 && size_t(row_slot[r]) >= n_grad_rows) return SF_EINVAL;
+        if (row_slot[r] < SF_ROW_SKIP || (row_slot[r] >= 0 && size_t(row_slot[r]) >= n_grad_rows)) return SF_EINVAL;
     }
     const Scalars c = make_scalars(*hp);
     if (g_dtype == SF_DTYPE_BF16) adam_rows<SF_DTYPE_BF16>(params, exp_avg, exp_avg_sq, params_bf16, n_rows, row_len, row_slot, grads, c);

@@ -60,6 +60,11 @@ def _new_event() -> torch.cuda.Event:
     return torch.cuda.Event(enable_timing=False, blocking=False)
 
 
+# Queue priority of work that may wait until the host AdamW has nothing else
+# ready (the gradient-free rows of the embedding's update).
+EARLY_UPDATE_PRIORITY = 1 << 30
+
+
 class LayerBufferPool:
     """Fixed set of device units ``{"param", "grad"}`` reused round-robin.
 
@@ -827,6 +832,26 @@ class _UpdateReady:
             self.grads_ready.synchronize()
 
 
+class _LinkQuiet:
+    """Ready once ``first`` has completed and no host-to-device copy of a
+    unit is queued.  For update work that may wait (the embedding's
+    gradient-free rows): its host-memory traffic would slow the copies the
+    forward is waiting for, so it runs once they have landed.  Polled by the
+    executor like ``_UpdateReady``; after ``poll_fallback_s`` it runs anyway."""
+
+    poll_interval = 200e-6
+    poll_fallback_s = 10.0
+
+    def __init__(self, first, stager):
+        self.first, self.stager = first, stager
+
+    def query(self) -> bool:
+        return self.first.query() and self.stager.backlog() == 0
+
+    def synchronize(self) -> None:
+        self.first.synchronize()
+
+
 def _no_slot() -> None:
     """Offload gate with one slot per unit: nothing to wait for."""
     return None
@@ -1523,6 +1548,11 @@ class LayerRuntimeState(nn.Module):
         self._bad_ids.zero_()
         self._rows_host: Optional[torch.Tensor] = None
         self._ids_host: Optional[torch.Tensor] = None
+        # The batch's ids on the host, copied at the lookup (pinned, event),
+        # for the early part of the update; the early part itself, once queued.
+        self._ids_early_host: Optional[torch.Tensor] = None
+        self._lookup_ids: Optional[Tuple[torch.Tensor, torch.cuda.Event]] = None
+        self._early: Optional[Dict[str, Any]] = None
 
     def _host_table(self) -> torch.Tensor:
         V, H = self._rows_shape
@@ -1544,11 +1574,81 @@ class LayerRuntimeState(nn.Module):
         self._bad_ids.zero_()
         kernels.gather_rows(self._host_table(), flat, out.view(-1, H), bad=self._bad_ids,
                             stream=torch.cuda.current_stream())
+        self._copy_lookup_ids(flat)
         self._bwd_compute_done = False
         self._grads_offloaded = False
         self.runtime.log("h2d", self.layer_idx, False)
         self.runtime.mark("h2d_issued", self.layer_idx)
         return out
+
+    def _copy_lookup_ids(self, flat: torch.Tensor) -> None:
+        """Copy the batch's ids to pinned host memory on the D2H stream, for
+        the early part of this step's update.  The buffer's previous reader
+        (last step's update) finished before this lookup, which waited for
+        it."""
+        rt = self.runtime
+        ntok = flat.numel()
+        if self._ids_early_host is None or self._ids_early_host.numel() < ntok:
+            self._ids_early_host = pinned_empty(max(ntok, 1), torch.int64)
+        ready = _new_event()
+        ready.record(torch.cuda.current_stream())
+        rt.d2h_stream.wait_event(ready)
+        kernels.memcpy_async(self._ids_early_host[:ntok], flat, rt.d2h_stream)
+        flat.record_stream(rt.d2h_stream)
+        copied = _new_event()
+        copied.record(rt.d2h_stream)
+        self._lookup_ids = (self._ids_early_host[:ntok], copied)
+
+    def start_early_update(self) -> None:
+        """Queue the part of this step's update that needs no gradient: the
+        table rows the batch did not touch (zero gradient) get their AdamW
+        update now, at the lowest priority, so the host AdamW does it while
+        it would otherwise wait for the backward's first gradients; the
+        batch's rows follow once their gradient has landed (``step_rows_early``
+        then ``step_rows``: the bits of the whole update).  It waits for the
+        host link to have no unit copy queued, so that its host-memory traffic
+        does not slow the copies the forward is waiting for.  Called by the
+        model right before its backward, which is then certain to reach the
+        lookup (not in the reference, whose update of the whole table waits
+        for the gradient)."""
+        rt = self.runtime
+        opt = self.layer_optimizer
+        lookup, self._lookup_ids = self._lookup_ids, None
+        if (not self.row_sparse or lookup is None or opt is None or not getattr(opt, "reference_order", False)
+                or not self.layer.weight.requires_grad):
+            return
+        ids, copied = lookup
+        early = {"ids": ids, "ready": copied, "state": "queued"}
+        self._early = early
+        early["future"] = rt.update_executor.submit(EARLY_UPDATE_PRIORITY, self._do_update_rows_early, early,
+                                                    ready=_LinkQuiet(copied, rt.stager))
+
+    def _do_update_rows_early(self, early: Dict[str, Any]) -> bool:
+        """Update thread: the early part queued by ``start_early_update``
+        (nothing if the late part has already run it)."""
+        if early["state"] != "queued":
+            return False
+        rt = self.runtime
+        V, H = self._rows_shape
+        early["ready"].synchronize()
+        ids = early["ids"]
+        if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= V):
+            early["state"] = "skipped"   # the late part raises for these ids
+            return False
+        rt.mark("early_update_start", self.layer_idx)
+        slot = torch.full((V,), _native.SF_ROW_ZERO, dtype=torch.int64)
+        slot[ids] = _native.SF_ROW_SKIP
+        if rt.capture is not None:
+            early["master_before"] = self._cpu_params_flat.clone()
+        rt.set_adam_threads()
+        with self.update_lock:
+            early["state"] = "failed"
+            self.layer_optimizer.step_rows_early(self.layer_idx, slot, param_view=self._cpu_params_flat.view(V, H),
+                                                 bf16_view=None if self._cpu_params_bf16 is None
+                                                 else self._cpu_params_bf16.view(V, H))
+            early["state"] = "applied"
+        rt.mark("early_update_done", self.layer_idx)
+        return True
 
     def offload_rows(self, grad_out: torch.Tensor, ids: torch.Tensor) -> None:
         """Backward of the lookup: dense table gradient on the device (as the
@@ -1596,12 +1696,19 @@ class LayerRuntimeState(nn.Module):
                 raise ValueError(f"embedding unit {self.layer_idx}: input ids outside [0, {V})")
             ids = self._ids_host[:ntok]
             rows = self._rows_host[:ntok]
-            row_slot = torch.full((V,), -1, dtype=torch.int64)
+            early, self._early = self._early, None
+            if early is not None and early["state"] == "queued":
+                self._do_update_rows_early(early)   # not run yet: now, on this thread
+            applied = early is not None and early["state"] == "applied"
+            if early is not None and early["state"] == "failed":
+                raise RuntimeError(f"embedding unit {self.layer_idx}: the early part of the update failed")
+            row_slot = torch.full((V,), _native.SF_ROW_SKIP if applied else _native.SF_ROW_ZERO, dtype=torch.int64)
             row_slot[ids] = torch.arange(ntok, dtype=torch.int64)
             if rt.capture is not None:
                 dense = torch.zeros(V, H, dtype=rows.dtype)
                 dense[ids] = rows
-                rt.capture[self.layer_idx] = (dense.view(-1), self._cpu_params_flat.clone())
+                before = early["master_before"] if applied else self._cpu_params_flat.clone()
+                rt.capture[self.layer_idx] = (dense.view(-1), before)
             rt.set_adam_threads()
             with self.update_lock:
                 if self.layer_optimizer is not None:

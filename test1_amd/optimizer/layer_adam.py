@@ -80,6 +80,9 @@ class LayerAdam:
         # the scalars the reference's order -- last unit first, once per
         # step -- would give it.
         self.reference_order = False
+        # units whose current step was begun by step_rows_early on their
+        # gradient-free rows and awaits step_rows: {unit: (step, lr)}
+        self._early_rows: Dict[int, tuple] = {}
         self.state: DefaultDict[torch.Tensor, Any] = defaultdict(dict)
         if not 0.0 <= nvme_offload_fraction <= 1.0:
             raise ValueError("nvme_offload_fraction must be in [0, 1]")
@@ -369,25 +372,71 @@ class LayerAdam:
                 raise ValueError(f"LayerAdam: the pieces leave part of a parameter of {p.numel()} elements out")
 
     @torch.no_grad()
+    def step_rows_early(self, layer_idx: int, row_slot: torch.Tensor, param_view: torch.Tensor,
+                        bf16_view: Optional[torch.Tensor] = None):
+        """Begin a step of a one-parameter [V, H] unit with the part that needs
+        no gradient (not in the reference): the step counter advances, and
+        every row whose ``row_slot`` is ``SF_ROW_ZERO`` gets this step's
+        zero-gradient update now.  Rows marked ``SF_ROW_SKIP`` are left for
+        the ``step_rows`` call that completes the step, with the same step
+        and learning rate; it must mark these early rows ``SF_ROW_SKIP`` in
+        turn.  Together the two give the bits of one ``step_rows`` over all
+        rows.  Needs ``reference_order`` (the scalars then depend only on the
+        step and the learning rate)."""
+        if not self.reference_order:
+            raise RuntimeError("step_rows_early: needs reference_order")
+        if bool((row_slot >= 0).any()):
+            raise ValueError("step_rows_early: rows with a gradient belong to step_rows")
+        group = self._group(layer_idx)
+        if len(group["params"]) != 1:
+            raise ValueError("step_rows_early: the unit must hold exactly one parameter")
+        self._pre_step(layer_idx)
+        try:
+            group["step"] += 1
+            # a step begun here and never completed (its backward failed) is dropped
+            self._early_rows[layer_idx] = (group["step"], group["lr"])
+            p = group["params"][0]
+            st = self.state[p]
+            beta1, beta2 = group["betas"]
+            shape = param_view.shape
+            hp = _cpu_adam.hparams_in_reference_order(
+                group["step"], group["lr"], beta1, beta2, group["eps"], group["weight_decay"],
+                group["bias_correction"], self.defaults["adamw_mode"], self._first_of_step(group, p))
+            no_rows = torch.empty((0, shape[1]), dtype=torch.bfloat16)
+            _cpu_adam.adam_step_rows(param_view, st["exp_avg"].view(shape), st["exp_avg_sq"].view(shape),
+                                     row_slot, no_rows, hp, params_bf16=bf16_view)
+        finally:
+            self._post_step(layer_idx)
+
+    @torch.no_grad()
     def step_rows(self, layer_idx: int, row_slot: torch.Tensor, rows: torch.Tensor,
                   param_view: torch.Tensor, bf16_view: Optional[torch.Tensor] = None):
         """Update a one-parameter unit (a [V, H] table) whose gradient is zero
         outside the rows that ``row_slot`` maps into ``rows`` (not in the
         reference: the dense ``step_with_grad_views`` on the scattered
-        gradient gives the same bits)."""
+        gradient gives the same bits).  After ``step_rows_early`` it completes
+        that step, with its step and learning rate: the rows updated early
+        must be marked ``SF_ROW_SKIP``."""
         group = self._group(layer_idx)
         if len(group["params"]) != 1:
             raise ValueError("step_rows: the unit must hold exactly one parameter")
+        early = self._early_rows.pop(layer_idx, None)
+        if early is not None and not self.reference_order:
+            raise RuntimeError("step_rows: an early part needs reference_order")
         self._pre_step(layer_idx)
         try:
-            group["step"] += 1
+            if early is None:
+                group["step"] += 1
+                step, lr = group["step"], group["lr"]
+            else:
+                step, lr = early
             p = group["params"][0]
             st = self.state[p]
             beta1, beta2 = group["betas"]
             shape = param_view.shape
             if self.reference_order:
                 hp = _cpu_adam.hparams_in_reference_order(
-                    group["step"], group["lr"], beta1, beta2, group["eps"], group["weight_decay"],
+                    step, lr, beta1, beta2, group["eps"], group["weight_decay"],
                     group["bias_correction"], self.defaults["adamw_mode"], self._first_of_step(group, p))
                 _cpu_adam.adam_step_rows(param_view, st["exp_avg"].view(shape), st["exp_avg_sq"].view(shape),
                                          row_slot, rows, hp, params_bf16=bf16_view)

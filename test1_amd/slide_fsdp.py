@@ -192,6 +192,12 @@ class SlideFSDP(nn.Module):
                          per Llama-3-8B step instead of 51), but where host
                          memory bandwidth bounds the step it does not raise
                          the rate (measured within noise on a 16-core host).
+      early_embedding_update  True (default): with the row-sparse embedding,
+                         the table rows a batch does not touch (zero
+                         gradient) get their AdamW update as the backward
+                         starts, while the host AdamW would otherwise wait
+                         for the first gradients; the batch's rows follow
+                         once their gradient has landed.  Same bits.
       cast_at_use        True (default): with fp32 H2D, a unit staged right
                          after its update is copied into a device fp32 slot
                          of its own size, and its cast to bf16 runs where the
@@ -208,7 +214,7 @@ class SlideFSDP(nn.Module):
                  d2h_engine: str = "sdma", h2d_format: str = "fp32",
                  resident_layers: Optional[int] = None, row_sparse_embedding: bool = True,
                  fused_cross_entropy: bool = False, stage_after_update: bool = True,
-                 update_piece_elems: int = 0, cast_at_use: bool = True):
+                 update_piece_elems: int = 0, cast_at_use: bool = True, early_embedding_update: bool = True):
         super().__init__()
         if config.param_transfer_mode != "full":
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
@@ -238,6 +244,7 @@ class SlideFSDP(nn.Module):
             raise ValueError("update_piece_elems must be >= 0")
         self.runtime.piece_elems = int(update_piece_elems)
         self.runtime.cast_at_use = bool(cast_at_use) and h2d_format == "fp32"
+        self._early_embedding_update = bool(early_embedding_update)
         self.buffer_pool = self.runtime.pool
         self.layer_optimizer = self._create_optimizer(config)
         self.layer_states: List[LayerRuntimeState] = []
@@ -613,6 +620,10 @@ class SlideFSDP(nn.Module):
         loss, logits = self.output_layer(hidden_states, labels)
         if loss is not None:
             loss = self._PostLayerFunction.apply(loss, output_state, True)
+            if self._early_embedding_update and torch.is_grad_enabled() and loss.requires_grad:
+                # the backward below reaches the lookup: the embedding's
+                # gradient-free rows can be updated while it starts
+                self.layer_states[0].start_early_update()
             loss.backward()
             self._grow_grad_ring()
         return CausalLMOutputWithPast(loss=loss, logits=logits)

@@ -226,7 +226,7 @@ def test_row_sparse_update_rejects_bad_shapes():
     cpu_adam.destroy_adam(82)
 
 
-def _run_layer_adam(order_fn, reference_order, steps=6, seed=3, piece_elems=None, calls=None):
+def _run_layer_adam(order_fn, reference_order, steps=6, seed=3, piece_elems=None, calls=None, early=False):
     """Units 0 (a [64, 32] table, row-sparse updates) and 1..4 (several
     params each), stepped ``steps`` times in the order ``order_fn(step)``.
     With ``piece_elems``, units 1..4 are updated in pieces of that size (the
@@ -245,7 +245,15 @@ def _run_layer_adam(order_fn, reference_order, steps=6, seed=3, piece_elems=None
         grads = {u: [(torch.randn(p.shape, generator=gg) * 1e-3).bfloat16() for p in units[u]] for u in units}
         ids = torch.randperm(64, generator=gg)[:9]
         for u in order_fn(step):
-            if u == 0:
+            if u == 0 and early:
+                # the gradient-free rows first, the batch's rows once their gradient is there
+                untouched = torch.full((64,), -1, dtype=torch.int64)
+                untouched[ids] = -2
+                opt.step_rows_early(0, untouched, units[0][0].data)
+                row_slot = torch.full((64,), -2, dtype=torch.int64)
+                row_slot[ids] = torch.arange(ids.numel())
+                opt.step_rows(0, row_slot, grads[0][0][ids].contiguous(), units[0][0].data)
+            elif u == 0:
                 row_slot = torch.full((64,), -1, dtype=torch.int64)
                 row_slot[ids] = torch.arange(ids.numel())
                 opt.step_rows(0, row_slot, grads[0][0][ids].contiguous(), units[0][0].data)
@@ -366,3 +374,43 @@ def test_piecewise_update_rejects_ranges_off_the_vector_boundary():
     g = torch.zeros(100, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="16-element boundary"):
         opt.step_with_grad_views(0, {p: g}, pieces=[[(p, 0, 40)], [(p, 40, 100)]])
+
+
+def test_row_update_split_early_and_late_gives_the_reference_bits():
+    """The embedding's update split in two: the rows the batch did not touch
+    (zero gradient) first, the batch's rows once their gradient has landed.
+    Over 6 steps, in the reference's order and in shuffled orders, the table
+    and its moments carry the bits of the whole update pinned against the
+    reference's compiled cpu_adam above."""
+    import random
+
+    descending = lambda step: [4, 3, 2, 1, 0]  # noqa: E731
+    rng = random.Random(5)
+    orders = {s: rng.sample(range(5), 5) for s in range(6)}
+    ref_units, ref_opt = _run_layer_adam(descending, reference_order=False)
+    for order in (descending, lambda s: orders[s]):
+        got_units, got_opt = _run_layer_adam(order, reference_order=True, early=True)
+        for u in ref_units:
+            for a, b in zip(ref_units[u], got_units[u]):
+                assert torch.equal(a.data.view(torch.int32), b.data.view(torch.int32)), u
+                for k in ("exp_avg", "exp_avg_sq"):
+                    assert torch.equal(ref_opt.state[a][k].view(torch.int32), got_opt.state[b][k].view(torch.int32))
+        assert got_opt._groups_by_layer[0]["step"] == 6 and not got_opt._early_rows
+
+
+def test_row_update_skip_marker_and_invalid_markers():
+    """``SF_ROW_SKIP`` rows are left exactly as they are, ``SF_ROW_ZERO``
+    rows get the zero-gradient update, other negative markers are refused."""
+    from test1_amd import _native
+
+    g = torch.Generator().manual_seed(1)
+    p = torch.randn(8, 16, generator=g) * 0.02
+    m, v = torch.zeros(8, 16), torch.zeros(8, 16)
+    p0 = p.clone()
+    hp = cpu_adam.hparams_in_reference_order(1, 1e-3, 0.9, 0.999, 1e-8, 0.01, True, True, False)
+    slot = torch.tensor([_native.SF_ROW_SKIP, _native.SF_ROW_ZERO] * 4, dtype=torch.int64)
+    cpu_adam.adam_step_rows(p, m, v, slot, torch.empty((0, 16), dtype=torch.bfloat16), hp)
+    assert torch.equal(p[0::2], p0[0::2]) and not torch.equal(p[1::2], p0[1::2])
+    with pytest.raises(RuntimeError):
+        cpu_adam.adam_step_rows(p, m, v, torch.full((8,), -3, dtype=torch.int64),
+                                torch.empty((0, 16), dtype=torch.bfloat16), hp)

@@ -210,6 +210,26 @@ def test_evaluation_forwards_between_steps(dev, grad):
     assert len(seen) == 2
 
 
+@pytest.mark.parametrize("early", [True, False])
+def test_embedding_early_rows(dev, early):
+    """The embedding's update in two parts (default): the rows the batch does
+    not touch as the backward starts, the batch's rows after their gradient.
+    Every update stays the oracle's, bit for bit, over 3 steps (batches of
+    changing shape), and the early part ran once in every step; with
+    ``early_embedding_update=False`` the table is updated in one part after
+    the backward."""
+    def setup(sf):
+        sf.runtime.timeline = []
+
+    sf = check_updates_against_oracle(dev, "llama", "fp32", {}, dict(early_embedding_update=early), keep=True,
+                                      setup=setup, shapes=[(2, 128), (1, 96), (2, 128)])
+    marks = [w for _, _, w, u in sf.runtime.timeline if u == 0 and w in ("early_update_done", "update_start")]
+    assert marks.count("update_start") == 3, marks
+    # one early part per step (run by the late part itself if it came first)
+    assert marks.count("early_update_done") == (3 if early else 0), marks
+    sf.close()
+
+
 def test_cast_at_use_loss_parity(dev):
     """Casts where the unit is next used, against the non-offloaded run:
     first-step gradients and 10 losses."""

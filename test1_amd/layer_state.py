@@ -107,12 +107,17 @@ class LayerBufferPool:
             return len(self.pool)
 
 
+_BACKLOG_LOCK = threading.Lock()
+
+
 def _backlog(copies: deque) -> int:
     """Drop the completed events at the front of ``copies`` (one stream, so
-    they complete in order) and count the rest."""
-    while copies and copies[0].query():
-        copies.popleft()
-    return len(copies)
+    they complete in order) and count the rest.  Several threads trim (the
+    update thread, the threads that issue copies); appends need no lock."""
+    with _BACKLOG_LOCK:
+        while copies and copies[0].query():
+            copies.popleft()
+        return len(copies)
 
 
 def split_into_pieces(sizes: Sequence[int], piece_elems: int) -> List[Tuple[int, int]]:

@@ -315,3 +315,42 @@ def test_bench_refuses_more_than_one_gpu(args, env):
                        env={**os.environ, **env}, timeout=120)
     assert r.returncode == 2, (r.returncode, r.stderr[-500:])
     assert "one GPU only" in r.stderr
+
+
+def test_copy_backlog_trims_safely_from_several_threads():
+    """The copy backlog is trimmed by several threads at once while another
+    appends: no event is lost or popped twice, and the count ends at the
+    events still pending."""
+    import threading
+    from collections import deque
+
+    from test1_amd.layer_state import _backlog
+
+    class Ev:
+        def __init__(self, done):
+            self.done = done
+
+        def query(self):
+            return self.done
+
+    copies = deque(Ev(True) for _ in range(20000))
+    errors = []
+
+    def trim():
+        try:
+            for _ in range(2000):
+                _backlog(copies)
+        except BaseException as e:  # noqa: BLE001 - the test reports any failure
+            errors.append(e)
+
+    ts = [threading.Thread(target=trim) for _ in range(4)]
+    for t in ts:
+        t.start()
+    for _ in range(5000):
+        copies.append(Ev(True))
+    for t in ts:
+        t.join()
+    copies.append(Ev(False))
+    copies.append(Ev(True))
+    assert not errors
+    assert _backlog(copies) == 2

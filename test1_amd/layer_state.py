@@ -733,11 +733,20 @@ class PriorityUpdateExecutor:
             self._cv.notify()
         return f
 
+    @staticmethod
+    def _ready(t) -> bool:
+        if t[5] is None:
+            return True
+        try:
+            return bool(t[5].query())
+        except BaseException:
+            return True   # a failed input: the task runs and reports it
+
     def _pick(self):
         """Under the lock: (task, must_wait).  The lowest-priority ready task,
         else the oldest task, to be waited for outside the lock."""
         for t in sorted(self._tasks, key=lambda t: (t[0], t[1])):
-            if t[5] is None or t[5].query():
+            if self._ready(t):
                 return t, False
         return min(self._tasks, key=lambda t: t[1]), True
 

@@ -354,3 +354,29 @@ def test_copy_backlog_trims_safely_from_several_threads():
     copies.append(Ev(True))
     assert not errors
     assert _backlog(copies) == 2
+
+
+def test_priority_update_executor_survives_a_failing_readiness_query():
+    """A task whose readiness query raises is run (and reports its own
+    error) instead of stopping the worker thread; later tasks still run."""
+    from test1_amd.layer_state import PriorityUpdateExecutor
+
+    class Broken:
+        def query(self):
+            raise RuntimeError("event lost")
+
+        def synchronize(self):
+            raise RuntimeError("event lost")
+
+    ex = PriorityUpdateExecutor("test-exec")
+    try:
+        def boom():
+            raise ValueError("input failed")
+
+        f1 = ex.submit(0, boom, ready=Broken())
+        f2 = ex.submit(1, lambda: 42)
+        with pytest.raises(ValueError):
+            f1.result(timeout=10)
+        assert f2.result(timeout=10) == 42
+    finally:
+        ex.shutdown()

@@ -1631,6 +1631,10 @@ class LayerRuntimeState(nn.Module):
         if (not self.row_sparse or lookup is None or opt is None or not getattr(opt, "reference_order", False)
                 or not self.layer.weight.requires_grad):
             return
+        if getattr(opt, "offloader", None) is not None:
+            # moments on storage: the two parts would read the table's moments
+            # back twice, and that step is bound by storage, not by this wait
+            return
         ids, copied = lookup
         early = {"ids": ids, "ready": copied, "state": "queued"}
         self._early = early

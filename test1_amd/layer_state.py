@@ -1677,7 +1677,11 @@ class LayerRuntimeState(nn.Module):
         flat = ids.reshape(-1)
         ntok = flat.numel()
         pad = self.layer.padding_idx if self.layer.padding_idx is not None else -1
-        dense = torch.ops.aten.embedding_dense_backward(grad_out.reshape(ntok, H), flat, V, pad, False)
+        # ids outside the table were flagged by the lookup (the update raises
+        # for them); clamped here so that the dense backward never indexes
+        # outside the table.  Valid ids are unchanged.
+        dense = torch.ops.aten.embedding_dense_backward(grad_out.reshape(ntok, H), flat.clamp(0, V - 1), V, pad,
+                                                        False)
         if rt.capture is not None:
             rt.capture[("device_grads", self.layer_idx)] = [dense.detach().clone().view(V, H)]
         if self._rows_host is None or self._rows_host.shape[0] < ntok:

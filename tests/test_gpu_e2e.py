@@ -230,6 +230,28 @@ def test_embedding_early_rows(dev, early):
     sf.close()
 
 
+def test_out_of_range_input_id_raises_at_the_update(dev):
+    """An input id just past the vocabulary (labels valid): the lookup's
+    bounds check flags it instead of reading outside the host table, the
+    backward's dense embedding gradient stays inside the table, the
+    embedding's early rows are skipped, and its update raises ValueError,
+    which wait_for_updates reports."""
+    from test1_amd import SlideFSDP, SlideFSDPConfig
+
+    sf = SlideFSDP(make_model(), SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD), wait_timeout=120)
+    ids = batches(1)[0]
+    labels = ids.clone()
+    ids[0, 5] = V
+    sf(input_ids=ids.to(dev), labels=labels.to(dev))
+    with pytest.raises(ValueError, match="outside"):
+        sf.wait_for_updates()
+    assert sf.layer_optimizer._early_rows == {}
+    try:
+        sf.close()
+    except ValueError:
+        pass
+
+
 def test_cast_at_use_loss_parity(dev):
     """Casts where the unit is next used, against the non-offloaded run:
     first-step gradients and 10 losses."""

@@ -189,6 +189,13 @@ class _SlotPool:
         self._lock = threading.Lock()
 
     def take(self, n: int) -> Optional[Tuple[torch.Tensor, Optional[torch.cuda.Event]]]:
+        """A buffer of ``n`` elements: the free one given back last, else a
+        new one.  The last one's cast is usually still queued on the forward's
+        stream, so the next copy into it waits for the forward to reach that
+        cast; measured on one box, 30 steps each, this ran at 5,543 and 5,611
+        tokens/s, preferring buffers whose cast had finished (then the oldest)
+        at 4,883 and 4,236, and casting as soon as the copy lands at 5,303 and
+        5,323."""
         with self._lock:
             free = self._free.get(n)
             if free:

@@ -64,7 +64,10 @@ typedef struct sf_seg {
 /* Text for any status returned by this library (never NULL). */
 const char* sf_error_string(int status);
 
-/* ABI version, bumped on any incompatible change. */
+/* ABI version, bumped on any incompatible change (SF_ABI_VERSION).
+ * 2: row_slot markers of the row-wise AdamW (SF_ROW_SKIP; other values
+ *    below SF_ROW_SKIP are an error). */
+#define SF_ABI_VERSION 2
 int sf_abi_version(void);
 
 /* ---------------------------------------------------------------------

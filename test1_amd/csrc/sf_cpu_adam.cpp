@@ -295,7 +295,7 @@ const char* sf_error_string(int status) {
     return "sf: unknown status";
 }
 
-int sf_abi_version(void) { return 1; }
+int sf_abi_version(void) { return SF_ABI_VERSION; }
 
 int sf_cpu_set_threads(int nthreads) {
     g_threads = nthreads;

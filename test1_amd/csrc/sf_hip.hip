@@ -351,7 +351,7 @@ const char* sf_error_string(int status) {
     }
 }
 
-int sf_abi_version(void) { return 1; }
+int sf_abi_version(void) { return SF_ABI_VERSION; }
 
 }  // extern "C"
 
@@ -363,7 +363,18 @@ namespace {
 // first and the last launch's own dispatch, so they time the kernels alone,
 // not what the stream waited for before them.
 int cast_launch(const float* src, uint16_t* dst, size_t n, hipStream_t st, hipEvent_t start, hipEvent_t stop) {
-    if (n == 0) return SF_OK;
+    if (n == 0) {
+        // nothing to launch: the events still mark the (empty) interval
+        if (start != nullptr) {
+            const hipError_t e = hipEventRecord(start, st);
+            if (e != hipSuccess) return hip_status(e);
+        }
+        if (stop != nullptr) {
+            const hipError_t e = hipEventRecord(stop, st);
+            if (e != hipSuccess) return hip_status(e);
+        }
+        return SF_OK;
+    }
     if (src == nullptr || dst == nullptr) return SF_EINVAL;
     const uintptr_t s = reinterpret_cast<uintptr_t>(src), d = reinterpret_cast<uintptr_t>(dst);
     // fp32 source [s, s+4n) and bf16 destination [d, d+2n) must not overlap:

@@ -59,6 +59,16 @@ def test_cast_unaligned_views(dev, src_off, dst_off):
     assert np.array_equal(bits16(out), exp)
 
 
+def test_timed_cast_of_nothing_records_its_events(dev):
+    """An empty timed cast launches nothing but still records both events,
+    so their elapsed time can be read (and is tiny)."""
+    timer = kernels.KernelTimer()
+    kernels.cast_f32_bf16_(torch.empty(0, dtype=torch.bfloat16, device=dev), torch.empty(0, device=dev),
+                           timer=timer)
+    torch.cuda.synchronize()
+    assert 0.0 <= timer.elapsed_ms() < 1.0
+
+
 @pytest.mark.parametrize("n,src_off", [(1 << 20, 0), ((1 << 20) + 5, 0), (4099, 1), (7, 0)])
 def test_timed_cast_times_the_kernel_alone(dev, n, src_off):
     """The timed cast (vector kernel, vector + tail, scalar only) gives the

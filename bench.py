@@ -303,29 +303,33 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
     return r
 
 
-def cast_alone(dev, n: int, reps: int = 20) -> dict:
+def cast_alone(dev, n: int, reps: int = 20, pairs: int = 4) -> dict:
     """The staging cast on an otherwise idle GPU, for context beside the
-    in-pipeline figure: one ``n``-element launch repeated ``reps`` times
-    (after 3 warmups) on a stream of its own, timed with HIP events stamped
-    around the kernel as in the pipeline figure."""
+    in-pipeline figure: ``n``-element launches (after 3 warmups) on a stream
+    of their own, timed with HIP events stamped around the kernel as in the
+    pipeline figure.  The launches cycle through ``pairs`` source/destination
+    pairs (6 B x n each, 5 GB for a Llama-3-8B layer and 4 pairs), so that no
+    launch finds its operands in the 256 MB Infinity Cache."""
     import torch
 
     from test1_amd import kernels
 
-    src = torch.randn(n, device=dev)
-    dst = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    bufs = [(torch.randn(n, device=dev), torch.empty(n, dtype=torch.bfloat16, device=dev)) for _ in range(pairs)]
     st = torch.cuda.Stream(device=dev)
-    for _ in range(3):
+    for k in range(3):
+        src, dst = bufs[k % pairs]
         kernels.cast_f32_bf16_(dst, src, st)
     timers = [kernels.KernelTimer() for _ in range(reps)]
-    for t in timers:
+    for k, t in enumerate(timers):
+        src, dst = bufs[k % pairs]
         kernels.cast_f32_bf16_(dst, src, st, timer=t)
     st.synchronize()
     ms = sum(t.elapsed_ms() for t in timers) / reps
     gbs = 6 * n / (ms * 1e-3) / 1e9
-    del src, dst
+    del bufs
     torch.cuda.empty_cache()
-    return {"elements": n, "launches": reps, "avg_launch_ms": ms, "achieved": gbs, "frac": gbs / HBM_PEAK_GBS}
+    return {"elements": n, "launches": reps, "operand_pairs": pairs, "avg_launch_ms": ms, "achieved": gbs,
+            "frac": gbs / HBM_PEAK_GBS}
 
 
 def _storage_snapshot(sf) -> dict:

@@ -255,7 +255,14 @@ def step_schedule(num_decoders: int, act_offload: bool = True, first_decoder_fir
     reference does not use; the set of events is unchanged).
     ``resident_units`` (not in the reference) keep their forward load for the
     backward: their backward ("h2d", u, True) event is absent.
-    Parity unpinned beyond this restatement: the reference has no tests.
+    Pinned by (tests/test_schedule.py): an event model of the reference's
+    autograd nodes and residency flags (its forward records the nodes, its
+    backward replays them in reverse), which must give the same schedule for
+    every L = 1..8, every resident set, with and without checkpoint offload
+    and in both first-load orders; invariants read off the reference's hook
+    order; and planted mistakes (last decoder reloaded, prefetch two ahead,
+    grads flag dropped, late checkpoint prefetch, embedding reload missing)
+    that both checks must reject.
     """
     L = num_decoders
     out: List[Tuple] = [("h2d", 0, False), ("h2d", 1, False)]

@@ -147,3 +147,31 @@ def test_param_streaming_llama3_8b_32_layers(dev):
         r = fwd(r)
     torch.cuda.synchronize()
     assert torch.equal(h.view(torch.int16), r.view(torch.int16))
+
+
+def test_noop_sync_copies_are_bit_exact(dev):
+    """The one-GPU transfer strategy (reference distributed_sync.py:324-354):
+    ``gather_params_to_gpu`` copies a pinned bf16 layer into the device buffer
+    and ``reduce_gradients_to_master`` copies device grads into a pinned host
+    buffer, returning once they are there; both bit for bit, for an odd size
+    into larger buffers (the rest untouched)."""
+    from test1_amd import SlideFSDPConfig
+    from test1_amd.distributed_sync import create_distributed_sync
+
+    sync = create_distributed_sync(SlideFSDPConfig(device=dev))
+    g = torch.Generator().manual_seed(5)
+    n = 3_000_017
+    host = pinned_empty(n, torch.bfloat16)
+    host.copy_(torch.randn(n, generator=g).bfloat16())
+    gpu = torch.full((n + 64,), 7.0, dtype=torch.bfloat16, device=dev)
+    sync.gather_params_to_gpu(host, gpu)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(gpu[:n]), bits16(host))
+    assert bool((gpu[n:] == 7.0).all())
+
+    grads = (torch.randn(n, generator=g) * 1e-3).bfloat16().to(dev)
+    back = pinned_empty(n + 64, torch.bfloat16)
+    back.fill_(3.0)
+    sync.reduce_gradients_to_master(grads, back)   # synchronises before returning
+    assert np.array_equal(bits16(back[:n]), bits16(grads))
+    assert bool((back[n:] == 3.0).all())

@@ -151,11 +151,11 @@ def test_priority_update_executor_polls_instead_of_committing_to_the_oldest():
 
 
 def test_grad_slots_per_unit_are_sized_and_never_block(monkeypatch):
-    from test1_amd import layer_state
-    from test1_amd.layer_state import GradSlotsPerUnit
+    from test1_amd import grad_slots
+    from test1_amd.grad_slots import GradSlotsPerUnit
 
     # pinned memory needs a GPU; plain host tensors stand in for it here
-    monkeypatch.setattr(layer_state, "pinned_empty", lambda n, dt: torch.empty(n, dtype=dt))
+    monkeypatch.setattr(grad_slots, "pinned_empty", lambda n, dt: torch.empty(n, dtype=dt))
     slots = GradSlotsPerUnit({0: 10, 1: 0, 2: 7}, torch.bfloat16)
     assert slots.slots[0].numel() == 10 and slots.slots[2].numel() == 7
     assert slots.acquire(timeout=0, unit=2) == 2 and slots.acquire(timeout=0, unit=2) == 2
@@ -165,7 +165,7 @@ def test_grad_slots_per_unit_are_sized_and_never_block(monkeypatch):
 
 
 def test_grad_slots_fall_back_to_a_ring_when_pinning_fails(monkeypatch):
-    from test1_amd import _native, layer_state
+    from test1_amd import _native, grad_slots, layer_state
 
     calls = []
 
@@ -175,7 +175,7 @@ def test_grad_slots_fall_back_to_a_ring_when_pinning_fails(monkeypatch):
             raise _native.NativeError("sf_host_alloc failed: out of memory", _native.HIP_ERROR_OUT_OF_MEMORY)
         return torch.empty(n, dtype=dt)
 
-    monkeypatch.setattr(layer_state, "pinned_empty", fake_pinned)
+    monkeypatch.setattr(grad_slots, "pinned_empty", fake_pinned)
     rt = object.__new__(layer_state.StreamingRuntime)
     rt.grad_ring, rt._dtype, rt.offload_executor, rt.wait_timeout = None, torch.bfloat16, None, None
     rt.pool = type("P", (), {"max_param_size": 9})()
@@ -191,7 +191,7 @@ def test_grad_slots_fall_back_to_a_ring_when_pinning_fails(monkeypatch):
     def broken(n, dt):
         raise _native.NativeError("sf_host_alloc failed: invalid argument", 9001)
 
-    monkeypatch.setattr(layer_state, "pinned_empty", broken)
+    monkeypatch.setattr(grad_slots, "pinned_empty", broken)
     rt.grad_ring = None
     with pytest.raises(_native.NativeError):
         rt.init_grad_slots({0: 5})
@@ -255,8 +255,8 @@ def test_grad_slot_ring_gives_big_units_their_own_slot_and_grows(monkeypatch):
     than twice the median size keep their own slot, the rest share a ring of
     slots of the largest remaining unit; ``grow`` pins more ring slots until
     the host refuses, then gives back enough for the headroom."""
-    from test1_amd import _native, layer_state
-    from test1_amd.layer_state import GradSlotRing
+    from test1_amd import _native, grad_slots
+    from test1_amd.grad_slots import GradSlotRing
 
     budget = {"left": 10}
 
@@ -266,7 +266,7 @@ def test_grad_slot_ring_gives_big_units_their_own_slot_and_grows(monkeypatch):
         budget["left"] -= 1
         return torch.empty(n, dtype=dt)
 
-    monkeypatch.setattr(layer_state, "pinned_empty", fake_pinned)
+    monkeypatch.setattr(grad_slots, "pinned_empty", fake_pinned)
     sizes = {0: 40, 1: 10, 2: 10, 3: 9, 4: 10, 5: 10, 6: 10, 7: 10, 8: 10, 9: 100}
     ring = GradSlotRing(sizes, 2, torch.bfloat16)
     assert ring.big == {0: 40, 9: 100} and ring.slot_elems == 10 and ring.depth == 2

@@ -143,7 +143,7 @@ class RowSparseEmbedding:
         rt.mark("early_update_start", self.layer_idx)
         slot = torch.full((V,), _native.SF_ROW_ZERO, dtype=torch.int64)
         slot[ids] = _native.SF_ROW_SKIP
-        if rt.capture is not None:
+        if rt.capturing(self.layer_idx):
             early["master_before"] = self._cpu_params_flat.clone()
         rt.set_adam_threads()
         with self.update_lock:
@@ -169,7 +169,7 @@ class RowSparseEmbedding:
         # outside the table.  Valid ids are unchanged.
         dense = torch.ops.aten.embedding_dense_backward(grad_out.reshape(ntok, H), flat.clamp(0, V - 1), V, pad,
                                                         False)
-        if rt.capture is not None:
+        if rt.capturing(self.layer_idx):
             rt.capture[("device_grads", self.layer_idx)] = [dense.detach().clone().view(V, H)]
         if self._rows_host is None or self._rows_host.shape[0] < ntok:
             self._rows_host = pinned_empty((ntok, H), torch.bfloat16)
@@ -213,7 +213,7 @@ class RowSparseEmbedding:
                 raise RuntimeError(f"embedding unit {self.layer_idx}: the early part of the update failed")
             row_slot = torch.full((V,), _native.SF_ROW_SKIP if applied else _native.SF_ROW_ZERO, dtype=torch.int64)
             row_slot[ids] = torch.arange(ntok, dtype=torch.int64)
-            if rt.capture is not None:
+            if rt.capturing(self.layer_idx):
                 dense = torch.zeros(V, H, dtype=rows.dtype)
                 dense[ids] = rows
                 before = early["master_before"] if applied else self._cpu_params_flat.clone()

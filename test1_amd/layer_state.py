@@ -78,8 +78,6 @@ def _no_slot() -> None:
     return None
 
 
-
-
 class StreamingRuntime:
     """Objects shared by all units of one model: streams, pool, stager, grad
     ring, worker threads and the optional event trace."""
@@ -164,8 +162,15 @@ class StreamingRuntime:
         # Test hook: when a dict, each update stores {unit: (host grads, fp32
         # master before the update)} and each gradient offload stores
         # {("device_grads", unit): [param.grad clones]}, for checking the
-        # pack and the update against the oracle.
+        # pack and the update against the oracle.  ``capture_units`` (a set)
+        # limits it to those units (None: every unit), so that full-size
+        # models capture a few units instead of copying every one.
         self.capture: Optional[dict] = None
+        self.capture_units: Optional[set] = None
+
+    def capturing(self, unit: int) -> bool:
+        """True if the test hook ``capture`` records ``unit``."""
+        return self.capture is not None and (self.capture_units is None or unit in self.capture_units)
 
     def set_adam_threads(self) -> None:
         """Team size of the next host update (update thread).  With two or
@@ -565,7 +570,7 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
                 raise RuntimeError(f"unit {self.layer_idx}: grad of {name} is {g.dtype} on {g.device}, "
                                    f"expected {unit['param'].dtype} on {unit['param'].device}")
             grads.append((g.detach().contiguous().reshape(-1), off))
-        if self.runtime.capture is not None:
+        if self.runtime.capturing(self.layer_idx):
             self.runtime.capture[("device_grads", self.layer_idx)] = [
                 None if p.grad is None else p.grad.detach().clone() for p in self._params]
         grad_ready = _new_event()
@@ -782,7 +787,7 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
                 # grad buffer of the reference gives it (layer_state.py:297);
                 # no copy writes these ranges
                 rt.grad_ring.slots[slot][off:off + size].zero_()
-            master_before = self._cpu_params_flat.clone() if rt.capture is not None else None
+            master_before = self._cpu_params_flat.clone() if rt.capturing(self.layer_idx) else None
             staging = self._open_staging_pieces(plan[0]) if plan is not None and rt.stage_after_update else None
             try:
                 rt.set_adam_threads()

@@ -1,0 +1,178 @@
+"""Helpers of the full-size end-to-end GPU tests (Llama-3.1-8B and
+Qwen2.5-14B shapes): a non-offloaded bf16 copy of the model on the GPU, the
+oracle AdamW driven over a few captured units, and the checks of captured
+gradients, updates and staged weights.
+
+The oracle keeps real arrays only for the captured units; every other unit is
+stepped with one-element stand-ins per parameter.  The reference's AdamW
+scalars (beta^t, bias corrections) depend on the sequence of calls across all
+units and parameters (optimizer/layer_adam/csrc/cpu_adam.h:57-89), not on the
+data, so the stand-ins reproduce them exactly while the captured units get
+the full arithmetic."""
+
+import time
+
+import numpy as np
+import torch
+
+import oracle
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def same_bits(a, b) -> bool:
+    """Two 16-bit tensors (any device, any shape of equal numel) hold the same bits."""
+    return np.array_equal(u16(a).reshape(-1), u16(b).reshape(-1))
+
+
+def check_step1_against_reference(cap, ref_grads, units):
+    """SlideFSDP's step-1 device gradients of ``units`` equal the
+    non-offloaded run's, bit for bit."""
+    for u in units:
+        got, exp = cap[("device_grads", u)], ref_grads[u]
+        assert len(got) == len(exp), f"unit {u}: {len(got)} gradients, expected {len(exp)}"
+        for j, (a, b) in enumerate(zip(got, exp)):
+            assert a.numel() == b.numel() and same_bits(a, b), \
+                f"unit {u} parameter {j}: step-1 gradient differs from the non-offloaded run's"
+
+
+def unit_params(model):
+    """Parameters of each SlideFSDP unit in its flat order: [embedding] +
+    decoder layers + [final norm, lm_head]."""
+    m = model.model
+    return ([[m.embed_tokens.weight]] + [list(l.parameters()) for l in m.layers]
+            + [[m.norm.weight, model.lm_head.weight]])
+
+
+def gpu_bf16_copy(model, dev):
+    """The model's architecture on the GPU in bf16, each weight the RNE cast of
+    its fp32 weight (cast on the GPU parameter by parameter, so no second host
+    copy is made); rotary frequencies rebuilt in fp32 as in the host model."""
+    cfg = model.config
+    with torch.device("meta"):
+        gm = type(model)(cfg)
+    gm = gm.to(torch.bfloat16).to_empty(device=dev)
+    gm.model.rotary_emb = type(model.model.rotary_emb)(config=cfg).to(dev)
+    with torch.no_grad():
+        for (n, gp), (n2, p) in zip(gm.named_parameters(), model.named_parameters()):
+            assert n == n2, (n, n2)
+            gp.copy_(p.detach().to(dev))
+    return gm
+
+
+def reference_step(gm, ids, vocab, units):
+    """One forward/backward of the non-offloaded model with transformers' own
+    decoder forward (causal mask, rotary) and per-layer recompute; returns the
+    loss and the bf16 gradients of ``units`` (host)."""
+    gm.gradient_checkpointing_enable(gradient_checkpointing_kwargs={"use_reentrant": False})
+    gm.train()
+    gm.zero_grad(set_to_none=True)
+    hidden = gm.model(input_ids=ids, use_cache=False).last_hidden_state
+    logits = gm.lm_head(hidden)
+    del hidden
+    loss = torch.nn.functional.cross_entropy(logits[..., :-1, :].reshape(-1, vocab), ids[..., 1:].reshape(-1))
+    del logits
+    loss.backward()
+    ups = unit_params(gm)
+    grads = {u: [p.grad.detach().cpu() for p in ups[u]] for u in units}
+    return loss.item(), grads
+
+
+class CapturedOracle:
+    """LayerAdamOracle over every unit: real fp32 arrays for ``units``,
+    one-element stand-ins for the others (same calls, so the same scalars)."""
+
+    def __init__(self, model, units, lr, betas, eps, wd):
+        self.units = set(units)
+        self.orc = oracle.LayerAdamOracle(lr=lr, betas=betas, eps=eps, weight_decay=wd)
+        self.arrays = {}
+        self.nparams = []
+        for u, ps in enumerate(unit_params(model)):
+            if u in self.units:
+                arrs = [p.detach().numpy().copy() for p in ps]
+                self.arrays[u] = arrs
+            else:
+                arrs = [np.zeros(1, np.float32) for _ in ps]
+            self.nparams.append(len(ps))
+            self.orc.add_layer(arrs)
+
+    def flat(self, u):
+        return np.concatenate([a.reshape(-1) for a in self.arrays[u]])
+
+    def step(self, cap):
+        """Check and apply one step: for each captured unit, the runtime's
+        fp32 master before its update must equal the oracle's, and its packed
+        host gradients feed the oracle update.  Units are stepped last first,
+        the order the reference runs updates in."""
+        n_units = len(self.nparams)
+        for u in range(n_units - 1, -1, -1):
+            if u in self.units:
+                grads, master_before = cap[u]
+                before = self.flat(u)
+                assert np.array_equal(master_before.numpy().view(np.uint32), before.view(np.uint32)), \
+                    f"unit {u}: master before the update differs from the oracle's"
+                g = u16(grads)
+                parts, off = [], 0
+                for a in self.arrays[u]:
+                    parts.append(g[off:off + a.size].reshape(a.shape))
+                    off += a.size
+                assert off == g.size, f"unit {u}: {g.size} packed gradient elements, expected {off}"
+                self.orc.step_layer(u, parts)
+            else:
+                self.orc.step_layer(u, [np.zeros(1, np.float32)] * self.nparams[u])
+
+
+def check_packed_grads(cap, units):
+    """The packed host gradients equal the device gradients, bit for bit, in
+    layout order."""
+    for u in units:
+        exp = oracle.pack_b16([u16(g) for g in cap[("device_grads", u)]])
+        assert np.array_equal(u16(cap[u][0]), exp), f"unit {u}: packed grads differ from the device grads"
+
+
+def check_masters(sf, orc, units):
+    """The runtime's fp32 masters after the step equal the oracle's."""
+    for u in units:
+        got = sf.layer_states[u]._cpu_params_flat.numpy()
+        assert np.array_equal(got.view(np.uint32), orc.flat(u).view(np.uint32)), f"unit {u}: master after update"
+
+
+def check_moments(sf, orc, units):
+    for u in units:
+        m, v = sf.layer_optimizer.layer_states(u)
+        om, ov = orc.orc.moments(u)
+        assert np.array_equal(m.numpy().view(np.uint32), om.view(np.uint32)), f"unit {u} exp_avg"
+        assert np.array_equal(v.numpy().view(np.uint32), ov.view(np.uint32)), f"unit {u} exp_avg_sq"
+
+
+def check_staged(sf, orc, units, ids):
+    """A forward without labels stages every unit with its current master;
+    each captured unit that keeps a device buffer of its own stays bound
+    after it: its bf16 weights must be the oracle's cast of the oracle's
+    master.  Returns the units checked."""
+    with torch.no_grad():
+        sf(input_ids=ids)
+    torch.cuda.synchronize()
+    checked = []
+    for u in units:
+        st = sf.layer_states[u]
+        unit = st._current_gpu_cache
+        if unit is None:
+            continue
+        got = u16(unit["param"][:st.total_size])
+        assert np.array_equal(got, oracle.cast_f32_bf16(orc.flat(u))), f"unit {u}: staged bf16 weights"
+        checked.append(u)
+    return checked
+
+
+def timed(what, fn, *a, **k):
+    t = time.time()
+    r = fn(*a, **k)
+    say(f"{what}: {time.time() - t:.1f} s")
+    return r

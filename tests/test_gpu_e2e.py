@@ -1,9 +1,14 @@
 """SlideFSDP end to end on small Llama and Qwen2 models, across the runtime's
-options: staging order, update parity with the oracle (bit-exact), loss
-parity with a non-offloaded PyTorch bf16 run over 10 steps, padding masks,
-learning-rate changes and save_pretrained."""
+options: staging order, update parity with the oracle (bit-exact), parity
+with a non-offloaded PyTorch bf16 run over 10 steps (bit-identical gradients
+and losses where the output unit computes the loss as the reference does),
+padding masks, learning-rate changes and save_pretrained.
 
-import copy
+The non-offloaded run starts from the same bf16 weights and fp32 rotary
+frequencies (``fullsize.gpu_bf16_copy``): the same kernels then see the same
+bits, so offloading, recomputing from offloaded checkpoints and staging
+change nothing."""
+
 import os
 
 import numpy as np
@@ -11,6 +16,7 @@ import pytest
 import torch
 
 import oracle
+from fullsize import gpu_bf16_copy
 
 pytestmark = pytest.mark.gpu
 
@@ -391,7 +397,7 @@ def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, 
 def reference_losses(model, steps_ids, dev):
     """Non-offloaded run: bf16 model on the GPU, same loss as OutputLayer,
     fp32 masters updated by the oracle AdamW unit by unit (last unit first)."""
-    gm = copy.deepcopy(model).to(dev, torch.bfloat16)
+    gm = gpu_bf16_copy(model, dev)
     units_gpu = units_of(gm)
     masters = [[p.detach().float().numpy().copy() for p in ps] for ps in units_of(model)]
     orc = oracle.LayerAdamOracle(lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
@@ -461,17 +467,23 @@ def check_loss_parity(dev, arch, fused, cfg_kw, sf_kw):
             for u, ref_u in enumerate(ref_grads):
                 got = u16(cap[u][0]).view(np.int16).view(np.uint16)
                 exp = np.concatenate([g.reshape(-1) for g in ref_u])
-                # Same bf16 weights through the same kernels; reductions with
-                # atomics (the embedding backward) may differ in the last bits,
-                # so compare in relative L2 and report the bit-exact fraction.
                 gf = torch.from_numpy(got.view(np.int16).copy()).view(torch.bfloat16).float()
                 ef = torch.from_numpy(exp.view(np.int16).copy()).view(torch.bfloat16).float()
                 rel = ((gf - ef).norm() / ef.norm().clamp_min(1e-30)).item()
                 exact = float((got == exp).mean())
                 print(f"unit {u}: grad rel-L2 {rel:.2e}, bit-exact fraction {exact:.4f}")
-                assert rel < 1e-2, f"unit {u} grads"
+                if fused:
+                    # the chunked cross entropy sums the loss gradient in
+                    # another order than the reference's full-logits loss
+                    assert rel < 1e-2, f"unit {u} grads"
+                else:
+                    assert exact == 1.0, f"unit {u}: step-1 gradients differ from the non-offloaded run's"
     print("losses", [round(x, 5) for x in losses])
     print("ref   ", [round(x, 5) for x in ref_losses])
+    if not fused:
+        # same gradients and the same AdamW (the oracle's bits): the whole
+        # trajectory is the non-offloaded run's
+        assert losses == ref_losses, (losses, ref_losses)
     for a, b in zip(losses, ref_losses):
         assert abs(a - b) <= 1e-2 * abs(b), (a, b)
     # first step, same weights: equal up to the reference's bf16 loss (the
@@ -483,13 +495,13 @@ def check_loss_parity(dev, arch, fused, cfg_kw, sf_kw):
 def test_padding_mask_matches_non_offloaded_run(dev):
     """Left-padded batch: the padding mask reaches every layer (the causal
     mask is built as the model itself builds it) and the checkpointed mask
-    round-trips through host memory.  The logits of the padded sequence
-    equal a non-offloaded run's with the mask and differ from the run
-    without it; the loss is finite over two steps."""
+    round-trips through host memory.  The logits of the padded sequence's
+    real tokens equal a non-offloaded run's with the mask, bit for bit, and
+    differ from the run without it; the loss is finite over two steps."""
     from test1_amd import SlideFSDP, SlideFSDPConfig
 
     model = make_model()
-    gm = copy.deepcopy(model).to(dev, torch.bfloat16)
+    gm = gpu_bf16_copy(model, dev)
     ids = batches(1)[0].to(dev)
     mask = torch.ones_like(ids)
     mask[1, :40] = 0  # second sequence: 40 padding tokens in front
@@ -509,9 +521,10 @@ def test_padding_mask_matches_non_offloaded_run(dev):
     d_mask = rel(got[1, 40:], ref[1, 40:])
     d_nomask = rel(got[1, 40:], ref_nomask[1, 40:])
     print("padded sequence logits: rel-L2 vs masked reference", d_mask, "vs unmasked", d_nomask)
-    assert d_mask < 1e-2
-    assert d_nomask > 5 * d_mask and d_nomask > 1e-3
-    assert rel(got[0], ref[0]) < 1e-2  # the unpadded sequence is unaffected
+    # same weights and kernels: the real tokens' logits are the masked run's, bit for bit
+    assert torch.equal(got[1, 40:], ref[1, 40:])
+    assert d_nomask > 1e-3
+    assert torch.equal(got[0], ref[0])  # the unpadded sequence is unaffected
     loss2 = sf(input_ids=ids, attention_mask=mask, labels=labels).loss.item()
     sf.wait_for_updates()
     assert np.isfinite(out.loss.item()) and np.isfinite(loss2)

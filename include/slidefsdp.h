@@ -221,7 +221,12 @@ int sf_dma_get_engines(uint32_t* engine_mask);
  * to pinned host address segs[k].dst.  Segments of 4 MiB or more are split
  * evenly over the selected engines, others go round-robin.  One completion
  * handle per issued copy is written to signals (at most max_signals);
- * *nsignals receives their number. */
+ * *nsignals receives their number.  Every segment is checked before the
+ * first copy is issued.  If a later step fails (SF_ETOOMANY, or a ROCr call
+ * as SF_EDMA_BASE + status), the copies issued before it still run:
+ * *nsignals and signals[] then describe them, and the caller must wait for
+ * them (sf_dma_wait) before reusing the destinations or freeing the
+ * sources. */
 int sf_dma_copy_d2h(const sf_seg* segs, int nsegs, uint64_t* signals,
                     int max_signals, int* nsignals);
 

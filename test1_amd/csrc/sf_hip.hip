@@ -644,34 +644,49 @@ int sf_dma_init(int device) {
 }
 
 int sf_dma_set_engines(uint32_t engine_mask) {
+    std::lock_guard<std::mutex> lk(g_dma_mu);
     if (!g_dma.ok) return SF_EINVAL;
     g_dma.engine_mask = engine_mask & 0xFFFFu;
     return SF_OK;
 }
 
 int sf_dma_get_engines(uint32_t* engine_mask) {
+    std::lock_guard<std::mutex> lk(g_dma_mu);
     if (!g_dma.ok || engine_mask == nullptr) return SF_EINVAL;
     *engine_mask = g_dma.engine_mask;
     return SF_OK;
 }
 
+// On an error after some copies were issued, *nsignals holds their number and
+// signals[0 .. *nsignals) their handles: those copies run to completion, and
+// the caller waits for them (sf_dma_wait) before reusing the destination.
 int sf_dma_copy_d2h(const sf_seg* segs, int nsegs, uint64_t* signals, int max_signals, int* nsignals) {
     if (nsegs < 0 || (nsegs > 0 && (segs == nullptr || signals == nullptr)) || nsignals == nullptr) return SF_EINVAL;
-    if (!g_dma.ok) return SF_EINVAL;
     *nsignals = 0;
-    // Engines to spread over: the set bits of engine_mask, or one
+    uint32_t mask = 0;
+    hsa_agent_t cpu{0}, gpu{0};
+    {
+        std::lock_guard<std::mutex> lk(g_dma_mu);
+        if (!g_dma.ok) return SF_EINVAL;
+        mask = g_dma.engine_mask;
+        cpu = g_dma.cpu;
+        gpu = g_dma.gpu;
+    }
+    // Every segment is checked before the first copy is issued.
+    for (int i = 0; i < nsegs; ++i)
+        if (segs[i].n != 0 && (segs[i].src == 0 || segs[i].dst == 0)) return SF_EINVAL;
+    // Engines to spread over: the set bits of the engine mask, or one
     // runtime-chosen engine.
     uint32_t engines[16];
     int nengines = 0;
     for (int e = 0; e < 16; ++e)
-        if (g_dma.engine_mask & (1u << e)) engines[nengines++] = 1u << e;
+        if (mask & (1u << e)) engines[nengines++] = 1u << e;
     if (nengines == 0) engines[nengines++] = 0;
     constexpr uint64_t kSplit = uint64_t(4) << 20;  // split copies above 4 MiB
     int rr = 0;
     for (int i = 0; i < nsegs; ++i) {
         const uint64_t bytes = segs[i].n;
         if (bytes == 0) continue;
-        if (segs[i].src == 0 || segs[i].dst == 0) return SF_EINVAL;
         const int parts = (bytes >= kSplit && nengines > 1) ? nengines : 1;
         const uint64_t chunk = (bytes / parts) & ~uint64_t(4095);
         for (int k = 0; k < parts; ++k) {
@@ -685,10 +700,10 @@ int sf_dma_copy_d2h(const sf_seg* segs, int nsegs, uint64_t* signals, int max_si
             const void* src = reinterpret_cast<const char*>(segs[i].src) + off;
             const uint32_t eng = engines[rr++ % nengines];
             if (eng != 0)
-                st = hsa_amd_memory_async_copy_on_engine(dst, g_dma.cpu, src, g_dma.gpu, size_t(n), 0, nullptr, sig,
+                st = hsa_amd_memory_async_copy_on_engine(dst, cpu, src, gpu, size_t(n), 0, nullptr, sig,
                                                          static_cast<hsa_amd_sdma_engine_id_t>(eng), true);
             else
-                st = hsa_amd_memory_async_copy(dst, g_dma.cpu, src, g_dma.gpu, size_t(n), 0, nullptr, sig);
+                st = hsa_amd_memory_async_copy(dst, cpu, src, gpu, size_t(n), 0, nullptr, sig);
             if (st != HSA_STATUS_SUCCESS) {
                 hsa_signal_destroy(sig);
                 return hsa_status_to_sf(st);

@@ -10,6 +10,8 @@ gradient elsewhere (the dense update's bits).
 
 from __future__ import annotations
 
+import threading
+from concurrent import futures
 from typing import Any, Dict, Optional, Tuple
 
 import torch
@@ -54,6 +56,7 @@ class RowSparseEmbedding:
         self._ids_early_host: Optional[torch.Tensor] = None
         self._lookup_ids: Optional[Tuple[torch.Tensor, torch.cuda.Event]] = None
         self._early: Optional[Dict[str, Any]] = None
+        self._early_lock = threading.Lock()
 
     def _host_table(self) -> torch.Tensor:
         V, H = self._rows_shape
@@ -63,6 +66,7 @@ class RowSparseEmbedding:
     def gather_rows(self, ids: torch.Tensor) -> torch.Tensor:
         """Forward lookup: [*ids.shape, H] bf16 rows of the current master."""
         self.wait_for_update()
+        self.settle_orphaned_early()
         V, H = self._rows_shape
         flat = ids.reshape(-1)
         if flat.dtype != torch.int64:
@@ -130,30 +134,79 @@ class RowSparseEmbedding:
 
     def _do_update_rows_early(self, early: Dict[str, Any]) -> bool:
         """Update thread: the early part queued by ``start_early_update``
-        (nothing if the late part has already run it)."""
-        if early["state"] != "queued":
-            return False
+        (nothing if the late part has already run it or it was cancelled).
+        States: queued -> running -> applied, skipped (ids out of range: the
+        late part raises for them) or failed; queued -> cancelled."""
+        with self._early_lock:
+            if early["state"] != "queued":
+                return False
+            early["state"] = "running"
         rt = self.runtime
         V, H = self._rows_shape
-        early["ready"].synchronize()
-        ids = early["ids"]
-        if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= V):
-            early["state"] = "skipped"   # the late part raises for these ids
-            return False
-        rt.mark("early_update_start", self.layer_idx)
-        slot = torch.full((V,), _native.SF_ROW_ZERO, dtype=torch.int64)
-        slot[ids] = _native.SF_ROW_SKIP
-        if rt.capturing(self.layer_idx):
-            early["master_before"] = self._cpu_params_flat.clone()
-        rt.set_adam_threads()
-        with self.update_lock:
-            early["state"] = "failed"
-            self.layer_optimizer.step_rows_early(self.layer_idx, slot, param_view=self._cpu_params_flat.view(V, H),
-                                                 bf16_view=None if self._cpu_params_bf16 is None
-                                                 else self._cpu_params_bf16.view(V, H))
+        try:
+            kernels.wait_event(early["ready"], rt.wait_timeout, f"unit {self.layer_idx}: lookup ids")
+            ids = early["ids"]
+            if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= V):
+                early["state"] = "skipped"
+                return False
+            rt.mark("early_update_start", self.layer_idx)
+            slot = torch.full((V,), _native.SF_ROW_ZERO, dtype=torch.int64)
+            slot[ids] = _native.SF_ROW_SKIP
+            if rt.capturing(self.layer_idx):
+                early["master_before"] = self._cpu_params_flat.clone()
+            rt.set_adam_threads()
+            with self.update_lock:
+                self.layer_optimizer.step_rows_early(self.layer_idx, slot,
+                                                     param_view=self._cpu_params_flat.view(V, H),
+                                                     bf16_view=None if self._cpu_params_bf16 is None
+                                                     else self._cpu_params_bf16.view(V, H))
             early["state"] = "applied"
+        except BaseException:
+            early["state"] = "failed"
+            raise
         rt.mark("early_update_done", self.layer_idx)
         return True
+
+    def settle_orphaned_early(self) -> None:
+        """Close an early part whose late part will never run: the step's
+        backward failed before it reached the lookup.  A part still queued is
+        cancelled; one that ran began the table's step (its untouched rows
+        were updated with zero gradient), which is completed here with zero
+        gradient for the batch's rows as well, so that every row of the table
+        has taken the same step and the next step starts from a consistent
+        table and step counter.  Waits for a part that is running, so that no
+        update writes the table while the next lookup reads it."""
+        early, self._early = getattr(self, "_early", None), None
+        if early is None:
+            return
+        rt = self.runtime
+        with self._early_lock:
+            cancelled = early["state"] == "queued"
+            if cancelled:
+                early["state"] = "cancelled"
+        f = early.get("future")
+        if cancelled:
+            if f is not None:
+                f.cancel()   # the worker skips it (or finds it cancelled)
+        elif f is not None:
+            try:
+                f.result(timeout=rt.wait_timeout)
+            except futures.TimeoutError:
+                raise TimeoutError(f"Layer {self.layer_idx}: early update not finished after "
+                                   f"{rt.wait_timeout:g} s") from None
+            except Exception:
+                pass   # its state says what happened
+        opt = self.layer_optimizer
+        if early["state"] == "applied":
+            V, H = self._rows_shape
+            row_slot = torch.full((V,), _native.SF_ROW_SKIP, dtype=torch.int64)
+            row_slot[early["ids"]] = _native.SF_ROW_ZERO
+            no_rows = torch.empty((0, H), dtype=torch.bfloat16)
+            with self.update_lock:
+                opt.step_rows(self.layer_idx, row_slot, no_rows, param_view=self._cpu_params_flat.view(V, H),
+                              bf16_view=None if self._cpu_params_bf16 is None else self._cpu_params_bf16.view(V, H))
+        elif early["state"] == "failed":
+            opt.abandon_early_step(self.layer_idx)
 
     def offload_rows(self, grad_out: torch.Tensor, ids: torch.Tensor) -> None:
         """Backward of the lookup: dense table gradient on the device (as the
@@ -192,20 +245,21 @@ class RowSparseEmbedding:
         done.record(rt.d2h_stream)
         self._grads_offloaded = True
         self._bwd_compute_done = True
+        # this step's early part (if any) now belongs to the late part
+        early, self._early = self._early, None
         self._update_future = rt.update_executor.submit(rt.update_priority(self.layer_idx), self._do_update_rows,
-                                                        done, ntok, ready=self._update_ready(done))
+                                                        done, ntok, early, ready=self._update_ready(done))
 
-    def _do_update_rows(self, d2h_done: torch.cuda.Event, ntok: int) -> bool:
+    def _do_update_rows(self, d2h_done: torch.cuda.Event, ntok: int, early: Optional[Dict[str, Any]]) -> bool:
         rt = self.runtime
         V, H = self._rows_shape
         try:
             rt.mark("update_start", self.layer_idx)
-            d2h_done.synchronize()
+            kernels.wait_event(d2h_done, rt.wait_timeout, f"unit {self.layer_idx}: gradient rows")
             if int(self._bad_ids[0]) != 0:
                 raise ValueError(f"embedding unit {self.layer_idx}: input ids outside [0, {V})")
             ids = self._ids_host[:ntok]
             rows = self._rows_host[:ntok]
-            early, self._early = self._early, None
             if early is not None and early["state"] == "queued":
                 self._do_update_rows_early(early)   # not run yet: now, on this thread
             applied = early is not None and early["state"] == "applied"

@@ -12,7 +12,7 @@ import ctypes
 import threading
 import time
 import os
-from typing import Optional, Sequence, Tuple
+from typing import Callable, Optional, Sequence, Tuple
 
 import torch
 
@@ -304,11 +304,44 @@ def dma_enable_timing(on: bool) -> None:
     _native.check(_native.hip().sf_dma_enable_timing(1 if on else 0), "sf_dma_enable_timing")
 
 
-def dma_copy_d2h(pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]]):
+class DmaCopiesOutstanding(TimeoutError):
+    """SDMA copies that had not completed when a bounded wait for them ended.
+    Their destinations must not be reused nor their sources freed: an engine
+    may still be moving the bytes."""
+
+
+def _poll(done: Callable[[], bool], timeout: Optional[float]) -> bool:
+    """Poll ``done`` with short sleeps (10 us doubling to 100 us) until it is
+    true (returns True) or ``timeout`` seconds have passed (False); None
+    waits without limit."""
+    deadline = None if timeout is None else time.monotonic() + timeout
+    pause = 10e-6
+    while not done():
+        if deadline is not None and time.monotonic() >= deadline:
+            return False
+        time.sleep(pause)
+        pause = min(pause * 2, 100e-6)
+    return True
+
+
+def wait_event(ev, timeout: Optional[float], what: str) -> None:
+    """Block until the device event ``ev`` has completed: ``synchronize()``
+    without a limit, else polling ``query()`` until ``timeout`` seconds,
+    then ``TimeoutError`` naming ``what``."""
+    if timeout is None:
+        ev.synchronize()
+        return
+    if not _poll(ev.query, timeout):
+        raise TimeoutError(f"{what}: not complete after {timeout:g} s")
+
+
+def dma_copy_d2h(pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]], timeout: Optional[float] = None):
     """Start SDMA copies of each contiguous GPU ``src`` into the pinned host
     ``dst`` of equal byte size.  The sources must already be complete on the
     device.  Returns a handle for ``dma_wait``; keep the tensors alive until
-    then."""
+    then.  If the library fails after issuing some of the copies, they are
+    waited for (up to ``timeout`` seconds, else ``DmaCopiesOutstanding``) and
+    released before the error is raised, so no copy outlives the call."""
     segs = []
     for k, (src, dst) in enumerate(pairs):
         _require_cuda(src, f"pair {k} src")
@@ -324,9 +357,24 @@ def dma_copy_d2h(pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]]):
     cap = 16 * max(1, len(segs))
     handles = (ctypes.c_uint64 * cap)()
     count = ctypes.c_int(0)
-    _native.check(_native.hip().sf_dma_copy_d2h(arr, len(segs), handles, cap, ctypes.byref(count)),
-                  "sf_dma_copy_d2h")
-    return (handles, count.value)
+    rc = _native.hip().sf_dma_copy_d2h(arr, len(segs), handles, cap, ctypes.byref(count))
+    return _issued_or_raise(rc, handles, count.value, timeout)
+
+
+def _issued_or_raise(rc: int, handles, n: int, timeout: Optional[float]):
+    """The handle of the ``n`` copies an ``sf_dma_copy_d2h`` call started; if
+    the call failed, those copies are waited for and released first, and the
+    call's error is raised (``DmaCopiesOutstanding`` if they do not complete
+    within ``timeout`` seconds)."""
+    if rc != 0:
+        if n > 0:
+            issued = (handles, n)
+            if not _poll(lambda: dma_query(issued), timeout):
+                raise DmaCopiesOutstanding(f"sf_dma_copy_d2h failed (status {rc}) with {n} copies issued that "
+                                           f"did not complete within {timeout:g} s")
+            dma_wait(issued)
+        _native.check(rc, "sf_dma_copy_d2h")
+    return (handles, n)
 
 
 def dma_query(handle) -> bool:
@@ -344,8 +392,9 @@ class DmaReady:
     signals) is allowed only after completion was seen, and later queries
     then never touch the freed signals."""
 
-    def __init__(self, handle):
+    def __init__(self, handle, timeout: Optional[float] = None):
         self.handle = handle
+        self.timeout = timeout
         self._done = False
         self._released = False
         self._lock = threading.Lock()
@@ -357,8 +406,10 @@ class DmaReady:
             return self._done
 
     def synchronize(self) -> None:
-        while not self.query():
-            time.sleep(50e-6)
+        """Wait until the copies have completed, at most ``timeout`` seconds
+        (then ``DmaCopiesOutstanding``)."""
+        if not _poll(self.query, self.timeout):
+            raise DmaCopiesOutstanding(f"{self.handle[1]} SDMA copies not complete after {self.timeout:g} s")
 
     def release(self) -> Tuple[int, int]:
         """Wait for the copies, free their signals and return their (start,

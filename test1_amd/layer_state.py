@@ -49,6 +49,7 @@ from __future__ import annotations
 import threading
 import time
 from collections import OrderedDict
+from concurrent import futures
 from concurrent.futures import Future
 from typing import Any, Callable, Dict, List, Optional, Tuple
 
@@ -85,6 +86,8 @@ class StreamingRuntime:
     def __init__(self, device: torch.device, dtype: torch.dtype, max_param_size: int, pool_size: int,
                  stage_chunk_elems: int, stage_depth: int, grad_ring_depth: int, wait_timeout: Optional[float],
                  d2h_workgroups: int = 8, d2h_engine: str = "sdma", h2d_format: str = "fp32"):
+        if wait_timeout is not None and not wait_timeout > 0:
+            raise ValueError("wait_timeout must be a positive number of seconds or None")
         if d2h_engine not in ("sdma", "kernel", "copy"):
             raise ValueError("d2h_engine must be 'kernel', 'copy' or 'sdma'")
         if h2d_format not in ("fp32", "bf16"):
@@ -167,6 +170,13 @@ class StreamingRuntime:
         # models capture a few units instead of copying every one.
         self.capture: Optional[dict] = None
         self.capture_units: Optional[set] = None
+        self._held: List[Any] = []
+
+    def hold_forever(self, objs) -> None:
+        """Keep ``objs`` referenced until the process ends: the host slot and
+        the device tensors of copies that never completed, which an engine
+        may still write into or read from."""
+        self._held.append(objs)
 
     def capturing(self, unit: int) -> bool:
         """True if the test hook ``capture`` records ``unit``."""
@@ -235,9 +245,13 @@ class StreamingRuntime:
             self.timeline.append((time.perf_counter(), threading.current_thread().name, what, unit))
 
     def shutdown(self) -> None:
-        if self.offload_executor is not None:
-            self.offload_executor.shutdown(wait=True)
-        self.update_executor.shutdown(wait=True)
+        """Finish the queued offloads and updates and stop both worker
+        threads (each join bounded by ``wait_timeout``)."""
+        try:
+            if self.offload_executor is not None:
+                self.offload_executor.shutdown(wait=True, timeout=self.wait_timeout)
+        finally:
+            self.update_executor.shutdown(wait=True, timeout=self.wait_timeout)
 
     def release_slots(self, states) -> None:
         """Give back the whole-unit slots of stagings not yet cast (their units
@@ -369,12 +383,43 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
         """Recompute the bf16 host copy from the fp32 master (bf16 H2D only)
         and drop a staging made for the next forward.  Updates keep both
         current; call this after writing the master directly."""
-        with self._prefetch_lock:
-            old, self._prefetched = self._prefetched, None
-        if old is not None and isinstance(old[1], PendingCast):
-            self.runtime.stager.drop_pending(old[1])
+        self._drop_prefetched()
         if self._cpu_params_bf16 is not None and self.total_size:
             _cpu_adam.cast_f32_bf16(self._cpu_params_flat, self._cpu_params_bf16)
+
+    def _drop_prefetched(self) -> None:
+        """Forget a staging made for the next forward (its master changed): a
+        copy not cast yet gives its slot back; a cast already issued becomes
+        the unit's last writer, which the next staging into it waits for."""
+        with self._prefetch_lock:
+            old, self._prefetched = self._prefetched, None
+        if old is None:
+            return
+        unit, done = old
+        if isinstance(done, PendingCast):
+            self.runtime.stager.drop_pending(done)
+        elif done is not None:
+            unit["ready"] = done
+
+    def release_device_unit(self) -> None:
+        """Give back this unit's device buffer if it is still loaded (after a
+        forward without a backward, units with a buffer of their own, the
+        last decoder and the output unit stay loaded) and point its
+        parameters at their fp32 master views again; drop a pending cast and
+        a staging made for the next forward.  Call before writing the
+        master directly: while the unit is loaded, ``param.data`` is its bf16
+        device view and a write there would not reach the master."""
+        unit = self._current_gpu_cache
+        if unit is not None:
+            self._drop_pending_cast()
+            ev = _new_event()
+            ev.record(torch.cuda.current_stream())
+            unit["ready"] = ev
+            self._bind_host_views()
+            self._current_gpu_cache = None
+            self._bwd_armed = False
+            self._release_unit(unit)
+        self._drop_prefetched()
 
     def stage_for_next_forward(self) -> None:
         """Stage the freshly updated master into this unit's own device buffer
@@ -493,7 +538,10 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
     def _acquire_unit(self) -> Dict[str, Any]:
         if self._own_unit is not None:
             return self._own_unit
-        return self.buffer_pool.acquire(timeout=self.runtime.wait_timeout)
+        try:
+            return self.buffer_pool.acquire(timeout=self.runtime.wait_timeout)
+        except TimeoutError as e:
+            raise TimeoutError(f"Layer {self.layer_idx}: {e}") from None
 
     def _release_unit(self, unit: Dict[str, Any]) -> None:
         if unit is not self._own_unit:
@@ -654,6 +702,7 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
                 slot = own(self.layer_idx)
         rt.mark("d2h_task", self.layer_idx)
         rt.mark("slot", self.layer_idx)
+        issued: List[Any] = []   # SDMA copies started so far (not stream-ordered)
         try:
             host = rt.grad_ring.slots[slot]
             pairs = [(g, host[off:off + g.numel()]) for g, off in grads]
@@ -661,24 +710,23 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
                 # The gradients must be complete before an SDMA engine reads
                 # them (the copy is not stream-ordered): wait here, on this
                 # worker thread, then hand the copy to the engine.
-                grad_ready.synchronize()
+                kernels.wait_event(grad_ready, rt.wait_timeout, f"unit {self.layer_idx}: gradients")
                 rt.mark("grad_ready", self.layer_idx)
                 plan = self._piece_plan()
                 if plan is None:
-                    handles = [kernels.dma_copy_d2h(pairs)]
+                    issued.append(kernels.dma_copy_d2h(pairs, timeout=rt.wait_timeout))
                 else:
                     # one copy per piece, in update order: the update starts
                     # once the first has landed
                     spans = [(off, g.numel()) for g, off in grads]
-                    handles = []
                     for a, b in plan[0]:
                         sub = [(grads[i][0][lo:hi], host[grads[i][1] + lo:grads[i][1] + hi])
                                for i, lo, hi in overlap_ranges(spans, a, b)]
-                        handles.append(kernels.dma_copy_d2h(sub) if sub else None)
+                        issued.append(kernels.dma_copy_d2h(sub, timeout=rt.wait_timeout) if sub else None)
                 rt.mark("dma_issued", self.layer_idx)
                 done = None
-                dma_ready = [None if h is None else kernels.DmaReady(h) for h in handles]
-                handle = handles
+                dma_ready = [None if h is None else kernels.DmaReady(h, timeout=rt.wait_timeout) for h in issued]
+                handle = issued
             else:
                 rt.d2h_stream.wait_event(grad_ready)
                 if cast_fence is not None:
@@ -700,22 +748,42 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
                 if timing:
                     rt.d2h_timing.append((t0, done, 2 * sum(g.numel() for g, _ in grads)))
                 handle = None
+            nbytes = 2 * sum(g.numel() for g, _ in grads)
+            # With SDMA the gradient tensors stay referenced until the copy is
+            # waited for; the caching allocator cannot hand them out before then.
+            keep = grads if handle is not None else None
+            if handle is None:
+                ready = done
+            else:
+                ready = next((d for d in dma_ready if d is not None), None)
+            self._update_future = rt.update_executor.submit(
+                rt.update_priority(self.layer_idx), self._do_update, slot, done, missing,
+                None if handle is None else dma_ready, keep, nbytes, ready=self._update_ready(ready))
         except BaseException:
-            rt.grad_ring.release(slot)
-            self.update_finished.set()
+            self._abandon_copies(issued, grads, slot)
             raise
-        nbytes = 2 * sum(g.numel() for g, _ in grads)
-        # With SDMA the gradient tensors stay referenced until the copy is
-        # waited for; the caching allocator cannot hand them out before then.
-        keep = grads if handle is not None else None
-        del grads, pairs
-        if handle is None:
-            ready = done
+
+    def _abandon_copies(self, issued, grads, slot) -> None:
+        """After a failed offload: the SDMA copies already started must land
+        before the host slot is handed back and the gradients are freed.
+        Copies that do not complete within the wait limit keep both for the
+        life of the process (an engine may still write into the slot)."""
+        rt = self.runtime
+        try:
+            for h in issued:
+                if h is not None:
+                    kernels.DmaReady(h, timeout=rt.wait_timeout).release()
+            if rt.d2h_engine != "sdma":
+                # stream-ordered copies that may have been enqueued
+                drained = _new_event()
+                drained.record(rt.d2h_stream)
+                kernels.wait_event(drained, rt.wait_timeout, f"unit {self.layer_idx}: gradient copies")
+        except TimeoutError:
+            rt.hold_forever((grads, issued, slot))
         else:
-            ready = next((d for d in dma_ready if d is not None), None)
-        self._update_future = rt.update_executor.submit(rt.update_priority(self.layer_idx), self._do_update,
-                                                        slot, done, missing, None if handle is None else dma_ready,
-                                                        keep, nbytes, ready=self._update_ready(ready))
+            rt.grad_ring.release(slot)
+        finally:
+            self.update_finished.set()
 
     def _update_ready(self, grads_ready):
         """Readiness of this unit's update: its gradients on the host and,
@@ -778,7 +846,7 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
         try:
             rt.mark("update_start", self.layer_idx)
             if d2h_done is not None:
-                d2h_done.synchronize()
+                kernels.wait_event(d2h_done, rt.wait_timeout, f"unit {self.layer_idx}: gradient copy")
             plan = self._piece_plan() if self.layer_optimizer is not None else None
             if plan is None or len(chunks) not in (0, len(plan[0])):
                 wait_chunks(len(chunks))
@@ -818,7 +886,12 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
         finally:
             try:
                 # every gradient copy has landed before the slot is handed back
-                wait_chunks(len(chunks))
+                # and the gradients are freed
+                try:
+                    wait_chunks(len(chunks))
+                except kernels.DmaCopiesOutstanding:
+                    rt.hold_forever((keep, chunks, slot))
+                    raise
                 del keep
                 if rt.d2h_timing is not None and state["t0"] is not None:
                     rt.d2h_timing.append(("interval_ns", state["t0"], state["t1"], nbytes))
@@ -835,11 +908,13 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
         """Block until this unit's last update finished; re-raise its error.
         A unit whose offload is still queued is waited for as well."""
         t = timeout if timeout is not None else self.runtime.wait_timeout
-        if self._d2h_future is not None:
-            self._d2h_future.result(timeout=t)
-        f = self._update_future
-        if f is not None:
-            f.result(timeout=t)
+        for what, f in (("gradient offload", self._d2h_future), ("parameter update", self._update_future)):
+            if f is None:
+                continue
+            try:
+                f.result(timeout=t)
+            except futures.TimeoutError:
+                raise TimeoutError(f"Layer {self.layer_idx} {what} not finished after {t:g} s") from None
         if not self.update_finished.wait(timeout=t):
             raise TimeoutError(f"Layer {self.layer_idx} parameter update timed out")
 

@@ -408,6 +408,12 @@ class LayerAdam:
         finally:
             self._post_step(layer_idx)
 
+    def abandon_early_step(self, layer_idx: int) -> None:
+        """Forget a step begun by ``step_rows_early`` that will not be
+        completed (its early part failed); the next ``step_rows`` then starts
+        a step of its own."""
+        self._early_rows.pop(layer_idx, None)
+
     @torch.no_grad()
     def step_rows(self, layer_idx: int, row_slot: torch.Tensor, rows: torch.Tensor,
                   param_view: torch.Tensor, bf16_view: Optional[torch.Tensor] = None):

@@ -132,6 +132,11 @@ def adam_threads() -> int:
     return max(1, n - 1)
 
 
+# Seconds a host wait of the runtime (a pool unit, a gradient slot, a unit's
+# offload or update, a copy's completion) may take before it raises.
+DEFAULT_WAIT_TIMEOUT = 600.0
+
+
 class SlideFSDP(nn.Module):
     """Layer-streaming trainer (reference slide_fsdp.py:116-211).
 
@@ -145,7 +150,11 @@ class SlideFSDP(nn.Module):
                          gradient offload never waits for the host optimizer
                          (2 bytes of pinned host memory per parameter)
       wait_timeout       seconds before a host wait raises TimeoutError
-                         (default None: wait forever, as the reference)
+                         naming the unit (default 600: a lost copy
+                         completion or a wedged worker thread ends the step
+                         with an error instead of blocking it forever, as
+                         the reference's unbounded waits would; None: wait
+                         without limit)
       d2h_engine         "sdma" (default): gradient D2H on SDMA engines of its
                          own; "kernel": by a capped-grid pack kernel writing
                          into host memory (slows the backward kernels beside
@@ -210,7 +219,8 @@ class SlideFSDP(nn.Module):
     """
 
     def __init__(self, model, config: SlideFSDPConfig, *, stage_chunk_elems: Optional[int] = None,
-                 stage_depth: int = 3, grad_ring_depth: Optional[int] = None, wait_timeout: Optional[float] = None,
+                 stage_depth: int = 3, grad_ring_depth: Optional[int] = None,
+                 wait_timeout: Optional[float] = DEFAULT_WAIT_TIMEOUT,
                  d2h_engine: str = "sdma", h2d_format: str = "fp32",
                  resident_layers: Optional[int] = None, row_sparse_embedding: bool = True,
                  fused_cross_entropy: bool = False, stage_after_update: bool = True,
@@ -624,9 +634,40 @@ class SlideFSDP(nn.Module):
                 # the backward below reaches the lookup: the embedding's
                 # gradient-free rows can be updated while it starts
                 self.layer_states[0].start_early_update()
-            loss.backward()
+            try:
+                loss.backward()
+            except BaseException:
+                self._after_failed_backward()
+                raise
             self._grow_grad_ring()
         return CausalLMOutputWithPast(loss=loss, logits=logits)
+
+    def _after_failed_backward(self) -> None:
+        """The backward raised part-way (a hook, an out-of-memory error, an
+        interrupt): the units it finished were offloaded and their updates
+        queued, the others never were.  Let the queued work finish, close the
+        embedding's early update part (its late part will not come), give
+        back every unit still on the device and drop gradients, so the next
+        step starts from the masters as they are.  Errors here are secondary
+        to the one being raised and are not reported."""
+        for s in self.layer_states:
+            try:
+                s.wait_for_update()
+            except Exception:
+                pass
+        try:
+            if self.layer_states[0].row_sparse:
+                self.layer_states[0].settle_orphaned_early()
+        except Exception:
+            pass
+        for s in self.layer_states:
+            with s._grad_lock:
+                s._bwd_armed = False
+                s._post_called = False
+                s._grads_seen = 0
+            s.release_device_unit()
+            for p in s._params:
+                p.grad = None
 
     def _grow_grad_ring(self) -> None:
         """After the first step, when its checkpoint slots and embedding rows
@@ -646,11 +687,27 @@ class SlideFSDP(nn.Module):
         for s in self.layer_states:
             s.wait_for_update()
 
-    def refresh_host_copies(self) -> None:
-        """With h2d_format='bf16': recompute every unit's bf16 host copy from
-        its fp32 master, after the masters were written outside the optimizer
-        (a loaded checkpoint).  A no-op with fp32 H2D."""
+    def release_device_units(self) -> None:
+        """Give back every unit still loaded on the device and point all
+        parameters at their fp32 masters.  After a forward without a backward
+        (evaluation), units with a buffer of their own, the last decoder and
+        the output unit stay loaded, with ``param.data`` their bf16 device
+        views; call this before writing the masters directly (e.g.
+        ``model.load_state_dict``), then ``refresh_host_copies``."""
         self.wait_for_updates()
+        if self.layer_states and self.layer_states[0].row_sparse:
+            self.layer_states[0].settle_orphaned_early()
+        for s in self.layer_states:
+            s.release_device_unit()
+
+    def refresh_host_copies(self) -> None:
+        """After the masters were written outside the optimizer (a loaded
+        checkpoint): drop the stagings made for the next forward, so every
+        unit is staged from its new master, and with h2d_format='bf16'
+        recompute every unit's bf16 host copy.  Masters may only be written
+        while no unit is loaded (``release_device_units``, which this calls
+        as well)."""
+        self.release_device_units()
         for s in self.layer_states:
             s.refresh_host_copy()
 
@@ -717,6 +774,8 @@ class SlideFSDP(nn.Module):
         gradient hooks from the model's parameters (which would otherwise keep
         this wrapper's host state alive)."""
         try:
+            if self.layer_states and self.layer_states[0].row_sparse:
+                self.layer_states[0].settle_orphaned_early()
             self.wait_for_updates()
         finally:
             for h in getattr(self, "_hook_handles", []):

@@ -405,6 +405,7 @@ class _StagerPieces:
         self.buf, self.slot_free = slot
         self.pushed = 0
         self.last_copy: Optional[torch.cuda.Event] = None
+        self.last_issued: Optional[torch.cuda.Event] = None   # the latest piece's copy
         self.open = True
 
     def push(self, j: int) -> None:
@@ -424,6 +425,7 @@ class _StagerPieces:
         if timing:
             st.copy_timing.append((t0, copied, (b - a) * 4))
         self.pushed += 1
+        self.last_issued = copied
         if self.pushed == len(self.pieces):
             self.last_copy = copied
             # the backlog counts units: queued until the unit's last copy is done
@@ -443,12 +445,13 @@ class _StagerPieces:
         return self.stager.cast_pending(p, self.dst, self.stager.cast_stream)
 
     def abort(self) -> None:
-        """Give the slot back without casting (the unit is staged whole later);
-        copies already issued finish into it ahead of its next user's copies
-        on the same stream."""
+        """Give the slot back without casting (the unit is staged whole later).
+        Its next writer waits for what this one waited for: the slot's last
+        reader when no piece was pushed, else the last piece's copy (issued
+        after that reader, on the same stream)."""
         if self.open:
             self.open = False
-            self.stager.slots.give(self.buf, None)
+            self.stager.slots.give(self.buf, self.slot_free if self.pushed == 0 else self.last_issued)
 
 
 class BF16Loader:

@@ -142,12 +142,17 @@ class PriorityUpdateExecutor:
             except BaseException as e:  # delivered to whoever waits on f
                 f.set_exception(e)
 
-    def shutdown(self, wait: bool = True) -> None:
+    def shutdown(self, wait: bool = True, timeout: Optional[float] = None) -> None:
+        """Stop taking tasks; the worker finishes the queued ones and exits.
+        With ``wait``, join it, for at most ``timeout`` seconds (then
+        ``TimeoutError``: a task is still running)."""
         with self._cv:
             self._stop = True
             self._cv.notify_all()
         if wait and self._thread is not threading.current_thread():
-            self._thread.join()
+            self._thread.join(timeout)
+            if self._thread.is_alive():
+                raise TimeoutError(f"{self._thread.name}: worker still running after {timeout:g} s")
 
 
 class _UpdateReady:

@@ -216,6 +216,43 @@ def test_evaluation_forwards_between_steps(dev, grad):
     assert len(seen) == 2
 
 
+@pytest.mark.parametrize("h2d_format", ["fp32", "bf16"])
+def test_masters_written_between_steps(dev, h2d_format):
+    """Masters written directly between training steps (``load_state_dict``
+    after a forward without labels, which leaves the units with own buffers,
+    the last decoder and the output unit loaded), between
+    ``release_device_units`` and ``refresh_host_copies``: the next forward
+    computes with the cast of the new masters, and every update that follows
+    is the oracle's on the new masters, bit for bit."""
+    def between(sf, k):
+        model = sf.base_model
+        with torch.no_grad():
+            sf(input_ids=batches(1)[0].to(dev))
+        assert sum(s.is_resident() for s in sf.layer_states) >= 2
+        sf.release_device_units()
+        assert not any(s.is_resident() for s in sf.layer_states)
+        g = torch.Generator().manual_seed(100 + k)
+        new = {n: p.detach() + 0.01 * torch.randn(p.shape, generator=g) for n, p in model.named_parameters()}
+        model.load_state_dict(new, strict=False)
+        sf.refresh_host_copies()
+        name_of = {id(p): n for n, p in model.named_parameters()}
+        arrays = {u: [new[name_of[id(p)]].numpy() for p in ps] for u, ps in enumerate(units_of(model))}
+        # the next forward stages the new masters
+        with torch.no_grad():
+            sf(input_ids=batches(1)[0].to(dev))
+        torch.cuda.synchronize()
+        staged = 0
+        for u, st in enumerate(sf.layer_states):
+            if st.is_resident():
+                exp = oracle.cast_f32_bf16(np.concatenate([a.reshape(-1) for a in arrays[u]]))
+                assert np.array_equal(u16(st._current_gpu_cache["param"][:st.total_size]), exp), (k, u)
+                staged += 1
+        assert staged >= 2
+        return arrays
+
+    check_updates_against_oracle(dev, "llama", h2d_format, {}, dict(resident_layers=L - 1), between=between)
+
+
 @pytest.mark.parametrize("early", [True, False])
 def test_embedding_early_rows(dev, early):
     """The embedding's update in two parts (default): the rows the batch does
@@ -256,6 +293,40 @@ def test_out_of_range_input_id_raises_at_the_update(dev):
         sf.close()
     except ValueError:
         pass
+
+
+def test_failed_backward_leaves_the_wrapper_usable(dev):
+    """A backward that raises part-way (a host-side hook on the first
+    decoder's weight raises; every kernel completes normally): the error
+    reaches the caller, the offloads and updates already queued finish, no
+    unit stays on the device (with the 2-unit pool, a unit left loaded would
+    block the next step's load), the embedding's early update part is closed,
+    and the next two steps train every unit."""
+    from test1_amd import SlideFSDP, SlideFSDPConfig
+
+    sf = SlideFSDP(make_model(), SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD), wait_timeout=120,
+                   resident_layers=0)
+    ids = batches(3)
+
+    def boom(grad):
+        raise RuntimeError("injected backward failure")
+
+    h = sf.layer_states[1].layer.self_attn.q_proj.weight.register_hook(boom)
+    with pytest.raises(RuntimeError, match="injected"):
+        sf(input_ids=ids[0].to(dev), labels=ids[0].to(dev))
+    h.remove()
+    assert not any(s.is_resident() for s in sf.layer_states)
+    assert sf.buffer_pool.available() == sf.buffer_pool.pool_size
+    assert sf.layer_states[0]._early is None and sf.layer_optimizer._early_rows == {}
+    before = [g["step"] for g in sf.layer_optimizer.param_groups]
+    assert before[2:] == [1] * L and before[1] == 0      # units above the failure were updated
+    for k in (1, 2):
+        loss = sf(input_ids=ids[k].to(dev), labels=ids[k].to(dev)).loss.item()
+        sf.wait_for_updates()
+        assert np.isfinite(loss)
+    after = [g["step"] for g in sf.layer_optimizer.param_groups]
+    assert [b - a for a, b in zip(before, after)] == [2] * (L + 2)
+    sf.close()
 
 
 def test_cast_at_use_loss_parity(dev):
@@ -355,7 +426,10 @@ def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, 
         steps_ids = [batches(1, B, S, vocab=vocab)[0] for B, S in shapes]
     for k, ids in enumerate(steps_ids):
         if between is not None and k > 0:
-            between(sf, k)
+            # a hook that writes the masters returns their new values per unit
+            for u, arrs in (between(sf, k) or {}).items():
+                for a, b in zip(ref_units[u], arrs):
+                    a[...] = b
         sf.runtime.capture = {}
         ids = ids.to(dev)
         sf(input_ids=ids, labels=ids)

@@ -91,6 +91,21 @@ int sf_cast_f32_bf16_timed(const float* src, uint16_t* dst, size_t n,
                            sf_stream_t stream, sf_event_t start,
                            sf_event_t stop);
 
+/* Stage n fp32 values from pinned host memory into a bf16 device array:
+ * dst[i] = rne(host_src[i]) (the rounding of sf_cast_f32_bf16).  The values
+ * travel in pieces of workspace_elems (rounded down to a multiple of 8)
+ * through the caller's device fp32 `workspace`: each piece is copied into
+ * it by DMA and cast from it into dst, all in order on `stream`, so the
+ * workspace may be reused once the stream has passed the call.  host_src
+ * must be pinned host memory (SF_EINVAL otherwise: an asynchronous copy
+ * needs it), dst and workspace device memory.  Replaces the reference's
+ * staging of one unit, layer_state.py:299-314 (host cast of the flat master
+ * into the pinned convert buffer, then a non_blocking bf16 copy on the H2D
+ * stream), with the cast moved to the device. */
+int sf_stage_f32_bf16(const float* host_src, uint16_t* dst, size_t n,
+                      float* workspace, size_t workspace_elems,
+                      sf_stream_t stream);
+
 /* Timing events for sf_cast_f32_bf16_timed: create, destroy, and the
  * milliseconds between two completed events (a HIP status, e.g. not ready,
  * while either is pending).  No counterpart in the reference. */

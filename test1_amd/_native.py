@@ -32,6 +32,8 @@ SF_MAX_SEGS = 64
 SF_IO_READ = 0
 SF_IO_WRITE = 1
 SF_IO_ALIGN = 4096
+SF_EINVAL = 9001
+SF_ETOOMANY = 9002
 SF_EALIGN = 9007
 # row_slot markers of the row-wise AdamW: a zero-gradient row, a row left as it is
 SF_ROW_ZERO = -1
@@ -76,6 +78,7 @@ HIP_SIGNATURES = {
     "sf_fill_b16": [_vp, _sz, ctypes.c_uint16, _vp],
     "sf_gather_rows_f32_bf16": [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _i, _vp],
     "sf_gather_rows_b16": [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _i, _vp],
+    "sf_stage_f32_bf16": [_vp, _vp, _sz, _vp, _sz, _vp],
     "sf_memcpy_async": [_vp, _vp, _sz, _i, _vp],
     "sf_host_alloc": [ctypes.POINTER(_vp), _sz],
     "sf_host_free": [_vp],

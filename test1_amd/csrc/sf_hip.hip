@@ -518,6 +518,58 @@ int sf_fill_b16(uint16_t* dst, size_t n, uint16_t value, sf_stream_t stream) {
     return e == hipSuccess ? SF_OK : int(e);
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------------
+// Staging: pinned fp32 host array -> bf16 device array, through a device
+// fp32 buffer, all on one stream.  Each piece is copied into the buffer by
+// DMA and cast from it by cast_flat_kernel; the next piece's copy into the
+// same buffer follows that cast in stream order.  With one stream the copy
+// and the cast do not overlap; the cast moves 1.5x the copy's bytes over
+// HBM at ~100x the host link's rate, so it adds ~1-2 % to the copy.
+// ---------------------------------------------------------------------
+namespace {
+
+// The memory type the runtime records for ptr, or -1 for memory it does
+// not know (pageable host memory).
+int memory_type(const void* p) {
+    hipPointerAttribute_t a;
+    const hipError_t e = hipPointerGetAttributes(&a, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return -1;
+    }
+    return int(a.type);
+}
+
+int stage_launch(const float* host, uint16_t* dst, size_t n, float* buf, size_t chunk, hipStream_t st) {
+    if (n == 0) return SF_OK;
+    if (host == nullptr || dst == nullptr || buf == nullptr) return SF_EINVAL;
+    // an asynchronous copy needs pinned host memory; the cast writes device memory
+    if (memory_type(host) != int(hipMemoryTypeHost) || memory_type(dst) != int(hipMemoryTypeDevice))
+        return SF_EINVAL;
+    chunk -= chunk % kGroup;  // every piece starts 16-byte aligned in dst if dst does
+    if (chunk == 0) return SF_EINVAL;
+    for (size_t off = 0; off < n; off += chunk) {
+        const size_t c = n - off < chunk ? n - off : chunk;
+        const hipError_t e = hipMemcpyAsync(buf, host + off, c * sizeof(float), hipMemcpyHostToDevice, st);
+        if (e != hipSuccess) return hip_status(e);
+        const int rc = cast_launch(buf, dst + off, c, st, nullptr, nullptr);
+        if (rc != SF_OK) return rc;
+    }
+    return SF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sf_stage_f32_bf16(const float* host_src, uint16_t* dst, size_t n, float* workspace, size_t workspace_elems,
+                      sf_stream_t stream) {
+    if (n > 0 && (workspace == nullptr || memory_type(workspace) != int(hipMemoryTypeDevice))) return SF_EINVAL;
+    return stage_launch(host_src, dst, n, workspace, workspace_elems, reinterpret_cast<hipStream_t>(stream));
+}
+
 int sf_memcpy_async(void* dst, const void* src, size_t bytes, int kind, sf_stream_t stream) {
     if (bytes == 0) return SF_OK;
     if (dst == nullptr || src == nullptr) return SF_EINVAL;

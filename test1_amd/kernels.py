@@ -93,6 +93,36 @@ def cast_f32_bf16_(dst: torch.Tensor, src: torch.Tensor, stream: Optional[torch.
     return dst
 
 
+def _check_stage_args(dst: torch.Tensor, host_src: torch.Tensor) -> None:
+    if host_src.dtype != torch.float32 or dst.dtype != torch.bfloat16:
+        raise TypeError(f"stage_f32_bf16_: need float32 -> bfloat16, got {host_src.dtype} -> {dst.dtype}")
+    if host_src.device.type != "cpu" or (host_src.numel() and not host_src.is_pinned()):
+        raise ValueError("stage_f32_bf16_: the source must be a pinned host tensor")
+    _require_cuda(dst, "dst")
+    _require_contig(host_src, "host_src")
+    _require_contig(dst, "dst")
+    if host_src.numel() != dst.numel():
+        raise ValueError(f"stage_f32_bf16_: numel mismatch {host_src.numel()} vs {dst.numel()}")
+
+
+def stage_f32_bf16_(dst: torch.Tensor, host_src: torch.Tensor, workspace: torch.Tensor,
+                    stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """dst[:] = RNE-bf16(host_src) for a pinned fp32 host tensor and a bf16 GPU
+    tensor: copied piece by piece through the fp32 GPU tensor ``workspace``
+    (pieces of its size rounded down to 8 elements) and cast from there, all
+    in order on ``stream``; ``workspace`` is free again once the stream has
+    passed the call."""
+    _check_stage_args(dst, host_src)
+    if workspace.dtype != torch.float32 or workspace.numel() < 8:
+        raise ValueError("stage_f32_bf16_: the workspace must be a float32 GPU tensor of at least 8 elements")
+    _require_cuda(workspace, "workspace")
+    _require_contig(workspace, "workspace")
+    _native.check(_native.hip().sf_stage_f32_bf16(host_src.data_ptr(), dst.data_ptr(), host_src.numel(),
+                                                  workspace.data_ptr(), workspace.numel(), _stream_ptr(stream)),
+                  "sf_stage_f32_bf16")
+    return dst
+
+
 def _seg_array(segs: Sequence[Tuple[int, int, int]]):
     arr = (_native.SfSeg * max(1, len(segs)))()
     for i, (s, d, n) in enumerate(segs):

@@ -53,6 +53,8 @@ def test_device_entry_points_reject_bad_arguments_without_a_gpu():
     assert hip.sf_cast_f32_bf16(None, None, 10, None) == 9001
     assert hip.sf_cast_f32_bf16(None, None, 0, None) == 0
     assert hip.sf_memcpy_async(None, None, 16, 1, None) == 9001
+    assert hip.sf_stage_f32_bf16(None, None, 10, None, 8, None) == 9001
+    assert hip.sf_stage_f32_bf16(None, None, 0, None, 0, None) == 0
     assert hip.sf_copy_segs_b16(None, -1, 0, None) == 9001
     buf = (ctypes.c_uint16 * 64)()
     # overlapping cast source and destination

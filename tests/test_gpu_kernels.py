@@ -109,6 +109,40 @@ def test_cast_full_llama_layer(dev):
     assert np.array_equal(bits16(out), oracle.cast_f32_bf16(x.numpy()))
 
 
+@pytest.mark.parametrize("n,ws", [(0, 8), (1, 8), (13, 8), (100_003, 4099), ((1 << 22) + 5, 1 << 20),
+                                  (1 << 20, 1 << 22)])
+def test_stage_pinned_master_through_workspace(dev, n, ws):
+    """Pinned fp32 host array -> bf16 device array through a device workspace
+    (pieces of the workspace's size rounded down to 8: several pieces, a
+    ragged last one, a workspace larger than the array), bit-exact against
+    the oracle; the stream's order makes one workspace enough, and the array
+    ends where it should (the element after it untouched)."""
+    x = pinned_empty(n, torch.float32)
+    x.copy_(rand_f32(n, n + 1))
+    if n:
+        x[0] = float("nan")
+    out = torch.full((n + 1,), 7.0, dtype=torch.bfloat16, device=dev)
+    work = torch.empty(ws, dtype=torch.float32, device=dev)
+    kernels.stage_f32_bf16_(out[:n], x, work)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(out[:n]), oracle.cast_f32_bf16(x.numpy()))
+    assert bits16(out[n:])[0] == bits16(torch.tensor([7.0], dtype=torch.bfloat16))[0]
+
+
+def test_stage_refuses_pageable_host_memory(dev):
+    """A pageable source cannot be copied asynchronously: the library says so
+    before it enqueues anything (checked in C, below the Python wrapper)."""
+    from test1_amd import _native
+
+    x = torch.randn(1000)                      # pageable
+    out = torch.empty(1000, dtype=torch.bfloat16, device=dev)
+    work = torch.empty(256, dtype=torch.float32, device=dev)
+    with pytest.raises(ValueError, match="pinned"):
+        kernels.stage_f32_bf16_(out, x, work)
+    rc = _native.hip().sf_stage_f32_bf16(x.data_ptr(), out.data_ptr(), 1000, work.data_ptr(), 256, None)
+    assert rc == _native.SF_EINVAL
+
+
 def test_cast_scatter_segments(dev):
     # 70 segments (> one launch's 64), ragged sizes, some misaligned, one empty
     rng = np.random.default_rng(1)

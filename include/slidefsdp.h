@@ -42,6 +42,7 @@ typedef void* sf_event_t;
 #define SF_EOVERLAP 9005    /* source and destination ranges overlap */
 #define SF_ENOREQ 9006      /* unknown or already released I/O ticket */
 #define SF_EALIGN 9007      /* O_DIRECT transfer not aligned to SF_IO_ALIGN */
+#define SF_ETOOBIG 9008     /* larger than the library's device scratch */
 #define SF_EDMA_BASE 10000  /* + (hsa_status_t & 0xFFF): a ROCr DMA call failed */
 #define SF_EIO_BASE 20000   /* + errno: a file operation failed */
 
@@ -105,6 +106,25 @@ int sf_cast_f32_bf16_timed(const float* src, uint16_t* dst, size_t n,
 int sf_stage_f32_bf16(const float* host_src, uint16_t* dst, size_t n,
                       float* workspace, size_t workspace_elems,
                       sf_stream_t stream);
+
+/* Elements (fp32) of the device scratch buffer of
+ * sf_stage_f32_bf16_noalloc: 64 MiB on every device the library runs on,
+ * held until the process ends. */
+#define SF_STAGE_SCRATCH_ELEMS ((size_t)16 << 20)
+
+/* sf_stage_f32_bf16 that allocates nothing: the pieces (chunk_elems fp32
+ * elements; 0 selects SF_STAGE_SCRATCH_ELEMS, more is refused with
+ * SF_ETOOBIG before anything is enqueued) go through a device buffer of the
+ * library's own, one static array per device, whose address is looked up on
+ * the first call on each device.  `stream` must belong to the current
+ * device.  No hipMalloc, hipFree or other allocating call is made.  Every
+ * call on a device uses that device's one buffer: calls on one stream (or
+ * otherwise ordered) are safe; calls that overlap on one device race.  No
+ * counterpart in the reference (its staging allocates nothing on the device
+ * but runs on the host, layer_state.py:299-314); for callers that cannot
+ * allocate device memory: code under HIP graph capture, serving loops. */
+int sf_stage_f32_bf16_noalloc(const float* host_src, uint16_t* dst, size_t n,
+                              size_t chunk_elems, sf_stream_t stream);
 
 /* Timing events for sf_cast_f32_bf16_timed: create, destroy, and the
  * milliseconds between two completed events (a HIP status, e.g. not ready,

@@ -35,6 +35,8 @@ SF_IO_ALIGN = 4096
 SF_EINVAL = 9001
 SF_ETOOMANY = 9002
 SF_EALIGN = 9007
+SF_ETOOBIG = 9008
+SF_STAGE_SCRATCH_ELEMS = 16 << 20
 # row_slot markers of the row-wise AdamW: a zero-gradient row, a row left as it is
 SF_ROW_ZERO = -1
 SF_ROW_SKIP = -2
@@ -79,6 +81,7 @@ HIP_SIGNATURES = {
     "sf_gather_rows_f32_bf16": [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _i, _vp],
     "sf_gather_rows_b16": [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _i, _vp],
     "sf_stage_f32_bf16": [_vp, _vp, _sz, _vp, _sz, _vp],
+    "sf_stage_f32_bf16_noalloc": [_vp, _vp, _sz, _sz, _vp],
     "sf_memcpy_async": [_vp, _vp, _sz, _i, _vp],
     "sf_host_alloc": [ctypes.POINTER(_vp), _sz],
     "sf_host_free": [_vp],

@@ -345,6 +345,7 @@ const char* sf_error_string(int status) {
         case SF_EDTYPE: return "sf: dtype combination not supported";
         case SF_ENOOPT: return "sf: unknown optimizer id";
         case SF_EOVERLAP: return "sf: source and destination overlap";
+        case SF_ETOOBIG: return "sf: piece larger than the library's device scratch (SF_STAGE_SCRATCH_ELEMS)";
         default:
             if (status >= SF_EDMA_BASE && status < SF_EDMA_BASE + 0x1000) return "sf: ROCr DMA call failed";
             return hipGetErrorString(hipError_t(status));
@@ -568,6 +569,66 @@ int sf_stage_f32_bf16(const float* host_src, uint16_t* dst, size_t n, float* wor
                       sf_stream_t stream) {
     if (n > 0 && (workspace == nullptr || memory_type(workspace) != int(hipMemoryTypeDevice))) return SF_EINVAL;
     return stage_launch(host_src, dst, n, workspace, workspace_elems, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------
+// Staging without allocating: the pieces go through the library's own
+// device buffer instead of a caller workspace.  `scratch` is a static
+// device array, so every device the library's code object is loaded on
+// holds one for the life of the process.  In host code its name is not a
+// device address: the address comes from hipGetSymbolAddress, looked up
+// once per device with that device current, and only that address is
+// passed to the copies and the cast.
+// ---------------------------------------------------------------------
+namespace {
+
+__device__ __align__(256) float scratch[SF_STAGE_SCRATCH_ELEMS];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, which must be the
+// device of `st` (the null stream: the current device).
+int scratch_for_stream(hipStream_t st, float** out) {
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_status(e);
+    if (st != nullptr) {
+        hipDevice_t sd = 0;
+        e = hipStreamGetDevice(st, &sd);
+        if (e != hipSuccess) return hip_status(e);
+        if (int(sd) != cur) return SF_EINVAL;
+    }
+    if (cur < 0 || cur >= kMaxDevices) return SF_EINVAL;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[cur] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e);
+        if (p == nullptr) return SF_EINVAL;
+        g_scratch_ptr[cur] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[cur];
+    return SF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sf_stage_f32_bf16_noalloc(const float* host_src, uint16_t* dst, size_t n, size_t chunk_elems,
+                              sf_stream_t stream) {
+    if (chunk_elems > SF_STAGE_SCRATCH_ELEMS) return SF_ETOOBIG;
+    if (n == 0) return SF_OK;
+    if (host_src == nullptr || dst == nullptr) return SF_EINVAL;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    float* buf = nullptr;
+    const int rc = scratch_for_stream(st, &buf);
+    if (rc != SF_OK) return rc;
+    return stage_launch(host_src, dst, n, buf, chunk_elems == 0 ? SF_STAGE_SCRATCH_ELEMS : chunk_elems, st);
 }
 
 int sf_memcpy_async(void* dst, const void* src, size_t bytes, int kind, sf_stream_t stream) {

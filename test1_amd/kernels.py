@@ -123,6 +123,19 @@ def stage_f32_bf16_(dst: torch.Tensor, host_src: torch.Tensor, workspace: torch.
     return dst
 
 
+def stage_f32_bf16_noalloc_(dst: torch.Tensor, host_src: torch.Tensor, chunk_elems: int = 0,
+                            stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """``stage_f32_bf16_`` through the library's own device scratch buffer
+    (pieces of ``chunk_elems``, at most ``_native.SF_STAGE_SCRATCH_ELEMS``;
+    0: that size), allocating nothing.  Calls on one device share the
+    buffer: keep them on one stream or otherwise ordered."""
+    _check_stage_args(dst, host_src)
+    _native.check(_native.hip().sf_stage_f32_bf16_noalloc(host_src.data_ptr(), dst.data_ptr(), host_src.numel(),
+                                                          int(chunk_elems), _stream_ptr(stream)),
+                  "sf_stage_f32_bf16_noalloc")
+    return dst
+
+
 def _seg_array(segs: Sequence[Tuple[int, int, int]]):
     arr = (_native.SfSeg * max(1, len(segs)))()
     for i, (s, d, n) in enumerate(segs):

@@ -14,16 +14,21 @@ Llama for a quick check).
 
 One JSON line is printed with the metric (tokens/s), the roofline of the
 staging cast kernel (HBM-bound, measured with HIP events on its stream over
-the timed region), host-link rates of the H2D/D2H copies, and the reference's
-host-side staging + LayerAdam path timed on this machine's cores
-(``cpu_baseline``).  ``variants`` holds a second timed run on the same model
-with the other parameter H2D format (fp32 masters + GPU cast, or the host
-optimizer's bf16 copy), on fresh batches.
+the timed region), the host-link-bound kernels beside it (checkpoint pack,
+embedding row gathers), the host link per direction (rate over the union of
+all transfers' intervals, the fraction of that time under layer compute, and
+plain pinned copies for the rate this box reaches), and the reference's
+host-side staging + AdamW path restated with this build's code and timed on
+this machine's cores (``cpu_baseline``).  ``variants`` holds shorter timed
+runs on the same model: ``pool``, the reference's schedule (every unit in the
+2-unit pool and reloaded for its backward), and the other parameter H2D
+format (fp32 masters + GPU cast, or the host optimizer's bf16 copy).
 """
 
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import os
 import sys
@@ -134,88 +139,93 @@ def elapsed_stats(records):
     return ms, amt
 
 
-def cpu_baseline(layer_numel: int, total_params: int, tokens: int, resident_params: int, iters: int = 150,
-                 warmup: int = 5):
-    """The reference's host-side work, timed on this host: per unit the fp32 ->
-    bf16 cast of the master (reference layer_state.py:301, torch CPU copy),
-    twice per step (forward and backward load), the ``grad.float()`` unpack
-    (layer_adam.py:404) and the CPU Adam (the reference's own cpu_adam when
-    oracle/_ref is built, else the oracle's scalar port), on a sample of one
-    Llama-3-8B decoder layer, scaled to the model's parameter count."""
+# One Llama-3-8B decoder layer's parameters in named_parameters() order.
+LLAMA3_8B_LAYER_SHAPES = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096), (14336, 4096),
+                          (4096, 14336), (4096,), (4096,)]
+
+
+def cpu_baseline(total_params: int, tokens: int, resident_params: int, min_seconds: float = 10.0,
+                 warmup: int = 3):
+    """The reference's host-side work per unit, timed on this host's cores on
+    a sample of one Llama-3-8B decoder layer (218,112,000 parameters, seed
+    42), restated with this build's own code: the fp32 -> bf16 cast of the
+    flat master (torch CPU ``copy_``, the call of reference layer_state.py:301)
+    for each load, ``grad.float()`` per parameter (layer_adam.py:404) and the
+    AdamW per parameter through the reference's ``cpu_adam.adam_update``
+    interface (layer_adam.py:405-425; this build's AVX-512 implementation,
+    bit-exact with the reference's).  Scaled to the model: the per-parameter
+    cost times its parameters, the cast counted twice per step (forward and
+    backward loads) except for the units that stay loaded.  Timed iterations
+    run until ``min_seconds`` of CPU work (at least 5)."""
     import torch
 
-    n = layer_numel
-    threads = torch.get_num_threads()
-    ref = None
-    kind = "port"
-    path = os.path.join(ROOT, "oracle", "_ref", "cpu_adam_ref.so")
-    if os.path.exists(path):
-        import importlib.util
+    from test1_amd.optimizer import cpu_adam
 
-        spec = importlib.util.spec_from_file_location("cpu_adam_ref", path)
-        ref = importlib.util.module_from_spec(spec)
-        spec.loader.exec_module(ref)
-        kind = "reference"
+    threads = torch.get_num_threads()
     g = torch.Generator().manual_seed(42)
+    sizes = [int(torch.Size(s).numel()) for s in LLAMA3_8B_LAYER_SHAPES]
+    n = sum(sizes)
     master = torch.randn(n, generator=g) * 0.02
     bf = torch.empty(n, dtype=torch.bfloat16)
     grad = (torch.randn(n, generator=g) * 1e-3).bfloat16()
     m = torch.zeros(n)
     v = torch.zeros(n)
-    if ref is not None:
-        ref.create_adam(77, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, False)
-
-        def adam(step, gf):
-            ref.adam_update(77, step, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, master, gf, m, v)
-    else:
-        import numpy as np
-
-        import oracle
-        opt = oracle.OracleAdam(1e-5, (0.9, 0.999), 1e-8, 0.01, True)
-        n = min(n, 8_000_000)  # the scalar port is single-threaded: sample fewer elements
-        master, grad, m, v, bf = master[:n], grad[:n], m[:n], v[:n], bf[:n]
-
-        def adam(step, gf):
-            opt.update(step, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, master.numpy(), gf.numpy(), m.numpy(), v.numpy())
-        threads = 1
+    offs = [sum(sizes[:i]) for i in range(len(sizes))]
+    views = [(master[o:o + k], grad[o:o + k], m[o:o + k], v[o:o + k]) for o, k in zip(offs, sizes)]
+    opt_id = 77
+    cpu_adam.create_adam(opt_id, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, False)
     t_cast = t_unpack = t_adam = 0.0
     t_all = time.perf_counter()
-    for it in range(iters + warmup):
-        t0 = time.perf_counter()
-        bf.copy_(master)
-        t1 = time.perf_counter()
-        gf = grad.float()
-        t2 = time.perf_counter()
-        adam(it + 1, gf)
-        t3 = time.perf_counter()
-        if it >= warmup:
-            t_cast += t1 - t0
-            t_unpack += t2 - t1
-            t_adam += t3 - t2
+    iters = 0
+    t_timed = None
+    try:
+        for it in itertools.count():
+            if it == warmup:
+                t_timed = time.perf_counter()
+            if t_timed is not None and iters >= 5 and time.perf_counter() - t_timed >= min_seconds:
+                break
+            t0 = time.perf_counter()
+            bf.copy_(master)
+            t1 = time.perf_counter()
+            dt_unpack = dt_adam = 0.0
+            for p, gb, mm, vv in views:
+                a = time.perf_counter()
+                gf = gb.float()
+                b = time.perf_counter()
+                cpu_adam.adam_update(opt_id, it + 1, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, p, gf, mm, vv)
+                dt_unpack += b - a
+                dt_adam += time.perf_counter() - b
+            if it >= warmup:
+                t_cast += t1 - t0
+                t_unpack += dt_unpack
+                t_adam += dt_adam
+                iters += 1
+    finally:
+        cpu_adam.destroy_adam(opt_id)
     t_all = time.perf_counter() - t_all
     t_cast, t_unpack, t_adam = (x / iters for x in (t_cast, t_unpack, t_adam))
     per_param = (t_cast * 2 + t_unpack + t_adam) / n
     # units that stay resident are cast once per step, not twice
     step_s = per_param * total_params - t_cast / n * resident_params
-    if ref is not None:
-        ref.destroy_adam(77)
     return {
         "value": tokens / step_s,
         "unit": "tokens/s",
         "cores": threads,
-        "kind": kind,
-        "sample": (f"one Llama-3-8B decoder layer sample ({n:,} params), {warmup} warmup + {iters} timed "
-                   f"iterations ({t_all:.1f} s of CPU work): torch CPU fp32->bf16 cast "
-                   f"{t_cast * 1e3:.1f} ms, grad.float() {t_unpack * 1e3:.1f} ms, CPU Adam {t_adam * 1e3:.1f} ms "
-                   f"({28 * n / t_adam / 1e9:.1f} GB/s at 28 B/param); per-step time = per-param cost x "
-                   f"{total_params:,} params (cast twice, resident units once)"),
+        "kind": "port",
+        "sample": (f"one Llama-3-8B decoder layer ({n:,} params in its 9 parameters), {warmup} warmup + "
+                   f"{iters} timed iterations ({t_all:.1f} s of CPU work) on {threads} threads: torch CPU "
+                   f"fp32->bf16 cast {t_cast * 1e3:.1f} ms, grad.float() per parameter {t_unpack * 1e3:.1f} ms, "
+                   f"AdamW per parameter (this build's AVX-512 cpu_adam, reference call pattern) "
+                   f"{t_adam * 1e3:.1f} ms ({28 * n / t_adam / 1e9:.1f} GB/s at 28 B/param); per-step time = "
+                   f"per-parameter cost x {total_params:,} params (cast twice, resident units once)"),
         "ms_per_layer": {"cast": t_cast * 1e3, "unpack": t_unpack * 1e3, "adam": t_adam * 1e3},
         "adam_gbs": 28 * n / t_adam / 1e9,
     }
 
 
 def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_engine: str,
-              timeline: str = "", batch_seed: int = 0) -> dict:
+              timeline: str = "", batch_seed: int = 0, steps: Optional[int] = None,
+              warmup: Optional[int] = None) -> dict:
     """Wrap ``model`` in SlideFSDP, run the warmup steps, then time
     ``args.steps`` steps between two device synchronisations.  Returns the
     timings and the per-kernel / per-copy event records; closes the wrapper.
@@ -234,36 +244,48 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
                           optimizer_nvme_offload_fraction=args.opt_nvme_fraction,
                           optimizer_offload_dir=os.path.join(args.offload_dir, "optimizer"),
                           enable_activation_checkpoint=not args.no_activation_checkpoint)
+    kw = {}
+    if args.wait_timeout is not None:
+        kw["wait_timeout"] = args.wait_timeout if args.wait_timeout > 0 else None
     sf = SlideFSDP(model, cfg, d2h_engine=d2h_engine, h2d_format=h2d_format, resident_layers=resident_layers,
                    fused_cross_entropy=args.fused_ce, update_piece_elems=args.piece_elems,
-                   cast_at_use=not args.cast_on_copy, early_embedding_update=not args.no_early_embedding)
+                   cast_at_use=not args.cast_on_copy, early_embedding_update=not args.no_early_embedding, **kw)
     uses_storage = args.ac_offload == "nvme" or args.opt_nvme_fraction > 0
     log(f"[bench] SlideFSDP ({h2d_format} H2D, {sf.resident_layers} resident decoders, {d2h_engine} D2H) "
         f"ready in {time.time() - t0:.1f}s")
     B, S = w["batch"], w["seq"]
+    n_steps = args.steps if steps is None else steps
+    n_warm = args.warmup if warmup is None else warmup
     g = torch.Generator().manual_seed(batch_seed)
-    batches = [torch.randint(0, w["vocab"], (B, S), generator=g).to(dev) for _ in range(args.warmup + args.steps)]
+    batches = [torch.randint(0, w["vocab"], (B, S), generator=g).to(dev) for _ in range(n_warm + n_steps)]
 
-    for i in range(args.warmup):
+    for i in range(n_warm):
         t = time.time()
         out = sf(input_ids=batches[i], labels=batches[i])
         sf.wait_for_updates()
         torch.cuda.synchronize()
         log(f"[bench] warmup {i}: loss {out.loss.item():.4f} {time.time() - t:.2f}s")
 
+    from test1_amd import kernels as _k
+
     rt = sf.runtime
     rt.stager.cast_timing, rt.stager.copy_timing, rt.d2h_timing = [], [], []
+    rt.enable_link_timing(not args.no_link_timing)
     if rt.d2h_engine == "sdma":
-        from test1_amd import kernels as _k
         _k.dma_enable_timing(True)
     if timeline:
         rt.timeline = []
     io0 = _storage_snapshot(sf) if uses_storage else None
+    # one clock for HIP events and SDMA copy times: an anchor event, and the
+    # SDMA clock read right after the anchor has completed
+    anchor = torch.cuda.Event(enable_timing=True)
+    anchor.record()
     torch.cuda.synchronize()
+    anchor_ns = _k.dma_clock_ns() if rt.d2h_engine == "sdma" else 0
     t_start = time.perf_counter()
     losses = []
-    for i in range(args.steps):
-        out = sf(input_ids=batches[args.warmup + i], labels=batches[args.warmup + i])
+    for i in range(n_steps):
+        out = sf(input_ids=batches[n_warm + i], labels=batches[n_warm + i])
         losses.append(out.loss)
         log(f"[bench] step {i} issued")
     sf.wait_for_updates()
@@ -274,20 +296,21 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
         with open(timeline, "w") as f:
             for t, th, what, unit in rt.timeline:
                 f.write(f"{(t - t_start) * 1e3:.3f} {th} {what} {unit}\n")
-    log(f"[bench] timed {args.steps} steps in {elapsed:.2f}s, losses {losses}")
+    log(f"[bench] timed {n_steps} steps in {elapsed:.2f}s, losses {losses}")
     storage_stats = None
     if uses_storage:
         io1 = _storage_snapshot(sf)
         storage_stats = {k: io1[k] - io0[k] for k in io1}
         rd, wr, busy = storage_stats["bytes_read"], storage_stats["bytes_written"], storage_stats["busy_s"]
         storage_stats.update({
-            "read_bytes_per_step": rd / args.steps, "write_bytes_per_step": wr / args.steps,
+            "read_bytes_per_step": rd / n_steps, "write_bytes_per_step": wr / n_steps,
             "busy_frac": busy / elapsed, "gbs_while_busy": (rd + wr) / busy / 1e9 if busy > 0 else None})
         log(f"[bench] storage: {storage_stats}")
     r = {
-        "elapsed": elapsed, "losses": losses, "tokens": B * S * args.steps,
+        "elapsed": elapsed, "losses": losses, "tokens": B * S * n_steps, "steps": n_steps, "warmup": n_warm,
         "cast": elapsed_stats(rt.stager.cast_timing), "ncast": len(rt.stager.cast_timing or []),
         "h2d": elapsed_stats(rt.stager.copy_timing), "d2h": elapsed_stats(rt.d2h_timing),
+        "link": link_timeline(rt, anchor, anchor_ns),
         "total_params": sf.total_params, "resident_layers": sf.resident_layers,
         "stage_after_update": sf.runtime.stage_after_update,
         "cast_at_use": sf.runtime.cast_at_use,
@@ -297,6 +320,12 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
         "storage": storage_stats,
     }
     sf.close()
+    # The parameters point at the wrapper's pinned masters; give them pageable
+    # copies, so the pinned memory goes with the wrapper (a next wrapper on
+    # this model pins its own, and the driver caps pinned memory per process).
+    with torch.no_grad():
+        for p in model.parameters():
+            p.data = p.data.clone()
     del sf, out, rt
     gc.collect()
     torch.cuda.empty_cache()
@@ -345,6 +374,16 @@ def _storage_snapshot(sf) -> dict:
             "checkpoint_slot_wait_s": 0.0 if spill is None else spill.slot_wait_s}
 
 
+def variant_summary(v: dict, h2d_format: str, d2h_engine: str) -> dict:
+    cast_ms, cast_elems = v["cast"]
+    cast_gbs = 6 * cast_elems / (cast_ms * 1e-3) / 1e9 if cast_ms > 0 else None
+    return {"value": v["tokens"] / v["elapsed"], "ms_per_step": v["elapsed"] / v["steps"] * 1e3,
+            "steps": v["steps"], "warmup": v["warmup"], "h2d_format": h2d_format,
+            "resident_layers": v["resident_layers"], "d2h_engine": d2h_engine,
+            "cast_frac": None if cast_gbs is None else cast_gbs / HBM_PEAK_GBS,
+            "host_link": link_stats(v, v["steps"]), "losses": v["losses"]}
+
+
 def megatron_flops_per_step(w: dict) -> float:
     """Model FLOPs of one training step by the Megatron-LM estimate with GQA
     and SwiGLU that the reference reports (utils/metric.py:4-53): 3 passes x
@@ -384,24 +423,153 @@ def host_mem_available() -> int:
     return 0
 
 
-def link_stats(r: dict, steps: int) -> dict:
-    (h2d_ms, h2d_bytes), (d2h_ms, d2h_bytes) = r["h2d"], r["d2h"]
-    h2d = h2d_bytes / (h2d_ms * 1e-3) / 1e9 if h2d_ms > 0 else None
-    d2h = d2h_bytes / (d2h_ms * 1e-3) / 1e9 if d2h_ms > 0 else None
+def link_timeline(rt, anchor, anchor_ns: int) -> dict:
+    """Every host-link transfer and every unit's compute of the timed steps as
+    (start_ns, end_ns[, bytes]) on one clock: HIP events placed by their time
+    since ``anchor`` (recorded and completed at ``anchor_ns`` of the SDMA
+    clock), SDMA gradient copies by their engine timestamps.
+    h2d: parameter copies, checkpoint prefetches, embedding lookup rows read
+    from the host table; d2h: gradient copies, checkpoint packs, embedding
+    gradient rows."""
+    def ns(ev):
+        return anchor_ns + anchor.elapsed_time(ev) * 1e6
+
+    def spans(records):
+        out = []
+        for rec in records or []:
+            if len(rec) == 4:                      # ("interval_ns", start, end, bytes)
+                out.append((rec[1], rec[2], rec[3]))
+            else:                                  # (start event, end event, bytes)
+                out.append((ns(rec[0]), ns(rec[1]), rec[2]))
+        return out
+
+    lt = rt.link_timing or {}
     return {
-        "h2d_gbs": h2d, "d2h_gbs": d2h,
-        "h2d_frac": None if h2d is None else h2d / LINK_PEAK_GBS,
-        "d2h_frac": None if d2h is None else d2h / LINK_PEAK_GBS,
-        "peak_gbs": LINK_PEAK_GBS,
-        "h2d_bytes_per_step": h2d_bytes / steps,
-        "d2h_bytes_per_step": d2h_bytes / steps,
-        "h2d_busy_frac": (h2d_ms * 1e-3) / r["elapsed"],
-        "note": "h2d: the parameter copies' bytes over the sum of HIP-event durations around each copy on "
-                "its stream, which also count the copy's wait for a copy engine and the events' own latency "
-                "(profiles/host_link__llama3_8b_train_step.md: 52-53 GB/s over the union of the copy "
-                "engines' busy intervals); d2h: the SDMA gradient copies over the union of their engine "
-                "timestamps",
+        "h2d": {"params": spans(rt.stager.copy_timing), "checkpoints": spans(lt.get("act_h2d")),
+                "rows": spans(lt.get("rows_h2d"))},
+        "d2h": {"grads": spans(rt.d2h_timing), "checkpoints": spans(lt.get("act_d2h")),
+                "rows": spans(lt.get("rows_d2h"))},
+        "compute": [(ns(a), ns(b)) for a, b in lt.get("compute", [])],
+        "common_clock": anchor_ns != 0,
     }
+
+
+def _union(spans):
+    """Sorted disjoint (start, end) covering the given spans."""
+    out = []
+    for s, e in sorted((sp[0], sp[1]) for sp in spans):
+        if out and s <= out[-1][1]:
+            out[-1][1] = max(out[-1][1], e)
+        else:
+            out.append([s, e])
+    return out
+
+
+def _length(u):
+    return sum(e - s for s, e in u)
+
+
+def _overlap(a, b):
+    """Length of the intersection of two sorted disjoint interval lists."""
+    i = j = 0
+    tot = 0.0
+    while i < len(a) and j < len(b):
+        lo, hi = max(a[i][0], b[j][0]), min(a[i][1], b[j][1])
+        if hi > lo:
+            tot += hi - lo
+        if a[i][1] < b[j][1]:
+            i += 1
+        else:
+            j += 1
+    return tot
+
+
+def link_stats(r: dict, steps: int, alone: Optional[dict] = None) -> dict:
+    """Per direction: bytes per step, the time per step at least one transfer
+    of that direction was in flight (union of their intervals), the rate
+    while busy against the nominal and the measured plain-copy peak, and the
+    fraction of that busy time during which the compute stream was running a
+    unit's forward or backward."""
+    lk = r["link"]
+    comp = _union(lk["compute"])
+    out = {"peak_gbs": LINK_PEAK_GBS, "alone": alone}
+    for d in ("h2d", "d2h"):
+        parts = lk[d]
+        allsp = [sp for v in parts.values() for sp in v]
+        u = _union(allsp)
+        busy_ns = _length(u)
+        nbytes = sum(sp[2] for sp in allsp)
+        gbs = nbytes / busy_ns if busy_ns > 0 else None
+        measured = None if not alone else alone.get(f"{d}_gbs")
+        out[d] = {
+            "bytes_per_step": nbytes / steps,
+            "bytes_per_step_by_kind": {k: sum(sp[2] for sp in v) / steps for k, v in parts.items()},
+            "busy_ms_per_step": busy_ns / steps * 1e-6,
+            "gbs_while_busy": gbs,
+            "frac": None if gbs is None else gbs / LINK_PEAK_GBS,
+            "frac_of_measured_copy": None if gbs is None or not measured else gbs / measured,
+            "busy_frac_of_step": busy_ns * 1e-9 / r["elapsed"],
+            "under_compute_frac": (_overlap(u, comp) / busy_ns) if (busy_ns > 0 and lk["common_clock"]) else None,
+        }
+    out["compute_busy_frac_of_step"] = _length(comp) * 1e-9 / r["elapsed"]
+    out["note"] = ("rates over the union of all transfers of a direction (h2d: parameter copies, checkpoint "
+                   "prefetches, embedding lookup rows; d2h: SDMA gradient copies, checkpoint packs, embedding "
+                   "gradient rows), HIP events and SDMA engine timestamps on one clock; under_compute_frac: "
+                   "share of that time while the compute stream ran a unit's forward or backward (events "
+                   "at unit boundaries); alone: plain pinned copies of 1 GiB, one direction at a time")
+    return out
+
+
+def link_alone(dev, nbytes: int = 1 << 30, reps: int = 4) -> dict:
+    """Plain pinned-host <-> device copies of ``nbytes``, one direction at a
+    time on an idle GPU: the host link rate this box reaches."""
+    import torch
+
+    from test1_amd.pinned import pinned_empty
+
+    host = pinned_empty(nbytes, torch.uint8)
+    host.fill_(1)
+    devbuf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    st = torch.cuda.Stream(device=dev)
+    out = {}
+    for d, (dst, src) in (("h2d", (devbuf, host)), ("d2h", (host, devbuf))):
+        with torch.cuda.stream(st):
+            dst.copy_(src, non_blocking=True)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        with torch.cuda.stream(st):
+            for _ in range(reps):
+                dst.copy_(src, non_blocking=True)
+        e1.record(st)
+        st.synchronize()
+        out[f"{d}_gbs"] = nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del host, devbuf
+    torch.cuda.empty_cache()
+    return out
+
+
+def secondary_rooflines(r: dict) -> list:
+    """Host-link-bound kernels besides the staging cast: achieved rate over
+    their own intervals (timing events around each launch on its stream)."""
+    lk = r["link"]
+    rows = []
+    for kind, d, kernel, what in (
+            ("checkpoints", "d2h", "seg_kernel<OpCopy16> (8 workgroups)",
+             "checkpoint pack: HBM -> pinned host slot"),
+            ("rows", "h2d", "gather_rows_kernel<cast>", "embedding lookup: batch rows of the pinned fp32 host "
+                                                          "table -> bf16 hidden states in HBM"),
+            ("rows", "d2h", "gather_rows_kernel<copy> (8 workgroups)",
+             "embedding gradient rows: HBM -> pinned host")):
+        sp = lk[d].get(kind) or []
+        if not sp:
+            continue
+        ms = sum(e - s for s, e, _ in sp) * 1e-6
+        nb = sum(n for _, _, n in sp)
+        gbs = nb / (ms * 1e-3) / 1e9 if ms > 0 else None
+        rows.append({"kernel": kernel, "work": what, "bound": "host link", "launches": len(sp),
+                     "avg_launch_ms": ms / len(sp), "link_bytes_per_launch": nb / len(sp), "achieved": gbs,
+                     "peak": LINK_PEAK_GBS, "unit": "GB/s", "frac": None if gbs is None else gbs / LINK_PEAK_GBS})
+    return rows
 
 
 def main():
@@ -439,6 +607,10 @@ def main():
     ap.add_argument("--cast-on-copy", action="store_true",
                     help="cast a unit staged after its update on the cast stream as soon as its copy lands "
                          "(default: where the unit is next used, between the forward's kernels)")
+    ap.add_argument("--wait-timeout", type=float, default=None,
+                    help="seconds a host wait of the runtime may take (default: the library's; 0: no limit)")
+    ap.add_argument("--no-link-timing", action="store_true",
+                    help="do not record the host-link and compute intervals (no host_link figures)")
     ap.add_argument("--offload-dir", default="/tmp/sf_offload",
                     help="directory of the storage-offload files (removed as they are opened)")
     args = ap.parse_args()
@@ -467,29 +639,39 @@ def main():
     value = r["tokens"] / elapsed
 
     variants = {}
-    v = None
-    other = "bf16" if args.h2d_format == "fp32" else "fp32"
-    # host bytes the second wrapper allocates: fp32 master, bf16 grad slot and two fp32 moments
-    # per parameter, plus the bf16 copy with bf16 H2D; the first run's masters stay alive
-    need = r["total_params"] * (4 + 2 + 8 + (2 if other == "bf16" else 0))
-    avail = host_mem_available()
-    if not args.no_variants and avail and need > 0.8 * avail:
-        log(f"[bench] variant h2d_{other} skipped: needs ~{need / 1e9:.0f} GB of host memory, "
-            f"{avail / 1e9:.0f} GB available")
-        variants[f"h2d_{other}"] = {"skipped": f"needs ~{need / 1e9:.0f} GB host memory, {avail / 1e9:.0f} GB available"}
-    elif not args.no_variants:
+    if not args.no_variants:
+        vs, vw = min(args.steps, 10), min(args.warmup, 2)
+        # The reference's schedule: every unit in the 2-unit pool and reloaded
+        # for its backward (slide_fsdp.py:443-444), for models whose bf16
+        # weights do not fit in HBM.
         try:
-            v = timed_run(model, w, args, dev, other, args.resident_layers, args.d2h_engine, batch_seed=1)
-        except RuntimeError as e:  # e.g. the host cannot pin the bf16 copies
-            log(f"[bench] variant h2d_{other} failed: {e}")
-            v = None
-            variants[f"h2d_{other}"] = {"skipped": str(e)[:300]}
-    if not args.no_variants and v is not None:
-        variants[f"h2d_{other}"] = {
-            "value": v["tokens"] / v["elapsed"], "ms_per_step": v["elapsed"] / args.steps * 1e3,
-            "h2d_format": other, "resident_layers": v["resident_layers"], "d2h_engine": args.d2h_engine,
-            "host_link": link_stats(v, args.steps), "losses": v["losses"],
-        }
+            vp = timed_run(model, w, args, dev, args.h2d_format, 0, args.d2h_engine, batch_seed=2, steps=vs,
+                           warmup=vw)
+            variants["pool"] = variant_summary(vp, args.h2d_format, args.d2h_engine)
+        except RuntimeError as e:
+            log(f"[bench] variant pool failed: {e}")
+            variants["pool"] = {"skipped": str(e)[:300]}
+        # The other parameter H2D format, default residency.
+        other = "bf16" if args.h2d_format == "fp32" else "fp32"
+        # host bytes of the second wrapper: fp32 master, bf16 grad slot and two fp32
+        # moments per parameter, plus the bf16 copy with bf16 H2D
+        need = r["total_params"] * (4 + 2 + 8 + (2 if other == "bf16" else 0))
+        avail = host_mem_available()
+        if avail and need > 0.8 * avail:
+            log(f"[bench] variant h2d_{other} skipped: needs ~{need / 1e9:.0f} GB of host memory, "
+                f"{avail / 1e9:.0f} GB available")
+            variants[f"h2d_{other}"] = {"skipped": f"needs ~{need / 1e9:.0f} GB host memory, "
+                                                   f"{avail / 1e9:.0f} GB available"}
+        else:
+            try:
+                v = timed_run(model, w, args, dev, other, args.resident_layers, args.d2h_engine, batch_seed=1,
+                              steps=vs, warmup=vw)
+                variants[f"h2d_{other}"] = variant_summary(v, other, args.d2h_engine)
+            except RuntimeError as e:  # e.g. the host cannot pin the bf16 copies
+                log(f"[bench] variant h2d_{other} failed: {e}")
+                variants[f"h2d_{other}"] = {"skipped": str(e)[:300]}
+    link_alone_gbs = link_alone(dev)
+    log(f"[bench] plain pinned copies of 1 GiB: {link_alone_gbs}")
 
     total_params = r["total_params"]
     layer_numel = r["layer_numel"]
@@ -499,8 +681,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         t = time.time()
-        cpu = cpu_baseline(218_112_000 if w["arch"] == "llama" and w["hidden"] == 4096 else layer_numel,
-                           total_params, B * S, resident)
+        cpu = cpu_baseline(total_params, B * S, resident)
         log(f"[bench] cpu baseline in {time.time() - t:.1f}s: {cpu['sample']}")
 
     res = {
@@ -555,7 +736,8 @@ def main():
                         "update)")
                      + "; alone: one decoder layer's cast on an idle GPU after the timed steps"),
         },
-        "host_link": link_stats(r, args.steps),
+        "roofline_secondary": secondary_rooflines(r),
+        "host_link": link_stats(r, args.steps, link_alone_gbs),
         "model_tflops": {
             "flops_per_step": megatron_flops_per_step(w),
             "tflops": megatron_flops_per_step(w) / (elapsed / args.steps) / 1e12,

@@ -282,6 +282,11 @@ int sf_dma_query(const uint64_t* signals, int nsignals, int* done);
 /* Record start/end times of later copies (1) or stop (0). */
 int sf_dma_enable_timing(int on);
 
+/* The HSA system clock now, in ns: the clock of the copy times of
+ * sf_dma_wait, so a caller can place other timestamps (HIP events, anchored
+ * once) on the same timeline.  No reference counterpart; measurement only. */
+int sf_dma_clock_ns(uint64_t* ns);
+
 /* ---------------------------------------------------------------------
  * Host AdamW (libsf_cpu.so)
  * ------------------------------------------------------------------- */

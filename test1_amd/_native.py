@@ -94,6 +94,7 @@ HIP_SIGNATURES = {
                     ctypes.POINTER(ctypes.c_uint64)],
     "sf_dma_query": [ctypes.POINTER(ctypes.c_uint64), _i, ctypes.POINTER(ctypes.c_int)],
     "sf_dma_enable_timing": [_i],
+    "sf_dma_clock_ns": [ctypes.POINTER(ctypes.c_uint64)],
 }
 
 CPU_SIGNATURES = {

@@ -876,6 +876,21 @@ int sf_dma_query(const uint64_t* signals, int nsignals, int* done) {
     return SF_OK;
 }
 
+int sf_dma_clock_ns(uint64_t* ns) {
+    if (ns == nullptr) return SF_EINVAL;
+    uint64_t freq = 0;
+    {
+        std::lock_guard<std::mutex> lk(g_dma_mu);
+        if (!g_dma.ok || g_dma.ts_freq == 0) return SF_EINVAL;
+        freq = g_dma.ts_freq;
+    }
+    uint64_t ticks = 0;
+    const hsa_status_t st = hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP, &ticks);
+    if (st != HSA_STATUS_SUCCESS) return hsa_status_to_sf(st);
+    *ns = uint64_t((long double)ticks * (1e9L / (long double)freq));
+    return SF_OK;
+}
+
 int sf_dma_enable_timing(int on) {
     if (!g_dma.ok) return SF_EINVAL;
     return hsa_status_to_sf(hsa_amd_profiling_async_copy_enable(on != 0));

@@ -77,8 +77,16 @@ class RowSparseEmbedding:
         # The flag's previous writer (last step's lookup) finished before that
         # step's update, which wait_for_update has just waited for.
         self._bad_ids.zero_()
-        kernels.gather_rows(self._host_table(), flat, out.view(-1, H), bad=self._bad_ids,
-                            stream=torch.cuda.current_stream())
+        lt = self.runtime.link_timing
+        cur = torch.cuda.current_stream()
+        if lt is not None:
+            t0 = torch.cuda.Event(enable_timing=True)
+            t0.record(cur)
+        kernels.gather_rows(self._host_table(), flat, out.view(-1, H), bad=self._bad_ids, stream=cur)
+        if lt is not None:
+            t1 = torch.cuda.Event(enable_timing=True)
+            t1.record(cur)
+            lt["rows_h2d"].append((t0, t1, flat.numel() * H * self._host_table().element_size()))
         self._copy_lookup_ids(flat)
         self._bwd_compute_done = False
         self._grads_offloaded = False
@@ -236,8 +244,16 @@ class RowSparseEmbedding:
         rt.log("d2h", self.layer_idx)
         rt.mark("post_backward", self.layer_idx)
         rt.d2h_stream.wait_event(grad_ready)
+        lt = rt.link_timing
+        if lt is not None:
+            t0 = torch.cuda.Event(enable_timing=True)
+            t0.record(rt.d2h_stream)
         kernels.gather_rows(dense, flat, self._rows_host[:ntok], stream=rt.d2h_stream,
                             max_workgroups=rt.d2h_workgroups)
+        if lt is not None:
+            t1 = torch.cuda.Event(enable_timing=True)
+            t1.record(rt.d2h_stream)
+            lt["rows_d2h"].append((t0, t1, ntok * H * 2))
         kernels.memcpy_async(self._ids_host[:ntok], flat, rt.d2h_stream)
         dense.record_stream(rt.d2h_stream)
         flat.record_stream(rt.d2h_stream)

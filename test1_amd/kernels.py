@@ -378,6 +378,13 @@ def wait_event(ev, timeout: Optional[float], what: str) -> None:
         raise TimeoutError(f"{what}: not complete after {timeout:g} s")
 
 
+def dma_clock_ns() -> int:
+    """The HSA system clock in ns, the clock of the SDMA copy times."""
+    t = ctypes.c_uint64(0)
+    _native.check(_native.hip().sf_dma_clock_ns(ctypes.byref(t)), "sf_dma_clock_ns")
+    return t.value
+
+
 def dma_copy_d2h(pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]], timeout: Optional[float] = None):
     """Start SDMA copies of each contiguous GPU ``src`` into the pinned host
     ``dst`` of equal byte size.  The sources must already be complete on the

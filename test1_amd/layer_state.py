@@ -171,6 +171,35 @@ class StreamingRuntime:
         self.capture: Optional[dict] = None
         self.capture_units: Optional[set] = None
         self._held: List[Any] = []
+        # Optional measurement: when a dict (``enable_link_timing``), timing
+        # events of the units' compute on the compute stream and of the host
+        # link work besides the parameter and gradient copies (checkpoint
+        # packs and prefetches, embedding row gathers).
+        self.link_timing: Optional[Dict[str, Any]] = None
+
+    def enable_link_timing(self, on: bool = True) -> None:
+        """Start (or stop) recording the intervals ``link_timing`` holds:
+        "compute" [(start, end)] events around each unit's forward and
+        backward on the compute stream, and (start, end, bytes) events of
+        "act_d2h" / "act_h2d" (checkpoint packs and prefetches) and
+        "rows_h2d" / "rows_d2h" (embedding row gathers)."""
+        self.link_timing = ({"compute": [], "act_d2h": [], "act_h2d": [], "rows_h2d": [], "rows_d2h": []}
+                            if on else None)
+
+    def compute_mark(self, start: bool) -> None:
+        """With link timing on, a timing event on the current stream that
+        opens (``start``) or closes a unit's compute interval."""
+        lt = self.link_timing
+        if lt is None:
+            return
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record(torch.cuda.current_stream())
+        if start:
+            lt["_open"] = ev
+        else:
+            first = lt.pop("_open", None)
+            if first is not None:
+                lt["compute"].append((first, ev))
 
     def hold_forever(self, objs) -> None:
         """Keep ``objs`` referenced until the process ends: the host slot and

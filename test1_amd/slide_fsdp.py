@@ -431,6 +431,7 @@ class SlideFSDP(nn.Module):
                     next_layer_state.to_device_async(is_backward=is_output)
                 layer_state._post_called = False
                 layer_state.wait_for_h2d()
+                sf.runtime.compute_mark(True)
                 return hidden_states
 
             @staticmethod
@@ -438,6 +439,7 @@ class SlideFSDP(nn.Module):
                 # The gradient has flowed past the unit's first operation: all
                 # of its backward kernels, including those reading its
                 # weights, are enqueued.
+                sf.runtime.compute_mark(False)
                 ctx.layer_state.mark_backward_compute_done()
                 return grad_output, None, None
 
@@ -446,6 +448,7 @@ class SlideFSDP(nn.Module):
             def forward(ctx, hidden_states, layer_state, is_last_layer):
                 ctx.layer_state = layer_state
                 ctx.set_materialize_grads(False)
+                sf.runtime.compute_mark(False)
                 if not is_last_layer:
                     layer_state.to_offload_async(is_backward=False)
                 return hidden_states
@@ -511,6 +514,8 @@ class SlideFSDP(nn.Module):
         if idx - 1 >= 0:
             self.layer_states[idx - 1].to_device_async(is_backward=True)
         layer_state.wait_for_h2d()
+        if idx > 0:   # the embedding's backward (a gradient scatter) is not timed
+            self.runtime.compute_mark(True)
 
     def _on_post_backward(self, layer_state: LayerRuntimeState, idx: int) -> None:
         """After a unit's last gradient: pack, offload and queue the update
@@ -617,7 +622,8 @@ class SlideFSDP(nn.Module):
                                        max_workgroups=self.runtime.d2h_workgroups,
                                        stream=self.runtime.d2h_stream,
                                        prefetch_stream=self._act_prefetch_stream(),
-                                       pack_fence=self.runtime.stager.fence_after_casts):
+                                       pack_fence=self.runtime.stager.fence_after_casts,
+                                       link_timing=self.runtime.link_timing):
                     hidden_states = checkpoint(_layer_forward, hidden_states, causal_mask, self.position_embeddings,
                                                layer_state.layer, **ckpt_kw)
             else:

@@ -293,6 +293,7 @@ class SlidingCheckpoint(saved_tensors_hooks):
         prefetch_stream: Optional[torch.cuda.Stream] = None,
         pack_fence=None,
         spill: Optional[StorageSpill] = None,
+        link_timing: Optional[dict] = None,
     ):
         if gds_offload:
             if file_paths is None:
@@ -327,6 +328,9 @@ class SlidingCheckpoint(saved_tensors_hooks):
         # Optional callable(stream): orders the host-writing pack behind other
         # work (SlideFSDP passes its stager's cast fence).
         self.pack_fence = pack_fence
+        # Optional measurement: (start, end, bytes) timing events of each pack
+        # ("act_d2h") and prefetch ("act_h2d") appended to these lists.
+        self.link_timing = link_timing
 
         def pack_hook(tensor: torch.Tensor) -> Tuple[torch.device, Any]:
             if tensor.size() == torch.Size([0]):
@@ -364,6 +368,10 @@ class SlidingCheckpoint(saved_tensors_hooks):
             if not src.is_contiguous():
                 with torch.cuda.stream(self.stream):
                     src = src.contiguous()
+            t_pack = None
+            if self.link_timing is not None:
+                t_pack = torch.cuda.Event(enable_timing=True)
+                t_pack.record(self.stream)
             if src.element_size() == 2:
                 # 16-bit tensors are packed by a capped-grid kernel writing
                 # straight into the pinned slot (a few CUs keep the link busy).
@@ -372,6 +380,10 @@ class SlidingCheckpoint(saved_tensors_hooks):
             else:
                 kernels.memcpy_async(slot, src, self.stream)
             src.record_stream(self.stream)
+            if t_pack is not None:
+                done = torch.cuda.Event(enable_timing=True)
+                done.record(self.stream)
+                self.link_timing["act_d2h"].append((t_pack, done, nbytes))
             self.pack_counter += 1
             self._counts[(self._key, self.layer_idx)] = self.pack_counter
             if self.gds_offload:
@@ -420,12 +432,19 @@ class SlidingCheckpoint(saved_tensors_hooks):
                         bufs = [torch.empty(t.shape, dtype=t.dtype, device=self.device) for t in host]
                     ps = self.prefetch_stream
                     ps.wait_event(self.pre_unpack_event)
+                    timed = self.link_timing is not None
+                    if timed:
+                        t0 = torch.cuda.Event(enable_timing=True)
+                        t0.record(ps)
                     for h, d in zip(host, bufs):
                         kernels.memcpy_async(d, h, ps)
                         if self.ring is None:
                             d.record_stream(ps)
-                    ev = torch.cuda.Event()
+                    ev = torch.cuda.Event(enable_timing=timed)
                     ev.record(ps)
+                    if timed:
+                        self.link_timing["act_h2d"].append(
+                            (t0, ev, sum(h.numel() * h.element_size() for h in host)))
                     self.fifo.append((bufs, ev))
                     if self._trace is not None:
                         self._trace("act_h2d", nxt + 1)

@@ -380,3 +380,31 @@ def test_priority_update_executor_survives_a_failing_readiness_query():
         assert f2.result(timeout=10) == 42
     finally:
         ex.shutdown()
+
+
+def test_bench_link_arithmetic():
+    """The bench's host-link figures: transfers of one direction that overlap
+    count their bytes once over the union of their intervals, and the share
+    under compute is the intersection of that union with the compute
+    intervals."""
+    import bench
+
+    assert bench._union([(5, 7, 0), (0, 2, 0), (1, 3, 0), (7, 8, 0)]) == [[0, 3], [5, 8]]
+    assert bench._overlap([[0, 3], [5, 8]], [[2, 6], [7, 100]]) == 1 + 1 + 1
+    ms = 1_000_000   # ns
+    r = {"elapsed": 0.1, "link": {
+        "h2d": {"params": [(0, 20 * ms, 1_000_000_000)], "checkpoints": [(10 * ms, 30 * ms, 500_000_000)],
+                "rows": []},
+        "d2h": {"grads": [(40 * ms, 50 * ms, 400_000_000)], "checkpoints": [], "rows": []},
+        "compute": [(0, 15 * ms), (45 * ms, 60 * ms)],
+        "common_clock": True}}
+    st = bench.link_stats(r, steps=1, alone={"h2d_gbs": 60.0, "d2h_gbs": 50.0})
+    h = st["h2d"]
+    assert h["busy_ms_per_step"] == 30 and h["bytes_per_step"] == 1.5e9
+    assert abs(h["gbs_while_busy"] - 50.0) < 1e-9 and abs(h["frac_of_measured_copy"] - 50 / 60) < 1e-9
+    assert abs(h["under_compute_frac"] - 0.5) < 1e-9          # 15 of 30 ms under compute
+    d = st["d2h"]
+    assert abs(d["gbs_while_busy"] - 40.0) < 1e-9 and abs(d["under_compute_frac"] - 0.5) < 1e-9
+    assert abs(st["compute_busy_frac_of_step"] - 0.3) < 1e-9
+    r["link"]["common_clock"] = False                          # no SDMA clock: no overlap figure
+    assert bench.link_stats(r, steps=1)["h2d"]["under_compute_frac"] is None

@@ -12,7 +12,9 @@
  *     the SF_E* codes below; sf_error_string() turns any of them into text.
  *   - Device entry points are asynchronous on the caller's stream, allocate
  *     nothing and keep no global mutable state, so any host thread may call
- *     them concurrently on different streams.
+ *     them concurrently on different streams.  The one exception is
+ *     sf_stage_f32_bf16_noalloc, whose device scratch buffer is shared by
+ *     all its calls on a device (calls must not overlap there).
  *   - Sizes are element counts unless the name says bytes.
  *
  * Each declaration names the reference interface (file:line in the

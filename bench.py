@@ -516,7 +516,9 @@ def link_stats(r: dict, steps: int, alone: Optional[dict] = None) -> dict:
                    "prefetches, embedding lookup rows; d2h: SDMA gradient copies, checkpoint packs, embedding "
                    "gradient rows), HIP events and SDMA engine timestamps on one clock; under_compute_frac: "
                    "share of that time while the compute stream ran a unit's forward or backward (events "
-                   "at unit boundaries); alone: plain pinned copies of 1 GiB, one direction at a time")
+                   "at unit boundaries, after the stream's waits for the unit's weights and checkpoint; gaps "
+                   "between a unit's kernels count as compute); alone: plain pinned copies of 1 GiB, one "
+                   "direction at a time")
     return out
 
 

@@ -623,7 +623,8 @@ class SlideFSDP(nn.Module):
                                        stream=self.runtime.d2h_stream,
                                        prefetch_stream=self._act_prefetch_stream(),
                                        pack_fence=self.runtime.stager.fence_after_casts,
-                                       link_timing=self.runtime.link_timing):
+                                       link_timing=self.runtime.link_timing,
+                                       on_prefetch_ready=self._reopen_compute):
                     hidden_states = checkpoint(_layer_forward, hidden_states, causal_mask, self.position_embeddings,
                                                layer_state.layer, **ckpt_kw)
             else:
@@ -674,6 +675,12 @@ class SlideFSDP(nn.Module):
             s.release_device_unit()
             for p in s._params:
                 p.grad = None
+
+    def _reopen_compute(self) -> None:
+        """With link timing on: a unit's backward compute starts once its
+        checkpoint prefetch has arrived, not when the stream began to wait."""
+        if self.runtime.link_timing is not None:
+            self.runtime.compute_mark(True)
 
     def _grow_grad_ring(self) -> None:
         """After the first step, when its checkpoint slots and embedding rows

@@ -294,6 +294,7 @@ class SlidingCheckpoint(saved_tensors_hooks):
         pack_fence=None,
         spill: Optional[StorageSpill] = None,
         link_timing: Optional[dict] = None,
+        on_prefetch_ready=None,
     ):
         if gds_offload:
             if file_paths is None:
@@ -329,8 +330,11 @@ class SlidingCheckpoint(saved_tensors_hooks):
         # work (SlideFSDP passes its stager's cast fence).
         self.pack_fence = pack_fence
         # Optional measurement: (start, end, bytes) timing events of each pack
-        # ("act_d2h") and prefetch ("act_h2d") appended to these lists.
+        # ("act_d2h") and prefetch ("act_h2d") appended to these lists, and a
+        # callable run once the compute stream has been made to wait for this
+        # layer's prefetched checkpoint (the recompute starts after it).
         self.link_timing = link_timing
+        self.on_prefetch_ready = on_prefetch_ready
 
         def pack_hook(tensor: torch.Tensor) -> Tuple[torch.device, Any]:
             if tensor.size() == torch.Size([0]):
@@ -462,6 +466,8 @@ class SlidingCheckpoint(saved_tensors_hooks):
                 if isinstance(ev, Future):
                     ev = ev.result()
                 cur.wait_event(ev)
+                if self.on_prefetch_ready is not None:
+                    self.on_prefetch_ready()
             result = bufs[self.unpack_counter]
             self.unpack_counter += 1
             # Pop once every prefetched tensor of this layer has been served.

@@ -94,6 +94,19 @@ int sf_cast_f32_bf16_timed(const float* src, uint16_t* dst, size_t n,
                            sf_stream_t stream, sf_event_t start,
                            sf_event_t stop);
 
+/* fp32 -> fp16 for units of dtype float16: IEEE round to nearest even with
+ * subnormals, overflow to infinity, NaN -> quiet NaN (sign and the top 9
+ * payload bits kept), dst[i] = rne_f16(src[i]) for i < n.  The cast of
+ * layer_state.py:301 when the convert buffer has the config's dtype float16
+ * (config.py:110-113, slide_fsdp.py:181-186): torch's CPU fp32 -> fp16
+ * conversion, here in HBM.  The _timed variant stamps events as
+ * sf_cast_f32_bf16_timed does. */
+int sf_cast_f32_f16(const float* src, uint16_t* dst, size_t n,
+                    sf_stream_t stream);
+int sf_cast_f32_f16_timed(const float* src, uint16_t* dst, size_t n,
+                          sf_stream_t stream, sf_event_t start,
+                          sf_event_t stop);
+
 /* Stage n fp32 values from pinned host memory into a bf16 device array:
  * dst[i] = rne(host_src[i]) (the rounding of sf_cast_f32_bf16).  The values
  * travel in pieces of workspace_elems (rounded down to a multiple of 8)
@@ -310,8 +323,9 @@ typedef struct sf_adam_hparams {
 } sf_adam_hparams;
 
 /* Stateless AdamW over n elements: fp32 params and moments updated in
- * place, grads read as g_dtype (SF_DTYPE_F32 or SF_DTYPE_BF16; bf16 is
- * widened exactly, so the result equals the fp32 call on `grad.float()`).
+ * place, grads read as g_dtype (SF_DTYPE_F32, SF_DTYPE_BF16 or
+ * SF_DTYPE_F16; 16-bit grads are widened exactly, so the result equals the
+ * fp32 call on `grad.float()`).
  * Per-element operation order follows Adam_Optimizer::Step_AVX,
  * optimizer/layer_adam/csrc/cpu_adam.h:143-192. */
 int sf_cpu_adam_step(float* params, const void* grads, int g_dtype,

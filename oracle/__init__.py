@@ -6,6 +6,8 @@ checker.  The product (``test1_amd``) never imports, links or runs it.
 
 Contents (each function cites the reference file:line it restates):
   cast_f32_bf16    layer_state.py:301                fp32 -> bf16 RNE cast
+  cast_f32_f16     layer_state.py:301 (float16 units) fp32 -> fp16 RNE cast
+  widen_f16        optimizer/layer_adam/layer_adam.py:404   fp16 -> fp32
   widen_bf16       optimizer/layer_adam/layer_adam.py:404   bf16 -> fp32
   pack_b16         layer_state.py:241-264, distributed_sync.py:353
   layer_layout     layer_state.py:241-264            flat offsets and views
@@ -24,9 +26,12 @@ from .oracle import (  # noqa: F401
     OracleAdam,
     cast_f32_bf16,
     cast_f32_bf16_c,
+    cast_f32_f16,
+    cast_f32_f16_c,
     layer_layout,
     lib_path,
     pack_b16,
     step_schedule,
     widen_bf16,
+    widen_f16,
 )

@@ -33,6 +33,7 @@ def _lib() -> ctypes.CDLL:
         vp, sz = ctypes.c_void_p, ctypes.c_size_t
         f = ctypes.c_float
         lib.oracle_cast_f32_bf16.argtypes = [vp, vp, sz]
+        lib.oracle_cast_f32_f16.argtypes = [vp, vp, sz]
         lib.oracle_widen_bf16.argtypes = [vp, vp, sz]
         lib.oracle_adam_init.argtypes = [vp, f, f, f, f, f, ctypes.c_int]
         lib.oracle_adam_update.argtypes = [vp, sz, f, f, f, f, f, ctypes.c_int, vp, vp, vp, vp, sz]
@@ -70,6 +71,65 @@ def cast_f32_bf16_c(x: np.ndarray) -> np.ndarray:
     out = np.empty(x.shape, dtype=np.uint16)
     _lib().oracle_cast_f32_bf16(x.ctypes.data, out.ctypes.data, x.size)
     return out
+
+
+def cast_f32_f16(x: np.ndarray) -> np.ndarray:
+    """fp32 -> fp16 bit patterns (uint16): IEEE round to nearest even with
+    subnormals, overflow to infinity, NaN -> quiet NaN keeping the sign and
+    the top 9 payload bits (sign | 0x7E00 | mantissa >> 13).
+
+    Restates the CPU cast of reference layer_state.py:301 for units of dtype
+    float16 (the convert buffer takes the config's dtype, slide_fsdp.py:
+    181-186; config.py:110-113 allows float16): torch's CPU float -> half
+    conversion.  Pinned by: torch CPU ``.to(torch.float16)`` itself on bit
+    sweeps and specials; numpy's own float -> half conversion (an independent
+    IEEE implementation) on every non-NaN input of the sweeps; closed forms
+    (exact halves map to themselves, the largest half 65504, the tie 65520 to
+    infinity, the smallest subnormal 2**-24 and the tie 2**-25 to zero)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    sign = ((u >> 16) & 0x8000).astype(np.uint64)
+    a = u & 0x7FFFFFFF
+    out = np.zeros(u.shape, dtype=np.uint64)
+    nan = a > 0x7F800000
+    inf = ~nan & (a >= 0x477FF000)
+    normal = ~nan & ~inf & (a >= 0x38800000)
+    sub = ~nan & ~inf & ~normal
+    out[nan] = 0x7E00 | ((a[nan] >> 13) & 0x1FF)
+    out[inf] = 0x7C00
+    r = a[normal] - 0x38000000
+    out[normal] = (r + 0xFFF + ((r >> 13) & 1)) >> 13
+    e = a[sub] >> 23
+    m = (a[sub] & 0x7FFFFF) | 0x800000
+    shift = np.clip(126 - e.astype(np.int64), 14, 40).astype(np.uint64)
+    q = m >> shift
+    rem = m & ((np.uint64(1) << shift) - 1)
+    half = np.uint64(1) << (shift - 1)
+    up = (rem > half) | ((rem == half) & ((q & 1) == 1))
+    val = q + up.astype(np.uint64)
+    val[e < 102] = 0
+    out[sub] = val
+    return (out | sign).astype(np.uint16)
+
+
+def cast_f32_f16_c(x: np.ndarray) -> np.ndarray:
+    """The same fp16 cast through the scalar C restatement (oracle/sf_oracle.c)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    _lib().oracle_cast_f32_f16(x.ctypes.data, out.ctypes.data, x.size)
+    return out
+
+
+def widen_f16(h: np.ndarray) -> np.ndarray:
+    """fp16 bit patterns -> fp32, exact: the ``grad.float()`` of reference
+    optimizer/layer_adam/layer_adam.py:404 for float16 units.  Pinned by torch
+    CPU ``.float()`` on all 65536 fp16 patterns, NaN payloads included (a
+    signaling NaN comes back quiet)."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = h.view(np.float16).astype(np.float32).view(np.uint32)   # exact for every non-NaN
+    nan = ((h & 0x7C00) == 0x7C00) & ((h & 0x3FF) != 0)
+    hn = h[nan].astype(np.uint32)
+    out[nan] = ((hn & 0x8000) << 16) | 0x7FC00000 | ((hn & 0x3FF) << 13)
+    return out.view(np.float32)
 
 
 def widen_bf16(b: np.ndarray) -> np.ndarray:
@@ -215,11 +275,17 @@ class LayerAdamOracle:
         return self.groups[idx]["m"], self.groups[idx]["v"]
 
     def step_layer(self, idx: int, grads: Sequence[np.ndarray]) -> None:
-        """grads: per-parameter arrays, float32 or bf16 bit patterns (uint16)."""
+        """grads: per-parameter arrays, float32, bf16 bit patterns (uint16) or
+        float16."""
         grp = self.groups[idx]
         grp["step"] += 1
         for p, g, (m, v) in zip(grp["params"], grads, grp["views"]):
-            g32 = widen_bf16(g) if g.dtype == np.uint16 else np.ascontiguousarray(g, np.float32)
+            if g.dtype == np.uint16:
+                g32 = widen_bf16(g)
+            elif g.dtype == np.float16:
+                g32 = widen_f16(g.view(np.uint16))
+            else:
+                g32 = np.ascontiguousarray(g, np.float32)
             self.adam.update(grp["step"], self.lr, self.betas[0], self.betas[1], self.eps, self.wd,
                              self.bias_correction, p.reshape(-1), g32.reshape(-1), m, v)
 

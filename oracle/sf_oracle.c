@@ -29,6 +29,40 @@ void oracle_cast_f32_bf16(const float* src, uint16_t* dst, size_t n) {
     for (size_t i = 0; i < n; ++i) dst[i] = rne(src[i]);
 }
 
+/* fp32 -> fp16, for units of dtype float16: the same cast of
+ * layer_state.py:301 into a float16 convert buffer (torch's CPU conversion):
+ * IEEE round to nearest even with subnormals, overflow to infinity, NaN ->
+ * quiet NaN keeping the sign and the top 9 payload bits.  Written from the
+ * IEEE definition: scale to units of the result's last place, round. */
+static uint16_t rne_f16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    const uint32_t a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((a >> 13) & 0x1FFu));
+    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
+    const int e = (int)(a >> 23);                 /* biased fp32 exponent */
+    if (e == 0) return sign;                      /* fp32 zero or subnormal: far below 2^-24 */
+    const uint32_t m = (a & 0x7FFFFFu) | 0x800000u;
+    /* value = m * 2^(e-150); the half's unit in the last place is 2^-24 below
+     * 2^-14 and 2^(e-127-10) above it */
+    const int ulp_exp = e >= 113 ? e - 137 : -24;
+    const int shift = ulp_exp - (e - 150);        /* bits of m below that unit */
+    if (shift > 31) return sign;
+    uint32_t q = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) ++q;
+    if (e >= 113) {
+        /* q is 1.mantissa in [2^10, 2^11]; a carry to 2^11 moves to the next binade */
+        return (uint16_t)(sign | ((((uint32_t)(e - 112)) << 10) + (q - 0x400u)));
+    }
+    return (uint16_t)(sign | q);                  /* subnormal, or 0x400 = the smallest normal */
+}
+
+void oracle_cast_f32_f16(const float* src, uint16_t* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = rne_f16(src[i]);
+}
+
 /* bf16 -> fp32 widening: the `.float()` of layer_adam.py:404. */
 void oracle_widen_bf16(const uint16_t* src, float* dst, size_t n) {
     for (size_t i = 0; i < n; ++i) {

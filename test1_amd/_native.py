@@ -70,6 +70,8 @@ HIP_SIGNATURES = {
     "sf_abi_version": [],
     "sf_cast_f32_bf16": [_vp, _vp, _sz, _vp],
     "sf_cast_f32_bf16_timed": [_vp, _vp, _sz, _vp, _vp, _vp],
+    "sf_cast_f32_f16": [_vp, _vp, _sz, _vp],
+    "sf_cast_f32_f16_timed": [_vp, _vp, _sz, _vp, _vp, _vp],
     "sf_event_create": [ctypes.POINTER(ctypes.c_void_p)],
     "sf_event_destroy": [_vp],
     "sf_event_elapsed_ms": [_vp, _vp, ctypes.POINTER(ctypes.c_float)],

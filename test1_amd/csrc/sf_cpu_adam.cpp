@@ -1,4 +1,5 @@
-// Host AdamW for LayerAdam: fp32 params and moments, fp32 or bf16 grads.
+// Host AdamW for LayerAdam: fp32 params and moments, fp32, bf16 or fp16 grads
+// (the row-wise update: fp32 or bf16).
 //
 // The update is bound by host DRAM bandwidth (26 bytes per element with bf16
 // grads: read p, g, m, v and write p, m, v; 28 when it also writes the bf16
@@ -106,10 +107,38 @@ inline void adam_one_tail(float& p, float g, float& m, float& v, const Scalars& 
     p = std::fma(u, c.step_size, p);
 }
 
+// fp16 -> fp32, exact (every fp16 value is an fp32 value): the widening of
+// `grad.float()` for fp16 units.  A signaling NaN comes back quiet, as the
+// hardware conversion gives it.
+inline float f16_to_f32(uint16_t h) {
+    const uint32_t sign = uint32_t(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    uint32_t u;
+    if (e == 0x1Fu) {
+        u = sign | 0x7F800000u | (m << 13) | (m ? 0x400000u : 0u);
+    } else if (e != 0) {
+        u = sign | ((e + 112u) << 23) | (m << 13);
+    } else if (m == 0) {
+        u = sign;
+    } else {
+        // subnormal: m x 2^-24, renormalised
+        uint32_t mm = m, ee = 113u;
+        while ((mm & 0x400u) == 0) {
+            mm <<= 1;
+            --ee;
+        }
+        u = sign | (ee << 23) | ((mm & 0x3FFu) << 13);
+    }
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
 template <int GDT>
 inline float load_grad(const void* g, size_t i) {
-    return GDT == SF_DTYPE_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(g)[i])
-                                : static_cast<const float*>(g)[i];
+    if (GDT == SF_DTYPE_BF16) return bf16_to_f32(static_cast<const uint16_t*>(g)[i]);
+    if (GDT == SF_DTYPE_F16) return f16_to_f32(static_cast<const uint16_t*>(g)[i]);
+    return static_cast<const float*>(g)[i];
 }
 
 template <int GDT>
@@ -160,6 +189,9 @@ __attribute__((target("avx512f,avx512bw"))) void adam_range_avx512(float* p, con
             const __m256i h = _mm256_loadu_si256(
                 reinterpret_cast<const __m256i*>(static_cast<const uint16_t*>(g) + i));
             gv = _mm512_castsi512_ps(_mm512_slli_epi32(_mm512_cvtepu16_epi32(h), 16));
+        } else if (GDT == SF_DTYPE_F16) {
+            gv = _mm512_cvtph_ps(_mm256_loadu_si256(
+                reinterpret_cast<const __m256i*>(static_cast<const uint16_t*>(g) + i)));
         } else {
             gv = _mm512_loadu_ps(static_cast<const float*>(g) + i);
         }
@@ -312,6 +344,7 @@ int sf_cpu_adam_step_cast(float* params, const void* grads, int g_dtype, float* 
     switch (g_dtype) {
         case SF_DTYPE_F32: adam_parallel<SF_DTYPE_F32>(params, grads, exp_avg, exp_avg_sq, n, c, params_bf16); break;
         case SF_DTYPE_BF16: adam_parallel<SF_DTYPE_BF16>(params, grads, exp_avg, exp_avg_sq, n, c, params_bf16); break;
+        case SF_DTYPE_F16: adam_parallel<SF_DTYPE_F16>(params, grads, exp_avg, exp_avg_sq, n, c, params_bf16); break;
         default: return SF_EDTYPE;
     }
     return SF_OK;
@@ -480,7 +513,7 @@ int sf_adam_update_cast(int optimizer_id, size_t step, float lr, float beta1, fl
                         int g_dtype, float* exp_avg, float* exp_avg_sq, uint16_t* params_bf16, size_t n) {
     std::shared_ptr<AdamState> st = find_state(optimizer_id);
     if (!st) return SF_ENOOPT;
-    if (g_dtype != SF_DTYPE_F32 && g_dtype != SF_DTYPE_BF16) return SF_EDTYPE;
+    if (g_dtype != SF_DTYPE_F32 && g_dtype != SF_DTYPE_BF16 && g_dtype != SF_DTYPE_F16) return SF_EDTYPE;
     if (n > 0 && (!params || !grads || !exp_avg || !exp_avg_sq)) return SF_EINVAL;
     sf_adam_hparams hp;
     stateful_hparams(*st, step, lr, beta1, beta2, eps, weight_decay, bias_correction, hp);

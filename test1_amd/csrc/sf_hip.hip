@@ -48,6 +48,29 @@ __device__ __forceinline__ uint32_t rne_bf16(uint32_t u) {
     return ((u & 0x7FFFFFFFu) > 0x7F800000u) ? 0xFFFFu : r;
 }
 
+// fp32 -> fp16, IEEE round to nearest even with subnormals; overflow to
+// infinity; NaN -> quiet NaN keeping the sign and the top 9 payload bits.
+// This is what torch's CPU cast gives (`.to(torch.float16)`, the reference's
+// staging of fp16 units, layer_state.py:301); the tests pin it against that
+// routine.  Integer arithmetic only, so the result does not depend on the
+// shader's floating-point modes.
+__device__ __forceinline__ uint32_t rne_f16(uint32_t u) {
+    const uint32_t sign = (u >> 16) & 0x8000u;
+    const uint32_t a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return sign | 0x7E00u | ((a >> 13) & 0x1FFu);   // NaN
+    if (a >= 0x477FF000u) return sign | 0x7C00u;                          // rounds past 65504
+    if (a >= 0x38800000u) {                                               // normal half
+        const uint32_t r = a - 0x38000000u;                               // exponent rebias 127 -> 15
+        return sign | ((r + 0xFFFu + ((r >> 13) & 1u)) >> 13);
+    }
+    const uint32_t e = a >> 23;                                           // subnormal half or zero
+    if (e < 102u) return sign;                                            // below half the smallest subnormal
+    const uint32_t m = (a & 0x7FFFFFu) | 0x800000u;
+    const uint32_t s = 126u - e;                                          // 14 .. 24
+    const uint32_t q = m >> s, rem = m & ((1u << s) - 1u), half = 1u << (s - 1u);
+    return sign | (q + ((rem > half) | ((rem == half) & (q & 1u))));
+}
+
 __device__ __forceinline__ uint32_t pack2(uint32_t lo, uint32_t hi) {
     return lo | (hi << 16);
 }
@@ -60,6 +83,25 @@ __device__ __forceinline__ u32x4 cast8(const f32x4 a, const f32x4 b) {
     o.w = pack2(rne_bf16(__float_as_uint(b.z)), rne_bf16(__float_as_uint(b.w)));
     return o;
 }
+
+__device__ __forceinline__ u32x4 cast8_f16(const f32x4 a, const f32x4 b) {
+    u32x4 o;
+    o.x = pack2(rne_f16(__float_as_uint(a.x)), rne_f16(__float_as_uint(a.y)));
+    o.y = pack2(rne_f16(__float_as_uint(a.z)), rne_f16(__float_as_uint(a.w)));
+    o.z = pack2(rne_f16(__float_as_uint(b.x)), rne_f16(__float_as_uint(b.y)));
+    o.w = pack2(rne_f16(__float_as_uint(b.z)), rne_f16(__float_as_uint(b.w)));
+    return o;
+}
+
+// Output formats of the flat cast.
+struct ToBf16 {
+    __device__ static u32x4 cast8(const f32x4 a, const f32x4 b) { return ::cast8(a, b); }
+    __device__ static uint16_t cast1(float x) { return uint16_t(rne_bf16(__float_as_uint(x))); }
+};
+struct ToF16 {
+    __device__ static u32x4 cast8(const f32x4 a, const f32x4 b) { return cast8_f16(a, b); }
+    __device__ static uint16_t cast1(float x) { return uint16_t(rne_f16(__float_as_uint(x))); }
+};
 
 // ---------------------------------------------------------------------
 // Flat cast: n8 groups of 8 elements, both pointers 16-byte aligned.
@@ -76,8 +118,9 @@ __device__ __forceinline__ u32x4 cast8(const f32x4 a, const f32x4 b) {
 // with 2 groups, and 0.245-0.249 against 0.252-0.256 ms beside the
 // backward's kernels.
 // ---------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void cast_flat_kernel(
-    const float* __restrict__ src, uint16_t* __restrict__ dst, uint64_t n8) {
+template <typename Fmt>
+__device__ __forceinline__ void cast_flat_body(const float* __restrict__ src, uint16_t* __restrict__ dst,
+                                               uint64_t n8) {
     // Highest issue priority among the waves of its SIMD: staged units are
     // cast while the backward's GEMMs run on the same CUs, and the cast's few
     // instructions per byte then issue without queueing behind MFMA waves
@@ -97,7 +140,7 @@ __global__ __launch_bounds__(kThreads) void cast_flat_kernel(
         }
 #pragma unroll
         for (int k = 0; k < kCastUnroll; ++k) {
-            __builtin_nontemporal_store(cast8(a[k], b[k]),
+            __builtin_nontemporal_store(Fmt::cast8(a[k], b[k]),
                 reinterpret_cast<u32x4*>(dst + (tile0 + k * kThreads + threadIdx.x) * kGroup));
         }
     } else {
@@ -105,10 +148,21 @@ __global__ __launch_bounds__(kThreads) void cast_flat_kernel(
             const uint64_t g = tile0 + k * kThreads + threadIdx.x;
             if (g < n8) {
                 const f32x4* p = reinterpret_cast<const f32x4*>(src + g * kGroup);
-                __builtin_nontemporal_store(cast8(p[0], p[1]), reinterpret_cast<u32x4*>(dst + g * kGroup));
+                __builtin_nontemporal_store(Fmt::cast8(p[0], p[1]), reinterpret_cast<u32x4*>(dst + g * kGroup));
             }
         }
     }
+}
+
+// The staging cast to bf16 (the default unit dtype) and to fp16.
+__global__ __launch_bounds__(kThreads) void cast_flat_kernel(
+    const float* __restrict__ src, uint16_t* __restrict__ dst, uint64_t n8) {
+    cast_flat_body<ToBf16>(src, dst, n8);
+}
+
+__global__ __launch_bounds__(kThreads) void cast_flat_f16_kernel(
+    const float* __restrict__ src, uint16_t* __restrict__ dst, uint64_t n8) {
+    cast_flat_body<ToF16>(src, dst, n8);
 }
 
 // ---------------------------------------------------------------------
@@ -154,11 +208,12 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
 }
 
 // Scalar cast for tails and for pointers that are not 16-byte aligned.
+template <typename Fmt>
 __global__ __launch_bounds__(kThreads) void cast_scalar_kernel(
     const float* __restrict__ src, uint16_t* __restrict__ dst, uint64_t n) {
     const uint64_t stride = uint64_t(gridDim.x) * kThreads;
     for (uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
-        dst[i] = uint16_t(rne_bf16(__float_as_uint(src[i])));
+        dst[i] = Fmt::cast1(src[i]);
     }
 }
 
@@ -363,7 +418,8 @@ namespace {
 // ``start`` / ``stop`` (may be null) are stamped by the runtime around the
 // first and the last launch's own dispatch, so they time the kernels alone,
 // not what the stream waited for before them.
-int cast_launch(const float* src, uint16_t* dst, size_t n, hipStream_t st, hipEvent_t start, hipEvent_t stop) {
+int cast_launch(const float* src, uint16_t* dst, size_t n, hipStream_t st, hipEvent_t start, hipEvent_t stop,
+                bool to_f16 = false) {
     if (n == 0) {
         // nothing to launch: the events still mark the (empty) interval
         if (start != nullptr) {
@@ -387,8 +443,8 @@ int cast_launch(const float* src, uint16_t* dst, size_t n, hipStream_t st, hipEv
     if (n8 > 0) {
         const uint64_t blocks = ceil_div(n8, uint64_t(kThreads) * kCastUnroll);
         if (blocks > kMaxBlocks) return SF_EINVAL;
-        hipExtLaunchKernelGGL(cast_flat_kernel, dim3(uint32_t(blocks)), dim3(kThreads), 0, st, start,
-                              tail ? nullptr : stop, 0, src, dst, n8);
+        hipExtLaunchKernelGGL(to_f16 ? cast_flat_f16_kernel : cast_flat_kernel, dim3(uint32_t(blocks)),
+                              dim3(kThreads), 0, st, start, tail ? nullptr : stop, 0, src, dst, n8);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return int(e);
     }
@@ -396,8 +452,8 @@ int cast_launch(const float* src, uint16_t* dst, size_t n, hipStream_t st, hipEv
         const uint64_t rest = n - done;
         uint64_t blocks = ceil_div(rest, kThreads);
         if (blocks > 65536) blocks = 65536;
-        hipExtLaunchKernelGGL(cast_scalar_kernel, dim3(uint32_t(blocks)), dim3(kThreads), 0, st,
-                              n8 > 0 ? nullptr : start, stop, 0, src + done, dst + done, rest);
+        hipExtLaunchKernelGGL(to_f16 ? cast_scalar_kernel<ToF16> : cast_scalar_kernel<ToBf16>, dim3(uint32_t(blocks)),
+                              dim3(kThreads), 0, st, n8 > 0 ? nullptr : start, stop, 0, src + done, dst + done, rest);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return int(e);
     }
@@ -417,6 +473,17 @@ int sf_cast_f32_bf16_timed(const float* src, uint16_t* dst, size_t n, sf_stream_
     if ((start == nullptr) != (stop == nullptr)) return SF_EINVAL;
     return cast_launch(src, dst, n, reinterpret_cast<hipStream_t>(stream), reinterpret_cast<hipEvent_t>(start),
                        reinterpret_cast<hipEvent_t>(stop));
+}
+
+int sf_cast_f32_f16(const float* src, uint16_t* dst, size_t n, sf_stream_t stream) {
+    return cast_launch(src, dst, n, reinterpret_cast<hipStream_t>(stream), nullptr, nullptr, true);
+}
+
+int sf_cast_f32_f16_timed(const float* src, uint16_t* dst, size_t n, sf_stream_t stream, sf_event_t start,
+                          sf_event_t stop) {
+    if ((start == nullptr) != (stop == nullptr)) return SF_EINVAL;
+    return cast_launch(src, dst, n, reinterpret_cast<hipStream_t>(stream), reinterpret_cast<hipEvent_t>(start),
+                       reinterpret_cast<hipEvent_t>(stop), true);
 }
 
 int sf_event_create(sf_event_t* ev) {

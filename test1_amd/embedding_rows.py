@@ -124,10 +124,12 @@ class RowSparseEmbedding:
         model right before its backward, which is then certain to reach the
         lookup (not in the reference, whose update of the whole table waits
         for the gradient)."""
+        if not self.row_sparse:
+            return   # a unit staged whole updates in one part, after its gradient
         rt = self.runtime
         opt = self.layer_optimizer
         lookup, self._lookup_ids = self._lookup_ids, None
-        if (not self.row_sparse or lookup is None or opt is None or not getattr(opt, "reference_order", False)
+        if (lookup is None or opt is None or not getattr(opt, "reference_order", False)
                 or not self.layer.weight.requires_grad):
             return
         if getattr(opt, "offloader", None) is not None:

@@ -67,30 +67,40 @@ class KernelTimer:
                     lib.sf_event_destroy(ev)
 
 
+_CASTS = {torch.bfloat16: ("sf_cast_f32_bf16", "sf_cast_f32_bf16_timed"),
+          torch.float16: ("sf_cast_f32_f16", "sf_cast_f32_f16_timed")}
+
+
+def cast_f32_16_(dst: torch.Tensor, src: torch.Tensor, stream: Optional[torch.cuda.Stream] = None,
+                 timer: Optional[KernelTimer] = None) -> torch.Tensor:
+    """dst[:] = src rounded to nearest even into dst's 16-bit float type
+    (bfloat16 or float16); both flat-contiguous GPU tensors of equal numel.
+    With ``timer``, its events are stamped around the cast kernels."""
+    if src.dtype != torch.float32 or dst.dtype not in _CASTS:
+        raise TypeError(f"cast_f32_16_: need float32 -> bfloat16 or float16, got {src.dtype} -> {dst.dtype}")
+    _require_cuda(src, "src")
+    _require_cuda(dst, "dst")
+    _require_contig(src, "src")
+    _require_contig(dst, "dst")
+    if src.numel() != dst.numel():
+        raise ValueError(f"cast_f32_16_: numel mismatch {src.numel()} vs {dst.numel()}")
+    plain, timed = _CASTS[dst.dtype]
+    if timer is None:
+        _native.check(getattr(_native.hip(), plain)(src.data_ptr(), dst.data_ptr(), src.numel(),
+                                                    _stream_ptr(stream)), plain)
+    else:
+        _native.check(getattr(_native.hip(), timed)(src.data_ptr(), dst.data_ptr(), src.numel(), _stream_ptr(stream),
+                                                    timer.start, timer.stop), timed)
+    return dst
+
+
 def cast_f32_bf16_(dst: torch.Tensor, src: torch.Tensor, stream: Optional[torch.cuda.Stream] = None,
                    timer: Optional[KernelTimer] = None) -> torch.Tensor:
     """dst[:] = RNE-bf16(src), both flat-contiguous GPU tensors of equal numel.
     With ``timer``, its events are stamped around the cast kernels."""
     if src.dtype != torch.float32 or dst.dtype != torch.bfloat16:
         raise TypeError(f"cast_f32_bf16_: need float32 -> bfloat16, got {src.dtype} -> {dst.dtype}")
-    _require_cuda(src, "src")
-    _require_cuda(dst, "dst")
-    _require_contig(src, "src")
-    _require_contig(dst, "dst")
-    if src.numel() != dst.numel():
-        raise ValueError(f"cast_f32_bf16_: numel mismatch {src.numel()} vs {dst.numel()}")
-    if timer is None:
-        _native.check(
-            _native.hip().sf_cast_f32_bf16(src.data_ptr(), dst.data_ptr(), src.numel(), _stream_ptr(stream)),
-            "sf_cast_f32_bf16",
-        )
-    else:
-        _native.check(
-            _native.hip().sf_cast_f32_bf16_timed(src.data_ptr(), dst.data_ptr(), src.numel(), _stream_ptr(stream),
-                                                 timer.start, timer.stop),
-            "sf_cast_f32_bf16_timed",
-        )
-    return dst
+    return cast_f32_16_(dst, src, stream, timer)
 
 
 def _check_stage_args(dst: torch.Tensor, host_src: torch.Tensor) -> None:

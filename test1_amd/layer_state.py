@@ -588,7 +588,7 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
     def _dummy_dst(self) -> torch.Tensor:
         # Only used to drain a staging ticket after a failed acquire: casts
         # into a scratch buffer so the ring's slot events stay consistent.
-        return torch.empty(self.total_size, dtype=torch.bfloat16, device=self.runtime.device)
+        return torch.empty(self.total_size, dtype=self.buffer_pool.dtype, device=self.runtime.device)
 
     def wait_for_h2d(self, timeout: Optional[float] = None) -> None:
         """Make the current stream wait for this unit's load (no host block).

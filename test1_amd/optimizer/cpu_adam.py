@@ -10,8 +10,8 @@ through pybind11; the same three are offered here over the C ABI of
   destroy_adam(id) -> 0
 
 Supported dtypes: fp32 params and fp32 moments (the combination LayerAdam
-uses, layer_adam.py:158 with fp32_optimizer_state=True), with fp32 or bf16
-grads; bf16 grads are widened exactly, so they give the bits of the
+uses, layer_adam.py:158 with fp32_optimizer_state=True), with fp32, bf16 or
+fp16 grads; 16-bit grads are widened exactly, so they give the bits of the
 reference's ``grad.float()`` call.  Other combinations raise the reference's
 RuntimeError.  Deliberate differences from the reference: a non-contiguous
 params/exp_avg/exp_avg_sq raises ValueError instead of silently updating a
@@ -55,6 +55,8 @@ def _grad_dtype_code(g: torch.Tensor) -> int:
         return _native.SF_DTYPE_F32
     if g.dtype == torch.bfloat16:
         return _native.SF_DTYPE_BF16
+    if g.dtype == torch.float16:
+        return _native.SF_DTYPE_F16
     return -1
 
 

@@ -228,8 +228,6 @@ class SlideFSDP(nn.Module):
         super().__init__()
         if config.param_transfer_mode != "full":
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
-        if config.dtype != torch.bfloat16:
-            raise NotImplementedError("SlideFSDP stages parameters as bfloat16; dtype=float16 is not supported")
         self.config = config
         self.device = torch.device(config.device)
         if self.device.type != "cuda":
@@ -363,8 +361,11 @@ class SlideFSDP(nn.Module):
         return rt.h2d_stream
 
     def _row_sparse_ok(self) -> bool:
+        """The row gathers round to bf16: float16 units stage the embedding
+        whole, as the reference does."""
         emb = self.embed_tokens
-        return (isinstance(emb, nn.Embedding) and emb.max_norm is None and not emb.scale_grad_by_freq
+        return (self.dtype == torch.bfloat16 and isinstance(emb, nn.Embedding) and emb.max_norm is None
+                and not emb.scale_grad_by_freq
                 and not emb.sparse and emb.weight.shape[1] % 16 == 0 and len(list(emb.parameters())) == 1)
 
     def _auto_resident(self) -> int:

@@ -5,7 +5,7 @@ pieces a unit's update and staging can be split into.
   units reused in FIFO order, each with a ``ready`` event its next writer
   waits on.
 * ``H2DStager``: pinned fp32 master -> device fp32 (DMA on ``h2d_stream``)
-  -> bf16 unit (HIP cast kernel), through a ring of chunk slots or a
+  -> bf16 or fp16 unit (HIP cast kernel), through a ring of chunk slots or a
   whole-unit slot whose cast can wait until the unit is used; replaces the
   host cast + bf16 copy of reference layer_state.py:296-314.
 * ``BF16Loader``: the host optimizer's pinned bf16 copy -> device bf16 unit,
@@ -195,7 +195,7 @@ class _SlotPool:
 
 
 class H2DStager:
-    """Pinned fp32 master -> device bf16 unit, through a device fp32 ring.
+    """Pinned fp32 master -> device bf16 (or fp16) unit, through a device fp32 ring.
 
     Two phases, so the host link never waits for a pool unit:
       ``begin``   issues the DMA copies of the first ``depth`` chunks into
@@ -300,7 +300,7 @@ class H2DStager:
                 s = t.slots[j]
                 self.cast_stream.wait_event(t.copied[j])
                 timer = kernels.KernelTimer() if timing else None
-                kernels.cast_f32_bf16_(dst_bf16[off:off + c], self._slot(s, c), self.cast_stream, timer=timer)
+                kernels.cast_f32_16_(dst_bf16[off:off + c], self._slot(s, c), self.cast_stream, timer=timer)
                 freed = _new_event()
                 freed.record(self.cast_stream)
                 if timing:
@@ -356,7 +356,7 @@ class H2DStager:
             stream.wait_event(p.wait_event)
         stream.wait_event(p.copied)
         timer = kernels.KernelTimer() if self.cast_timing is not None else None
-        kernels.cast_f32_bf16_(dst_bf16[:p.n], p.slot[:p.n], stream, timer=timer)
+        kernels.cast_f32_16_(dst_bf16[:p.n], p.slot[:p.n], stream, timer=timer)
         freed = _new_event()
         freed.record(stream)
         if timer is not None:

@@ -50,14 +50,15 @@ def unit_params(model):
             + [[m.norm.weight, model.lm_head.weight]])
 
 
-def gpu_bf16_copy(model, dev):
-    """The model's architecture on the GPU in bf16, each weight the RNE cast of
-    its fp32 weight (cast on the GPU parameter by parameter, so no second host
-    copy is made); rotary frequencies rebuilt in fp32 as in the host model."""
+def gpu_bf16_copy(model, dev, dtype=torch.bfloat16):
+    """The model's architecture on the GPU in ``dtype`` (bf16 or fp16), each
+    weight the RNE cast of its fp32 weight (cast on the GPU parameter by
+    parameter, so no second host copy is made); rotary frequencies rebuilt in
+    fp32 as in the host model."""
     cfg = model.config
     with torch.device("meta"):
         gm = type(model)(cfg)
-    gm = gm.to(torch.bfloat16).to_empty(device=dev)
+    gm = gm.to(dtype).to_empty(device=dev)
     gm.model.rotary_emb = type(model.model.rotary_emb)(config=cfg).to(dev)
     with torch.no_grad():
         for (n, gp), (n2, p) in zip(gm.named_parameters(), model.named_parameters()):

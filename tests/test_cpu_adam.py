@@ -63,6 +63,30 @@ def test_stateless_step_matches_oracle_on_large_tensor():
     cpu_adam.destroy_adam(50)
 
 
+def test_fp16_grads_match_the_oracle_on_widened_grads():
+    """float16 units: fp16 gradients read directly give the bits of the update
+    on ``grad.float()`` (reference layer_adam.py:404), including subnormal
+    and large fp16 values, over a vector body and a ragged tail."""
+    rng = np.random.default_rng(2)
+    n = 1_000_003
+    p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    g32 = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    g32[:64] = np.array([2.0 ** -24, -(2.0 ** -20), 6e-8, 65504.0, -1000.0, 0.0, -0.0, 1e-7] * 8, np.float32)
+    g = torch.from_numpy(g32).half()
+    tp, tm, tv = torch.from_numpy(p.copy()), torch.zeros(n), torch.zeros(n)
+    m, v = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    cpu_adam.create_adam(51, 1e-5, 0.9, 0.999, 1e-8, 0.01, True)
+    opt = oracle.OracleAdam(1e-5, (0.9, 0.999), 1e-8, 0.01, True)
+    for step in (1, 2, 3):
+        cpu_adam.adam_update(51, step, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, tp, g, tm, tv)
+        widened = oracle.widen_f16(g.view(torch.int16).numpy().view(np.uint16))
+        opt.update(step, 1e-5, 0.9, 0.999, 1e-8, 0.01, True, p, widened, m, v)
+    assert np.array_equal(tp.numpy().view(np.uint32), p.view(np.uint32))
+    assert np.array_equal(tm.numpy().view(np.uint32), m.view(np.uint32))
+    assert np.array_equal(tv.numpy().view(np.uint32), v.view(np.uint32))
+    cpu_adam.destroy_adam(51)
+
+
 def test_adam_update_errors_like_reference():
     cpu_adam.create_adam(60, 1e-3)
     p = torch.zeros(8)

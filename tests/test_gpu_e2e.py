@@ -446,6 +446,8 @@ def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, 
             flat_before = np.concatenate([a.reshape(-1) for a in ref_units[u]])
             assert np.array_equal(master_before.numpy().view(np.uint32), flat_before.view(np.uint32)), f"unit {u}"
             g = u16(grads)
+            if sf.dtype == torch.float16:
+                g = g.view(np.float16)
             parts, off = [], 0
             for a in ref_units[u]:
                 parts.append(g[off:off + a.size].reshape(a.shape))
@@ -468,10 +470,12 @@ def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, 
     sf.close()
 
 
-def reference_losses(model, steps_ids, dev):
-    """Non-offloaded run: bf16 model on the GPU, same loss as OutputLayer,
-    fp32 masters updated by the oracle AdamW unit by unit (last unit first)."""
-    gm = gpu_bf16_copy(model, dev)
+def reference_losses(model, steps_ids, dev, dtype=torch.bfloat16):
+    """Non-offloaded run: the model on the GPU in ``dtype``, same loss as
+    OutputLayer, fp32 masters updated by the oracle AdamW unit by unit (last
+    unit first)."""
+    cast = oracle.cast_f32_bf16 if dtype == torch.bfloat16 else oracle.cast_f32_f16
+    gm = gpu_bf16_copy(model, dev, dtype)
     units_gpu = units_of(gm)
     masters = [[p.detach().float().numpy().copy() for p in ps] for ps in units_of(model)]
     orc = oracle.LayerAdamOracle(lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
@@ -482,8 +486,8 @@ def reference_losses(model, steps_ids, dev):
         with torch.no_grad():
             for ps, arrs in zip(units_gpu, masters):
                 for p, a in zip(ps, arrs):
-                    b = oracle.cast_f32_bf16(a)
-                    p.data.copy_(torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).view(p.shape))
+                    b = cast(a)
+                    p.data.copy_(torch.from_numpy(b.view(np.int16)).view(dtype).view(p.shape))
         ids = ids.to(dev)
         gm.zero_grad(set_to_none=True)
         hidden = gm.model(input_ids=ids).last_hidden_state
@@ -495,7 +499,7 @@ def reference_losses(model, steps_ids, dev):
         if first_grads is None:
             first_grads = grads
         for u in range(len(units_gpu) - 1, -1, -1):
-            orc.step_layer(u, grads[u])
+            orc.step_layer(u, grads[u] if dtype == torch.bfloat16 else [g.view(np.float16) for g in grads[u]])
     return losses, first_grads
 
 
@@ -504,6 +508,38 @@ def test_loss_parity_with_non_offloaded_run(dev, h2d_format, resident, d2h_engin
     check_loss_parity(dev, arch, fused, {}, dict(h2d_format=h2d_format, resident_layers=resident,
                                                  d2h_engine=d2h_engine, grad_ring_depth=ring,
                                                  fused_cross_entropy=fused))
+
+
+@pytest.mark.parametrize("h2d_format", ["fp32", "bf16"])
+def test_whole_embedding_matches_oracle_bit_exact(dev, h2d_format):
+    """``row_sparse_embedding=False``: the embedding unit is staged whole and
+    its whole gradient offloaded, as the reference does; every update is the
+    oracle's over 3 steps, and the 10-step losses equal the non-offloaded
+    run's."""
+    sf = check_updates_against_oracle(dev, "llama", h2d_format, {}, dict(row_sparse_embedding=False), keep=True)
+    assert not sf.layer_states[0].row_sparse
+    sf.close()
+    check_loss_parity(dev, "llama", False, {}, dict(h2d_format=h2d_format, row_sparse_embedding=False))
+
+
+@pytest.mark.parametrize("resident,d2h_engine", [(0, "sdma"), (L - 1, "kernel")])
+def test_float16_units_match_oracle_bit_exact(dev, resident, d2h_engine):
+    """dtype=float16 (the reference's config allows it, config.py:110-113):
+    units staged with the fp32 -> fp16 cast, fp16 gradients offloaded and
+    widened exactly by the host AdamW; every update, moment and packed
+    gradient is the oracle's over 3 steps.  The embedding is staged whole
+    (its row gathers round to bf16)."""
+    sf = check_updates_against_oracle(dev, "llama", "fp32", dict(dtype=torch.float16),
+                                      dict(resident_layers=resident, d2h_engine=d2h_engine), keep=True)
+    assert sf.dtype == torch.float16 and not sf.layer_states[0].row_sparse
+    assert sf.buffer_pool.pool[0]["param"].dtype == torch.float16
+    sf.close()
+
+
+def test_float16_loss_parity_with_non_offloaded_run(dev):
+    """float16 units against a non-offloaded fp16 run of the same weights:
+    step-1 gradients and the 10 losses bit-identical."""
+    check_loss_parity(dev, "qwen2", False, dict(dtype=torch.float16), dict(resident_layers=L - 1))
 
 
 def test_piecewise_loss_parity(dev):
@@ -525,7 +561,7 @@ def check_loss_parity(dev, arch, fused, cfg_kw, sf_kw):
 
     model = make_model(arch)
     steps = batches(10)
-    ref_losses, ref_grads = reference_losses(model, steps, dev)
+    ref_losses, ref_grads = reference_losses(model, steps, dev, cfg_kw.get("dtype", torch.bfloat16))
     sf = SlideFSDP(model, SlideFSDPConfig(device=dev, lr=LR, weight_decay=WD, adam_betas=BETAS, adam_eps=EPS,
                                           **cfg_kw),
                    wait_timeout=120, **sf_kw)

@@ -32,6 +32,23 @@ def test_cast_flat_matches_oracle(dev, n):
     assert np.array_equal(bits16(out), oracle.cast_f32_bf16(x.numpy()))
 
 
+@pytest.mark.parametrize("n", [0, 1, 9, 8193, (1 << 20) | 13])
+def test_cast_f16_matches_oracle(dev, n):
+    """The fp32 -> fp16 staging cast of float16 units: random bit patterns (NaN
+    payloads, infinities, subnormals and overflow included) and normal values
+    of every magnitude, bit-exact against the oracle (pinned to torch's CPU
+    cast); an unaligned view takes the scalar kernel."""
+    bits = np.random.default_rng(n).integers(0, 1 << 32, n, dtype=np.uint64).astype(np.uint32)
+    x = torch.from_numpy(bits.view(np.float32).copy())
+    x[: n // 2] = rand_f32(n // 2, n, std=300.0)
+    out = torch.full((n + 1,), 7.0, dtype=torch.float16, device=dev)
+    kernels.cast_f32_16_(out[:n], x.to(dev))
+    kernels.cast_f32_16_(out[1:n + 1] if n else out[:0], x.to(dev))       # dst off by 2 bytes
+    torch.cuda.synchronize()
+    exp = oracle.cast_f32_f16(x.numpy())
+    assert np.array_equal(bits16(out[1:n + 1]), exp)
+
+
 def test_cast_golden_and_random_bit_patterns(dev):
     d = np.load(os.path.join(GOLDEN, "cast_f32_bf16.npz"))
     rng = np.random.default_rng(0)

@@ -57,6 +57,60 @@ def test_widen_all_bf16_patterns():
     assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
 
 
+# ---------------------------------------------------------------- fp16 cast (float16 units)
+def _f16_sweep():
+    # every high half-word with low half-words around the rounding point of
+    # fp16's 13 dropped bits, plus random patterns
+    hi = np.arange(1 << 16, dtype=np.uint32)
+    lo = np.array([0, 1, 0x0FFF, 0x1000, 0x1001, 0x2000, 0x3000, 0xF000, 0xFFFF], dtype=np.uint32)
+    bits = (hi[:, None] << 16 | lo[None, :]).reshape(-1)
+    rnd = np.random.default_rng(5).integers(0, 1 << 32, 500_000, dtype=np.uint64).astype(np.uint32)
+    return np.concatenate([bits, rnd]).view(np.float32)
+
+
+def test_f16_cast_matches_torch_on_bit_sweep():
+    x = _f16_sweep()
+    exp = torch.from_numpy(x.copy()).to(torch.float16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(oracle.cast_f32_f16(x), exp)
+    assert np.array_equal(oracle.cast_f32_f16_c(x), exp)
+
+
+def test_f16_cast_matches_numpy_on_non_nan():
+    # numpy's float -> half conversion is an independent IEEE implementation
+    x = _f16_sweep()
+    ok = ~np.isnan(x)
+    with np.errstate(over="ignore"):
+        exp = x[ok].astype(np.float16).view(np.uint16)
+    assert np.array_equal(oracle.cast_f32_f16(x)[ok], exp)
+
+
+def test_f16_cast_closed_forms():
+    f = lambda v: oracle.cast_f32_f16(np.array(v, dtype=np.float32)).tolist()   # noqa: E731
+    assert f([1.0, -2.0, 0.0, -0.0, 65504.0]) == [0x3C00, 0xC000, 0x0000, 0x8000, 0x7BFF]
+    assert f([65519.996, 65520.0, -1e30]) == [0x7BFF, 0x7C00, 0xFC00]     # the tie 65520 goes to inf
+    assert f([2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -25, 2.0 ** -14]) == [0x0001, 0x0000, 0x0002, 0x0400]
+    assert f([1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11]) == [0x3C00, 0x3C02]  # ties to even
+    nans = np.array([0x7FC00000, 0xFF800001, 0x7FBFFFFF], np.uint32).view(np.float32)
+    assert oracle.cast_f32_f16(nans).tolist() == [0x7E00, 0xFE00, 0x7FFF]
+
+
+def test_f16_cast_check_catches_truncation():
+    # a planted mistake (the 13 dropped bits truncated) must fail the torch sweep
+    x = _f16_sweep()
+    ok = (np.abs(x) < 60000) & (np.abs(x) > 1e-4)
+    u = x[ok].view(np.uint32)
+    trunc = (((u >> 16) & 0x8000) | (((u & 0x7FFFFFFF) - 0x38000000) >> 13)).astype(np.uint16)
+    exp = torch.from_numpy(x[ok].copy()).to(torch.float16).view(torch.int16).numpy().view(np.uint16)
+    assert not np.array_equal(trunc, exp)
+    assert np.array_equal(oracle.cast_f32_f16(x[ok]), exp)
+
+
+def test_widen_all_f16_patterns():
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    exp = torch.from_numpy(h.view(np.int16).copy()).view(torch.float16).float().numpy()
+    assert np.array_equal(oracle.widen_f16(h).view(np.uint32), exp.view(np.uint32))
+
+
 # ---------------------------------------------------------------- pack / layout
 def test_pack_is_concatenation_and_inverts():
     rng = np.random.default_rng(0)

@@ -550,9 +550,60 @@ def link_alone(dev, nbytes: int = 1 << 30, reps: int = 4) -> dict:
     return out
 
 
-def secondary_rooflines(r: dict) -> list:
+def link_kernels_alone(dev, w: dict, reps: int = 10) -> dict:
+    """The host-link kernels of the step on an otherwise idle GPU, at the
+    step's shapes: the embedding lookup (batch rows of a pinned fp32 table
+    of the vocabulary's size, cast to bf16), the gradient rows and the
+    checkpoint pack (bf16 into pinned host memory, 8 workgroups).  Average
+    ms per launch (HIP events around each launch, 3 warmups) and GB/s of
+    link bytes."""
+    import torch
+
+    from test1_amd import kernels
+    from test1_amd.pinned import pinned_empty
+
+    V, H, ntok = w["vocab"], w["hidden"], w["batch"] * w["seq"]
+    g = torch.Generator().manual_seed(3)
+    ids = torch.randint(0, V, (ntok,), generator=g).to(dev)
+    table = pinned_empty((V, H), torch.float32)
+    table.fill_(0.5)
+    rows_dev = torch.empty(ntok, H, dtype=torch.bfloat16, device=dev)
+    dense = torch.zeros(V, H, dtype=torch.bfloat16, device=dev)
+    rows_host = pinned_empty((ntok, H), torch.bfloat16)
+    act = torch.zeros(w["batch"], w["seq"], H, dtype=torch.bfloat16, device=dev)
+    act_host = pinned_empty(tuple(act.shape), torch.bfloat16)
+    st = torch.cuda.Stream(device=dev)
+    cases = {
+        "gather_rows_kernel<cast>": (lambda: kernels.gather_rows(table, ids, rows_dev, stream=st), ntok * H * 4),
+        "gather_rows_kernel<copy> (8 workgroups)": (
+            lambda: kernels.gather_rows(dense, ids, rows_host, stream=st, max_workgroups=8), ntok * H * 2),
+        "seg_kernel<OpCopy16> (8 workgroups)": (
+            lambda: kernels.copy_segs_b16([(act.view(-1), act_host.view(-1))], st, max_workgroups=8),
+            act.numel() * 2),
+    }
+    out = {}
+    for name, (fn, nbytes) in cases.items():
+        for _ in range(3):
+            fn()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in evs:
+            a.record(st)
+            fn()
+            b.record(st)
+        st.synchronize()
+        ms = sum(a.elapsed_time(b) for a, b in evs) / reps
+        out[name] = {"avg_launch_ms": ms, "achieved": nbytes / (ms * 1e-3) / 1e9,
+                     "frac": nbytes / (ms * 1e-3) / 1e9 / LINK_PEAK_GBS}
+    del table, dense, rows_host, act_host
+    torch.cuda.empty_cache()
+    return out
+
+
+def secondary_rooflines(r: dict, alone: Optional[dict] = None) -> list:
     """Host-link-bound kernels besides the staging cast: achieved rate over
-    their own intervals (timing events around each launch on its stream)."""
+    their own intervals in the step (timing events around each launch on its
+    stream; the link is shared with the copies running beside them) and, in
+    ``alone``, on an idle GPU."""
     lk = r["link"]
     rows = []
     for kind, d, kernel, what in (
@@ -570,7 +621,8 @@ def secondary_rooflines(r: dict) -> list:
         gbs = nb / (ms * 1e-3) / 1e9 if ms > 0 else None
         rows.append({"kernel": kernel, "work": what, "bound": "host link", "launches": len(sp),
                      "avg_launch_ms": ms / len(sp), "link_bytes_per_launch": nb / len(sp), "achieved": gbs,
-                     "peak": LINK_PEAK_GBS, "unit": "GB/s", "frac": None if gbs is None else gbs / LINK_PEAK_GBS})
+                     "peak": LINK_PEAK_GBS, "unit": "GB/s", "frac": None if gbs is None else gbs / LINK_PEAK_GBS,
+                     "alone": None if not alone else alone.get(kernel)})
     return rows
 
 
@@ -674,6 +726,8 @@ def main():
                 variants[f"h2d_{other}"] = {"skipped": str(e)[:300]}
     link_alone_gbs = link_alone(dev)
     log(f"[bench] plain pinned copies of 1 GiB: {link_alone_gbs}")
+    kernels_alone = link_kernels_alone(dev, w)
+    log(f"[bench] host-link kernels alone: {kernels_alone}")
 
     total_params = r["total_params"]
     layer_numel = r["layer_numel"]
@@ -738,7 +792,7 @@ def main():
                         "update)")
                      + "; alone: one decoder layer's cast on an idle GPU after the timed steps"),
         },
-        "roofline_secondary": secondary_rooflines(r),
+        "roofline_secondary": secondary_rooflines(r, kernels_alone),
         "host_link": link_stats(r, args.steps, link_alone_gbs),
         "model_tflops": {
             "flops_per_step": megatron_flops_per_step(w),

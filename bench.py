@@ -41,6 +41,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, GB/s
 LINK_PEAK_GBS = 63.0      # PCIe 5.0 x16, per direction, GB/s
+D2H_WORKGROUPS = 16       # grid of the kernels writing into pinned host memory (the runtime's default)
 
 WORKLOADS = {
     "llama3-8b": dict(vocab=128256, hidden=4096, inter=14336, layers=32, heads=32, kv=8, head_dim=128,
@@ -554,7 +555,7 @@ def link_kernels_alone(dev, w: dict, reps: int = 10) -> dict:
     """The host-link kernels of the step on an otherwise idle GPU, at the
     step's shapes: the embedding lookup (batch rows of a pinned fp32 table
     of the vocabulary's size, cast to bf16), the gradient rows and the
-    checkpoint pack (bf16 into pinned host memory, 8 workgroups).  Average
+    checkpoint pack (bf16 into pinned host memory, the runtime's 16 workgroups).  Average
     ms per launch (HIP events around each launch, 3 warmups) and GB/s of
     link bytes."""
     import torch
@@ -575,10 +576,10 @@ def link_kernels_alone(dev, w: dict, reps: int = 10) -> dict:
     st = torch.cuda.Stream(device=dev)
     cases = {
         "gather_rows_kernel<cast>": (lambda: kernels.gather_rows(table, ids, rows_dev, stream=st), ntok * H * 4),
-        "gather_rows_kernel<copy> (8 workgroups)": (
-            lambda: kernels.gather_rows(dense, ids, rows_host, stream=st, max_workgroups=8), ntok * H * 2),
-        "seg_kernel<OpCopy16> (8 workgroups)": (
-            lambda: kernels.copy_segs_b16([(act.view(-1), act_host.view(-1))], st, max_workgroups=8),
+        "gather_rows_kernel<copy> (16 workgroups)": (
+            lambda: kernels.gather_rows(dense, ids, rows_host, stream=st, max_workgroups=D2H_WORKGROUPS), ntok * H * 2),
+        "seg_kernel<OpCopy16> (16 workgroups)": (
+            lambda: kernels.copy_segs_b16([(act.view(-1), act_host.view(-1))], st, max_workgroups=D2H_WORKGROUPS),
             act.numel() * 2),
     }
     out = {}
@@ -607,11 +608,11 @@ def secondary_rooflines(r: dict, alone: Optional[dict] = None) -> list:
     lk = r["link"]
     rows = []
     for kind, d, kernel, what in (
-            ("checkpoints", "d2h", "seg_kernel<OpCopy16> (8 workgroups)",
+            ("checkpoints", "d2h", "seg_kernel<OpCopy16> (16 workgroups)",
              "checkpoint pack: HBM -> pinned host slot"),
             ("rows", "h2d", "gather_rows_kernel<cast>", "embedding lookup: batch rows of the pinned fp32 host "
                                                           "table -> bf16 hidden states in HBM"),
-            ("rows", "d2h", "gather_rows_kernel<copy> (8 workgroups)",
+            ("rows", "d2h", "gather_rows_kernel<copy> (16 workgroups)",
              "embedding gradient rows: HBM -> pinned host")):
         sp = lk[d].get(kind) or []
         if not sp:

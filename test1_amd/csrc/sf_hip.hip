@@ -5,8 +5,8 @@
 // copies), never the matrix cores.  The kernels therefore use
 //   - 128-bit global loads and stores, 8 elements per lane per group,
 //   - several independent groups per lane to keep enough bytes in flight,
-//   - 256-lane workgroups (4 wave64s) and an exact grid of many thousands
-//     of workgroups so all 256 CUs over the 8 XCDs stay busy,
+//   - 128- or 256-lane workgroups (2 or 4 wave64s) and an exact grid of
+//     many thousands of workgroups so all 256 CUs over the 8 XCDs stay busy,
 //   - no LDS and no MFMA.
 //
 // The C ABI is declared in include/slidefsdp.h.
@@ -29,6 +29,7 @@ namespace {
 constexpr int kThreads = 256;  // lanes per workgroup (4 wave64s)
 constexpr int kUnroll = 4;     // 8-element groups per lane per workgroup tile
 constexpr int kCastUnroll = 1; // the same for the flat cast (measured best, see below)
+constexpr int kCastThreads = 128;  // lanes per workgroup of the flat cast (2 wave64s, see below)
 constexpr int kGroup = 8;      // elements per 128-bit bf16 store
 constexpr uint64_t kTileElems = uint64_t(kThreads) * kUnroll * kGroup;  // 8192
 
@@ -105,9 +106,9 @@ struct ToF16 {
 
 // ---------------------------------------------------------------------
 // Flat cast: n8 groups of 8 elements, both pointers 16-byte aligned.
-// Workgroup b owns groups [b*kThreads*kCastUnroll, (b+1)*kThreads*kCastUnroll);
-// within it, unroll step k covers one contiguous run of kThreads groups,
-// so every load/store instruction of a wave touches one contiguous 1 KiB
+// Workgroup b owns groups [b*kCastThreads*kCastUnroll, (b+1)*kCastThreads*kCastUnroll);
+// within it, unroll step k covers one contiguous run of kCastThreads groups,
+// so every load/store instruction of a wave touches one contiguous 2 KiB
 // span.  Loads are ordinary (cached) 128-bit loads and stores are
 // nontemporal.  On gfx950, 218M-element layer, alternating runs on one box:
 // 2 groups per lane 6.16 TB/s, against 5.61 TB/s with nontemporal loads as
@@ -116,7 +117,13 @@ struct ToF16 {
 // workgroup, 106,500 workgroups), measured later on another box in the
 // training step: 0.2172-0.2182 ms per layer alone against 0.2245-0.2253
 // with 2 groups, and 0.245-0.249 against 0.252-0.256 ms beside the
-// backward's kernels.
+// backward's kernels.  Workgroup size, one group per lane, same layer, two
+// rounds on one box: 64 lanes 0.214 ms, 128 lanes 0.2124-0.2131 (6.15 TB/s,
+// 0.77 of peak), 256 lanes 0.2144-0.2157, 512 0.216-0.217, 1024 0.221-0.222;
+// a plain fp32 copy of the same bytes reaches 0.79 of peak.  Loads with every
+// lane's 16 bytes contiguous across the wave (then 8-byte stores, or 16-byte
+// stores after a lane-pair exchange), a blockIdx order that gives each XCD
+// one contiguous eighth, and persistent grid-stride loops were no faster.
 // ---------------------------------------------------------------------
 template <typename Fmt>
 __device__ __forceinline__ void cast_flat_body(const float* __restrict__ src, uint16_t* __restrict__ dst,
@@ -126,26 +133,26 @@ __device__ __forceinline__ void cast_flat_body(const float* __restrict__ src, ui
     // instructions per byte then issue without queueing behind MFMA waves
     // (in a training step: 0.2537 -> 0.2492 ms per Llama layer).
     __builtin_amdgcn_s_setprio(3);
-    const uint64_t tile0 = uint64_t(blockIdx.x) * (kThreads * kCastUnroll);
-    if (tile0 + kThreads * kCastUnroll <= n8) {
+    const uint64_t tile0 = uint64_t(blockIdx.x) * (kCastThreads * kCastUnroll);
+    if (tile0 + kCastThreads * kCastUnroll <= n8) {
         // Full tile (every workgroup but possibly the last): all loads are
         // issued before the first conversion, with no per-lane predicate
         // between them.
         f32x4 a[kCastUnroll], b[kCastUnroll];
 #pragma unroll
         for (int k = 0; k < kCastUnroll; ++k) {
-            const f32x4* p = reinterpret_cast<const f32x4*>(src + (tile0 + k * kThreads + threadIdx.x) * kGroup);
+            const f32x4* p = reinterpret_cast<const f32x4*>(src + (tile0 + k * kCastThreads + threadIdx.x) * kGroup);
             a[k] = p[0];
             b[k] = p[1];
         }
 #pragma unroll
         for (int k = 0; k < kCastUnroll; ++k) {
             __builtin_nontemporal_store(Fmt::cast8(a[k], b[k]),
-                reinterpret_cast<u32x4*>(dst + (tile0 + k * kThreads + threadIdx.x) * kGroup));
+                reinterpret_cast<u32x4*>(dst + (tile0 + k * kCastThreads + threadIdx.x) * kGroup));
         }
     } else {
         for (int k = 0; k < kCastUnroll; ++k) {
-            const uint64_t g = tile0 + k * kThreads + threadIdx.x;
+            const uint64_t g = tile0 + k * kCastThreads + threadIdx.x;
             if (g < n8) {
                 const f32x4* p = reinterpret_cast<const f32x4*>(src + g * kGroup);
                 __builtin_nontemporal_store(Fmt::cast8(p[0], p[1]), reinterpret_cast<u32x4*>(dst + g * kGroup));
@@ -155,12 +162,12 @@ __device__ __forceinline__ void cast_flat_body(const float* __restrict__ src, ui
 }
 
 // The staging cast to bf16 (the default unit dtype) and to fp16.
-__global__ __launch_bounds__(kThreads) void cast_flat_kernel(
+__global__ __launch_bounds__(kCastThreads) void cast_flat_kernel(
     const float* __restrict__ src, uint16_t* __restrict__ dst, uint64_t n8) {
     cast_flat_body<ToBf16>(src, dst, n8);
 }
 
-__global__ __launch_bounds__(kThreads) void cast_flat_f16_kernel(
+__global__ __launch_bounds__(kCastThreads) void cast_flat_f16_kernel(
     const float* __restrict__ src, uint16_t* __restrict__ dst, uint64_t n8) {
     cast_flat_body<ToF16>(src, dst, n8);
 }
@@ -172,8 +179,32 @@ __global__ __launch_bounds__(kThreads) void cast_flat_f16_kernel(
 // (the row-sparse embedding load) and dst may be pinned host memory (the
 // row-sparse gradient offload, then with a capped grid).  An id outside
 // [0, nrows) yields a row of 0xFFFF (a NaN in bf16) and sets *bad.
+//
+// Each lane issues the loads of kRows 8-element groups of its row (kRows =
+// whole groups per lane, 1 to 4, picked at launch from the row length) before
+// the first store, so a row crosses the host link in one round trip.  Those
+// passes carry no per-lane predicate: under one, the compiler waits for all
+// outstanding memory operations before each store, and since stores count as
+// outstanding, each store into host memory would wait for the previous one
+// to be acknowledged over the link.  The groups left over (fewer than
+// kThreads * kRows) go one per lane with a predicate.  With a capped
+// 8-workgroup grid for the gradient-row offload (HBM -> pinned host, rows of
+// 4096 bf16) the unpredicated two-group pass measured 52.1-53.7 GB/s alone
+// against 47.7-48.3 GB/s with one group in flight per lane or with
+// predicated stores, and 55.6 GB/s with the offload's 16 workgroups; the
+// lookup (host -> HBM, one workgroup per row) is at the link's rate either
+// way (53.9 GB/s).
 // ---------------------------------------------------------------------
 template <bool kCast>
+__device__ __forceinline__ u32x4 gather_group(const void* __restrict__ src, uint64_t base, uint64_t g) {
+    if (kCast) {
+        const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(src) + base + g * kGroup);
+        return cast8(p[0], p[1]);
+    }
+    return reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + base)[g];
+}
+
+template <bool kCast, int kRows>
 __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
     const void* __restrict__ src, const int64_t* __restrict__ ids, uint64_t ntok, uint64_t row_len,
     uint64_t nrows, uint16_t* __restrict__ dst, uint32_t* __restrict__ bad, int vec) {
@@ -187,17 +218,32 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
         }
         const uint64_t base = uint64_t(r) * row_len;
         if (vec) {
+            constexpr uint64_t kPass = uint64_t(kThreads) * kRows;
             const uint64_t g8 = row_len / kGroup;
-            for (uint64_t g = threadIdx.x; g < g8; g += kThreads) {
-                u32x4 v;
-                if (kCast) {
-                    const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(src) + base + g * kGroup);
-                    v = cast8(p[0], p[1]);
-                } else {
-                    v = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + base)[g];
+            const uint64_t full = g8 / kPass * kPass;
+            for (uint64_t g0 = 0; g0 < full; g0 += kPass) {
+                f32x4 a[kRows], b[kRows];
+                u32x4 v[kRows];
+#pragma unroll
+                for (int k = 0; k < kRows; ++k) {
+                    const uint64_t g = g0 + uint64_t(k) * kThreads + threadIdx.x;
+                    if (kCast) {
+                        const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(src) + base +
+                                                                       g * kGroup);
+                        a[k] = p[0];
+                        b[k] = p[1];
+                    } else {
+                        v[k] = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + base)[g];
+                    }
                 }
-                __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(out) + g);
+#pragma unroll
+                for (int k = 0; k < kRows; ++k) {
+                    const uint64_t g = g0 + uint64_t(k) * kThreads + threadIdx.x;
+                    __builtin_nontemporal_store(kCast ? cast8(a[k], b[k]) : v[k], reinterpret_cast<u32x4*>(out) + g);
+                }
             }
+            for (uint64_t g = full + threadIdx.x; g < g8; g += kThreads)
+                __builtin_nontemporal_store(gather_group<kCast>(src, base, g), reinterpret_cast<u32x4*>(out) + g);
         } else {
             for (uint64_t j = threadIdx.x; j < row_len; j += kThreads) {
                 out[j] = kCast ? uint16_t(rne_bf16(__float_as_uint(static_cast<const float*>(src)[base + j])))
@@ -384,8 +430,14 @@ int launch_gather_rows(const void* src, const int64_t* ids, size_t ntok, size_t 
     uint64_t grid = ntok;
     if (max_workgroups > 0 && grid > uint64_t(max_workgroups)) grid = uint64_t(max_workgroups);
     if (grid > kMaxBlocks) grid = kMaxBlocks;
-    hipLaunchKernelGGL(gather_rows_kernel<kCast>, dim3(uint32_t(grid)), dim3(kThreads), 0, st, src, ids,
-                       uint64_t(ntok), uint64_t(row_len), uint64_t(nrows), dst, bad, vec);
+    // whole groups of 8 per lane and pass, 1 to 4
+    const uint64_t per_lane = (row_len / kGroup) / kThreads;
+    auto kernel = per_lane >= 4 ? gather_rows_kernel<kCast, 4>
+                : per_lane == 3 ? gather_rows_kernel<kCast, 3>
+                : per_lane == 2 ? gather_rows_kernel<kCast, 2>
+                                : gather_rows_kernel<kCast, 1>;
+    hipLaunchKernelGGL(kernel, dim3(uint32_t(grid)), dim3(kThreads), 0, st, src, ids, uint64_t(ntok),
+                       uint64_t(row_len), uint64_t(nrows), dst, bad, vec);
     return hip_status(hipGetLastError());
 }
 }  // namespace
@@ -441,10 +493,10 @@ int cast_launch(const float* src, uint16_t* dst, size_t n, hipStream_t st, hipEv
     const uint64_t done = n8 * kGroup;
     const bool tail = done < n;
     if (n8 > 0) {
-        const uint64_t blocks = ceil_div(n8, uint64_t(kThreads) * kCastUnroll);
+        const uint64_t blocks = ceil_div(n8, uint64_t(kCastThreads) * kCastUnroll);
         if (blocks > kMaxBlocks) return SF_EINVAL;
         hipExtLaunchKernelGGL(to_f16 ? cast_flat_f16_kernel : cast_flat_kernel, dim3(uint32_t(blocks)),
-                              dim3(kThreads), 0, st, start, tail ? nullptr : stop, 0, src, dst, n8);
+                              dim3(kCastThreads), 0, st, start, tail ? nullptr : stop, 0, src, dst, n8);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return int(e);
     }

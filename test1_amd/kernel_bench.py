@@ -8,7 +8,7 @@ Times, with HIP events on the stream each runs on:
             the reference point for hardware counters (FETCH_SIZE and
             WRITE_SIZE are scaled by what they read for it)
   pack_d2h  sf_pack_b16 of N/2 bf16 elements into pinned host memory with
-            the offload path's 8-workgroup grid (host link)
+            the offload path's 16-workgroup grid (host link)
   h2d       one DMA copy of N fp32 elements from pinned host memory
 Default N is one Llama-3-8B decoder layer (218,112,000 parameters).
 
@@ -77,7 +77,7 @@ def main(argv=None):
                    "algorithmic_bytes": 6 * n, "rotated_pairs": len(pairs)}
     ms = _time(lambda: cp_dst.copy_(cp_src), s, reps)
     res["copy"] = {"ms": ms, "GB/s": 8 * half / ms / 1e6, "bytes_read": 4 * half, "bytes_written": 4 * half}
-    ms = _time(lambda: kernels.pack_b16([g], host_g, s, max_workgroups=8), s, max(1, reps // 4))
+    ms = _time(lambda: kernels.pack_b16([g], host_g, s, max_workgroups=16), s, max(1, reps // 4))
     res["pack_d2h"] = {"ms": ms, "GB/s": 2 * half / ms / 1e6}
     ms = _time(lambda: kernels.memcpy_async(dev_w, host_w, s), s, max(1, reps // 4))
     res["h2d"] = {"ms": ms, "GB/s": 4 * n / ms / 1e6}

@@ -289,7 +289,7 @@ class SlidingCheckpoint(saved_tensors_hooks):
         stream: Optional[torch.cuda.Stream] = None,
         prefetch_ring: Optional[ActivationRing] = None,
         trace=None,
-        max_workgroups: int = 8,
+        max_workgroups: int = 16,
         prefetch_stream: Optional[torch.cuda.Stream] = None,
         pack_fence=None,
         spill: Optional[StorageSpill] = None,

@@ -273,11 +273,13 @@ def test_sdma_copy_d2h(dev):
     assert np.array_equal(host.view(torch.int16).numpy().view(np.uint16), exp)
 
 
-@pytest.mark.parametrize("row_len", [4096, 24, 13])
+@pytest.mark.parametrize("row_len", [4096, 5120, 8192, 8200, 24, 13])
 def test_gather_rows_from_pinned_host_table(dev, row_len):
     # fp32 rows read by the kernel from pinned host memory, rounded to bf16:
     # equal to the oracle cast of the same rows (vector path for row_len % 8
-    # == 0, scalar path otherwise), repeated ids included.
+    # == 0, scalar path otherwise), repeated ids included.  Row lengths cover
+    # 2 and 2.5 groups of 8 per lane, exactly one pass of 4 groups per lane
+    # (8192) and a second pass with one group for the first lane (8200).
     V, ntok = 257, 300
     table = pinned_empty((V, row_len), torch.float32)
     table.copy_(rand_f32(V * row_len, row_len).view(V, row_len))
@@ -291,11 +293,12 @@ def test_gather_rows_from_pinned_host_table(dev, row_len):
     assert int(bad.item()) == 0
 
 
-def test_gather_rows_b16_into_pinned_host_and_bad_ids(dev):
+@pytest.mark.parametrize("H", [128, 5120, 8200])
+def test_gather_rows_b16_into_pinned_host_and_bad_ids(dev, H):
     # 16-bit rows copied from device memory into pinned host memory by a
     # capped grid (the gradient-row offload); ids out of range give 0xFFFF
     # rows and raise the flag, in-range rows are unaffected.
-    V, H = 64, 128
+    V = 64
     table = torch.randn(V, H, device=dev).bfloat16()
     ids = torch.tensor([3, 0, 63, 64, -1, 3, 17], dtype=torch.int64, device=dev)
     out = pinned_empty((ids.numel(), H), torch.bfloat16)

@@ -30,6 +30,7 @@ from __future__ import annotations
 import argparse
 import itertools
 import json
+import math
 import os
 import sys
 import time
@@ -293,6 +294,8 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
     losses = [x.item() for x in losses]
+    if not all(math.isfinite(x) for x in losses):
+        log(f"[bench] WARNING: non-finite training losses {losses}: the step's results are wrong")
     if timeline:
         with open(timeline, "w") as f:
             for t, th, what, unit in rt.timeline:
@@ -382,7 +385,8 @@ def variant_summary(v: dict, h2d_format: str, d2h_engine: str) -> dict:
             "steps": v["steps"], "warmup": v["warmup"], "h2d_format": h2d_format,
             "resident_layers": v["resident_layers"], "d2h_engine": d2h_engine,
             "cast_frac": None if cast_gbs is None else cast_gbs / HBM_PEAK_GBS,
-            "host_link": link_stats(v, v["steps"]), "losses": v["losses"]}
+            "host_link": link_stats(v, v["steps"]), "losses": v["losses"],
+            "losses_finite": all(math.isfinite(x) for x in v["losses"])}
 
 
 def megatron_flops_per_step(w: dict) -> float:
@@ -805,6 +809,7 @@ def main():
         "storage": r["storage"],
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
         "losses": losses,
+        "losses_finite": all(math.isfinite(x) for x in losses),
         "variants": variants,
     }
     print(json.dumps(res), flush=True)

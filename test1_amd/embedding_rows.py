@@ -58,6 +58,26 @@ class RowSparseEmbedding:
         self._early: Optional[Dict[str, Any]] = None
         self._early_lock = threading.Lock()
 
+    def host_buffers_fit(self, ntok: int) -> bool:
+        """The pinned buffers of a batch of ``ntok`` tokens (gradient rows and
+        ids, lookup ids) exist and are large enough."""
+        return all(b is not None and b.shape[0] >= ntok
+                   for b in (self._rows_host, self._ids_host, self._ids_early_host))
+
+    def has_host_buffers(self) -> bool:
+        return any(b is not None for b in (self._rows_host, self._ids_host, self._ids_early_host))
+
+    def alloc_host_buffers(self, ntok: int) -> None:
+        """Pin the buffers of a batch of ``ntok`` tokens.  Called before a
+        step's first copy (``SlideFSDP.forward``), with nothing in flight that
+        reads or writes the buffers it replaces, so that no pinned memory is
+        allocated while copies run (the lookup and the backward allocate them
+        only if this was not called)."""
+        n = max(int(ntok), 1)
+        self._rows_host = pinned_empty((n, self._rows_shape[1]), torch.bfloat16)
+        self._ids_host = pinned_empty(n, torch.int64)
+        self._ids_early_host = pinned_empty(n, torch.int64)
+
     def _host_table(self) -> torch.Tensor:
         V, H = self._rows_shape
         src = self._cpu_params_bf16 if self._cpu_params_bf16 is not None else self._cpu_params_flat

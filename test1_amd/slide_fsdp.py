@@ -560,13 +560,22 @@ class SlideFSDP(nn.Module):
             self._ring_grow_pending = False
             self._drain()
             self._grow_grad_ring()
-        if self.config.ac_offload_mode == "cpu" and self.config.enable_activation_checkpoint:
-            if self.layer_tensors is None or self.layer_tensors[0][0].shape != (batch_size, seq_length, hidden_size):
-                if self.layer_tensors is not None:
-                    # the previous step's packs and prefetches may still be
-                    # reading or writing the slots about to be freed
-                    self._drain()
+        # Pinned buffers sized by the batch are allocated here, before the
+        # step's first copy; the ones they replace may still be read or
+        # written by the previous step's copies and updates, so those finish
+        # first.
+        act_alloc = (self.config.ac_offload_mode == "cpu" and self.config.enable_activation_checkpoint
+                     and (self.layer_tensors is None
+                          or self.layer_tensors[0][0].shape != (batch_size, seq_length, hidden_size)))
+        embed_rows = self.layer_states[0].row_sparse and not self.layer_states[0].host_buffers_fit(input_ids.numel())
+        if act_alloc or embed_rows:
+            if (act_alloc and self.layer_tensors is not None) or (
+                    embed_rows and self.layer_states[0].has_host_buffers()):
+                self._drain()
+            if act_alloc:
                 self._allocate_activation_tensors(batch_size, seq_length, hidden_size)
+            if embed_rows:
+                self.layer_states[0].alloc_host_buffers(input_ids.numel())
         self._act_ring.reset()
 
         embed_state = self.layer_states[0]

@@ -91,6 +91,7 @@ HIP_SIGNATURES = {
     "sf_dma_init": [_i],
     "sf_dma_set_engines": [ctypes.c_uint32],
     "sf_dma_get_engines": [ctypes.POINTER(ctypes.c_uint32)],
+    "sf_dma_set_avoid_held": [_i],
     "sf_dma_copy_d2h": [ctypes.POINTER(SfSeg), _i, ctypes.POINTER(ctypes.c_uint64), _i, ctypes.POINTER(_i)],
     "sf_dma_wait": [ctypes.POINTER(ctypes.c_uint64), _i, ctypes.POINTER(ctypes.c_uint64),
                     ctypes.POINTER(ctypes.c_uint64)],

@@ -21,6 +21,7 @@
 #include <chrono>
 #include <mutex>
 #include <thread>
+#include <unordered_map>
 
 #include "../../include/slidefsdp.h"
 
@@ -800,9 +801,40 @@ struct DmaAgents {
     bool ok = false;
     uint32_t engine_mask = 0;  // one SDMA engine bit; 0: runtime's choice
     uint64_t ts_freq = 0;      // HSA system timestamp ticks per second
+    bool avoid_held = true;    // route around engines another client holds
+    // Copies issued here and not yet released by sf_dma_wait: signal handle
+    // -> engine bit (0 for a runtime-chosen engine).
+    std::unordered_map<uint64_t, uint32_t> outstanding;
 };
 DmaAgents g_dma;
 std::mutex g_dma_mu;
+
+// Engines for the next device -> host copies.  The runtime reports an engine
+// as unavailable while any copy is pending on it: ours, or one of HIP's.  A
+// HIP copy ordered after an event that has not fired yet sits on its engine
+// until the event fires, and a copy of ours queued on that engine waits
+// behind it (measured: 190 ms behind one such H2D).  So an engine of the
+// preferred set that is busy while none of our copies is pending on it is
+// held by another client: use the free engines among the first four in its
+// place (engines 4 and up move host copies at a fraction of the rate).
+// Called with g_dma_mu held.
+uint32_t pick_engines_locked(uint32_t preferred, hsa_agent_t cpu, hsa_agent_t gpu) {
+    if (preferred == 0 || !g_dma.avoid_held) return preferred;
+    uint32_t avail = 0;
+    if (hsa_amd_memory_copy_engine_status(cpu, gpu, &avail) != HSA_STATUS_SUCCESS) return preferred;
+    uint32_t ours = 0;
+    for (const auto& kv : g_dma.outstanding)
+        if (hsa_signal_load_scacquire(hsa_signal_t{kv.first}) >= 1) ours |= kv.second;
+    const uint32_t held = ~avail & ~ours & 0xFFFFu;
+    if ((preferred & held) == 0) return preferred;
+    uint32_t use = preferred & ~held;
+    const int want = __builtin_popcount(preferred);
+    for (int e = 0; e < 4 && __builtin_popcount(use) < want; ++e) {
+        const uint32_t b = 1u << e;
+        if ((avail & b) && !(use & b)) use |= b;
+    }
+    return use != 0 ? use : preferred;
+}
 
 struct AgentScan {
     uint32_t want_bdf;
@@ -882,6 +914,13 @@ int sf_dma_set_engines(uint32_t engine_mask) {
     return SF_OK;
 }
 
+int sf_dma_set_avoid_held(int on) {
+    std::lock_guard<std::mutex> lk(g_dma_mu);
+    if (!g_dma.ok) return SF_EINVAL;
+    g_dma.avoid_held = on != 0;
+    return SF_OK;
+}
+
 int sf_dma_get_engines(uint32_t* engine_mask) {
     std::lock_guard<std::mutex> lk(g_dma_mu);
     if (!g_dma.ok || engine_mask == nullptr) return SF_EINVAL;
@@ -900,13 +939,13 @@ int sf_dma_copy_d2h(const sf_seg* segs, int nsegs, uint64_t* signals, int max_si
     {
         std::lock_guard<std::mutex> lk(g_dma_mu);
         if (!g_dma.ok) return SF_EINVAL;
-        mask = g_dma.engine_mask;
+        // Every segment is checked before the first copy is issued.
+        for (int i = 0; i < nsegs; ++i)
+            if (segs[i].n != 0 && (segs[i].src == 0 || segs[i].dst == 0)) return SF_EINVAL;
         cpu = g_dma.cpu;
         gpu = g_dma.gpu;
+        mask = pick_engines_locked(g_dma.engine_mask, cpu, gpu);
     }
-    // Every segment is checked before the first copy is issued.
-    for (int i = 0; i < nsegs; ++i)
-        if (segs[i].n != 0 && (segs[i].src == 0 || segs[i].dst == 0)) return SF_EINVAL;
     // Engines to spread over: the set bits of the engine mask, or one
     // runtime-chosen engine.
     uint32_t engines[16];
@@ -940,6 +979,10 @@ int sf_dma_copy_d2h(const sf_seg* segs, int nsegs, uint64_t* signals, int max_si
                 hsa_signal_destroy(sig);
                 return hsa_status_to_sf(st);
             }
+            {
+                std::lock_guard<std::mutex> lk(g_dma_mu);
+                g_dma.outstanding[sig.handle] = eng;
+            }
             signals[(*nsignals)++] = sig.handle;
         }
     }
@@ -965,6 +1008,11 @@ int sf_dma_wait(const uint64_t* signals, int nsignals, uint64_t* start_ns, uint6
                 if (tm.start < t0) t0 = tm.start;
                 if (tm.end > t1) t1 = tm.end;
             }
+        }
+        {
+            // forget the copy before its signal handle can be reused
+            std::lock_guard<std::mutex> lk(g_dma_mu);
+            g_dma.outstanding.erase(signals[i]);
         }
         hsa_status_t st = hsa_signal_destroy(sig);
         if (st != HSA_STATUS_SUCCESS && rc == SF_OK) rc = hsa_status_to_sf(st);

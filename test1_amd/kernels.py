@@ -343,6 +343,8 @@ def dma_init(device: Optional[torch.device] = None) -> None:
         for e in env.split(","):
             mask |= 1 << int(e)
         _native.check(_native.hip().sf_dma_set_engines(mask), "sf_dma_set_engines")
+    if os.environ.get("SF_DMA_AVOID_HELD", "1") == "0":
+        _native.check(_native.hip().sf_dma_set_avoid_held(0), "sf_dma_set_avoid_held")
     _dma_ready.add(idx)
 
 
@@ -351,6 +353,21 @@ def dma_engines() -> list:
     m = ctypes.c_uint32(0)
     _native.check(_native.hip().sf_dma_get_engines(ctypes.byref(m)), "sf_dma_get_engines")
     return [e for e in range(16) if m.value >> e & 1]
+
+
+def dma_set_engines(engines: Sequence[int]) -> None:
+    """Select the SDMA engines for device -> host copies ([] : runtime's choice)."""
+    mask = 0
+    for e in engines:
+        if not 0 <= int(e) < 16:
+            raise ValueError(f"SDMA engine {e} out of range 0..15")
+        mask |= 1 << int(e)
+    _native.check(_native.hip().sf_dma_set_engines(mask), "sf_dma_set_engines")
+
+
+def dma_set_avoid_held(on: bool) -> None:
+    """Route device -> host copies around engines another client holds (default on)."""
+    _native.check(_native.hip().sf_dma_set_avoid_held(1 if on else 0), "sf_dma_set_avoid_held")
 
 
 def dma_enable_timing(on: bool) -> None:

@@ -267,14 +267,16 @@ int sf_dma_init(int device);
 int sf_dma_set_engines(uint32_t engine_mask);
 int sf_dma_get_engines(uint32_t* engine_mask);
 
-/* Route around held engines (1, the default) or not (0).  When on, each
- * sf_dma_copy_d2h asks the runtime which engines are free; an engine of the
- * selected set that is busy while none of this library's copies is pending
- * on it is held by another client (a HIP copy ordered after an event that
- * has not fired holds its engine until then), and the copies go to free
- * engines among 0-3 in its place.  No reference counterpart (its D2H is a
- * torch copy on a stream, layer_state.py:367-393). */
-int sf_dma_set_avoid_held(int on);
+/* Route around held engines: mode 0 no, 1 onto free engines 0-3, 2 (the
+ * default) also onto free engines from 4 up when none of 0-3 is free.  Each
+ * sf_dma_copy_d2h then asks the runtime which engines are free; an engine
+ * of the selected set that is busy while none of this library's copies is
+ * pending on it is held by another client (a HIP copy ordered after an
+ * event that has not fired holds its engine until then), and the copies go
+ * to free engines in its place (engines from 4 up: twice as many, they are
+ * slower for host copies).  SF_EINVAL for another mode.  No reference
+ * counterpart (its D2H is a torch copy on a stream, layer_state.py:367-393). */
+int sf_dma_set_avoid_held(int mode);
 
 /* For each segment, copy segs[k].n BYTES from device address segs[k].src
  * to pinned host address segs[k].dst.  Segments of 4 MiB or more are split

@@ -801,7 +801,8 @@ struct DmaAgents {
     bool ok = false;
     uint32_t engine_mask = 0;  // one SDMA engine bit; 0: runtime's choice
     uint64_t ts_freq = 0;      // HSA system timestamp ticks per second
-    bool avoid_held = true;    // route around engines another client holds
+    int avoid_held = 2;        // route around engines another client holds:
+                               // 0 no, 1 onto free engines 0-3, 2 also 4 and up
     // Copies issued here and not yet released by sf_dma_wait: signal handle
     // -> engine bit (0 for a runtime-chosen engine).
     std::unordered_map<uint64_t, uint32_t> outstanding;
@@ -816,7 +817,10 @@ std::mutex g_dma_mu;
 // behind it (measured: 190 ms behind one such H2D).  So an engine of the
 // preferred set that is busy while none of our copies is pending on it is
 // held by another client: use the free engines among the first four in its
-// place (engines 4 and up move host copies at a fraction of the rate).
+// place.  Engines 4 and up move host copies at a fraction of the rate; they
+// are taken (twice as many) only when no engine among the first four can
+// be (measured in the fp32 Qwen2.5-14B step: gradient copies had waited
+// ~300 ms behind held engines, and the host AdamW with them).
 // Called with g_dma_mu held.
 uint32_t pick_engines_locked(uint32_t preferred, hsa_agent_t cpu, hsa_agent_t gpu) {
     if (preferred == 0 || !g_dma.avoid_held) return preferred;
@@ -832,6 +836,11 @@ uint32_t pick_engines_locked(uint32_t preferred, hsa_agent_t cpu, hsa_agent_t gp
     for (int e = 0; e < 4 && __builtin_popcount(use) < want; ++e) {
         const uint32_t b = 1u << e;
         if ((avail & b) && !(use & b)) use |= b;
+    }
+    if (use == 0 && g_dma.avoid_held >= 2) {
+        // every fast engine held: free slower ones, twice as many
+        for (int e = 4; e < 16 && __builtin_popcount(use) < 2 * want; ++e)
+            if (avail & (1u << e)) use |= 1u << e;
     }
     return use != 0 ? use : preferred;
 }
@@ -914,10 +923,11 @@ int sf_dma_set_engines(uint32_t engine_mask) {
     return SF_OK;
 }
 
-int sf_dma_set_avoid_held(int on) {
+int sf_dma_set_avoid_held(int mode) {
     std::lock_guard<std::mutex> lk(g_dma_mu);
     if (!g_dma.ok) return SF_EINVAL;
-    g_dma.avoid_held = on != 0;
+    if (mode < 0 || mode > 2) return SF_EINVAL;
+    g_dma.avoid_held = mode;
     return SF_OK;
 }
 

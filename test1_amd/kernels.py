@@ -343,8 +343,9 @@ def dma_init(device: Optional[torch.device] = None) -> None:
         for e in env.split(","):
             mask |= 1 << int(e)
         _native.check(_native.hip().sf_dma_set_engines(mask), "sf_dma_set_engines")
-    if os.environ.get("SF_DMA_AVOID_HELD", "1") == "0":
-        _native.check(_native.hip().sf_dma_set_avoid_held(0), "sf_dma_set_avoid_held")
+    mode = os.environ.get("SF_DMA_AVOID_HELD", "")
+    if mode not in ("", "1"):
+        _native.check(_native.hip().sf_dma_set_avoid_held(int(mode)), "sf_dma_set_avoid_held")
     _dma_ready.add(idx)
 
 
@@ -365,9 +366,11 @@ def dma_set_engines(engines: Sequence[int]) -> None:
     _native.check(_native.hip().sf_dma_set_engines(mask), "sf_dma_set_engines")
 
 
-def dma_set_avoid_held(on: bool) -> None:
-    """Route device -> host copies around engines another client holds (default on)."""
-    _native.check(_native.hip().sf_dma_set_avoid_held(1 if on else 0), "sf_dma_set_avoid_held")
+def dma_set_avoid_held(mode: int) -> None:
+    """Route device -> host copies around engines another client holds: 0 no,
+    1 onto free engines 0-3, 2 (default) also onto slower free engines from 4
+    up when none of 0-3 is free."""
+    _native.check(_native.hip().sf_dma_set_avoid_held(int(mode)), "sf_dma_set_avoid_held")
 
 
 def dma_enable_timing(on: bool) -> None:

@@ -589,7 +589,11 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
     def _dummy_dst(self) -> torch.Tensor:
         # Only used to drain a staging ticket after a failed acquire: casts
         # into a scratch buffer so the ring's slot events stay consistent.
-        return torch.empty(self.total_size, dtype=self.buffer_pool.dtype, device=self.runtime.device)
+        # Taken on the cast stream, which writes it, so that neither pending
+        # work of another stream on the block nor its release after the cast
+        # is left unordered.
+        with torch.cuda.stream(self.runtime.cast_stream):
+            return torch.empty(self.total_size, dtype=self.buffer_pool.dtype, device=self.runtime.device)
 
     def wait_for_h2d(self, timeout: Optional[float] = None) -> None:
         """Make the current stream wait for this unit's load (no host block).

@@ -17,6 +17,7 @@ pieces a unit's update and staging can be split into.
 from __future__ import annotations
 
 import bisect
+import contextlib
 import itertools
 import threading
 from collections import deque
@@ -149,10 +150,19 @@ class _SlotPool:
     """Device fp32 buffers of whole units, keyed by size and reused.  A
     buffer comes back with the event after which it may be overwritten.
     Allocation stops at ``cap_bytes`` or at the first out-of-memory error;
-    callers then stage through the ring."""
+    callers then stage through the ring.
 
-    def __init__(self, device: torch.device, cap_bytes: int):
+    New buffers are allocated with ``alloc_stream`` (the stream that copies
+    into them) current.  The caching allocator hands a stream the blocks last
+    freed on it, ordered only with that stream's own work: a buffer taken on
+    the compute stream (the update thread's current stream is the same
+    default stream) may be memory the backward has freed while its kernels
+    on it are still queued, and a copy on another stream would then overwrite
+    it under them."""
+
+    def __init__(self, device: torch.device, cap_bytes: int, alloc_stream: Optional[torch.cuda.Stream] = None):
         self.device = device
+        self.alloc_stream = alloc_stream
         self.cap_bytes = int(cap_bytes)
         self.bytes = 0
         self.disabled = False
@@ -174,7 +184,9 @@ class _SlotPool:
             if self.disabled or self.bytes + 4 * n > self.cap_bytes:
                 return None
             try:
-                t = torch.empty(n, dtype=torch.float32, device=self.device)
+                with (torch.cuda.stream(self.alloc_stream) if self.alloc_stream is not None
+                      else contextlib.nullcontext()):
+                    t = torch.empty(n, dtype=torch.float32, device=self.device)
             except torch.cuda.OutOfMemoryError:
                 self.disabled = True
                 return None
@@ -237,7 +249,7 @@ class H2DStager:
         self.last_cast_done: Optional[torch.cuda.Event] = None
         self._copies: deque = deque()   # completion events of issued copies, in stream order
         # Whole-unit device slots of ``copy_for_later`` and ``open_pieces``.
-        self.slots = _SlotPool(device, slot_cap_bytes)
+        self.slots = _SlotPool(device, slot_cap_bytes, alloc_stream=h2d_stream)
 
     def backlog(self) -> int:
         """Host-to-device copies issued and not yet complete."""

@@ -149,6 +149,36 @@ def test_param_streaming_llama3_8b_32_layers(dev):
     assert torch.equal(h.view(torch.int16), r.view(torch.int16))
 
 
+def test_stager_slots_are_taken_on_the_stream_that_copies_into_them(dev):
+    """Whole-unit slots of units staged after their update are allocated on
+    the H2D stream, which copies into them.  Taken on the compute stream, a
+    slot could be memory the backward has just freed while its kernels on it
+    are still queued, and the copy, on another stream, would overwrite it
+    under them (step-1 gradients of the Qwen2.5-14B-shaped step differed from
+    a non-offloaded run's from the middle of the backward down).  The slot's
+    cast is the oracle's."""
+    h2d, cast = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
+    stager = H2DStager(dev, 1 << 20, 3, h2d, cast, slot_cap_bytes=1 << 30)
+    # a block freed on the current stream that the slot would fit in
+    junk = torch.empty(1 << 23, dtype=torch.float32, device=dev)
+    del junk
+    n = 3_000_001
+    g = torch.Generator().manual_seed(11)
+    host = pinned_empty(n, torch.float32)
+    host.copy_(torch.randn(n, generator=g) * 0.02)
+    p = stager.copy_for_later(host, None)
+    assert p is not None
+    addr = p.slot.data_ptr()
+    seg = [sg for sg in torch.cuda.memory_snapshot()
+           if sg["address"] <= addr < sg["address"] + sg["total_size"]]
+    assert len(seg) == 1 and seg[0]["stream"] == h2d.cuda_stream, \
+        "slot not allocated on the stream that copies into it"
+    dst = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    stager.cast_pending(p, dst, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(dst), oracle.cast_f32_bf16(host.numpy()))
+
+
 def test_noop_sync_copies_are_bit_exact(dev):
     """The one-GPU transfer strategy (reference distributed_sync.py:324-354):
     ``gather_params_to_gpu`` copies a pinned bf16 layer into the device buffer

@@ -20,7 +20,7 @@ import torch.nn as nn
 from . import _native, kernels
 from .pinned import pinned_empty
 from .staging import _new_event
-from .update_executor import EARLY_UPDATE_PRIORITY, _LinkQuiet, _PolledInput
+from .update_executor import EARLY_UPDATE_PRIORITY, _LinkQuiet
 
 
 class RowSparseEmbedding:
@@ -285,11 +285,8 @@ class RowSparseEmbedding:
         self._bwd_compute_done = True
         # this step's early part (if any) now belongs to the late part
         early, self._early = self._early, None
-        ready = self._update_ready(done)
-        if not getattr(ready, "poll_interval", None):
-            ready = _PolledInput(ready)
         self._update_future = rt.update_executor.submit(rt.update_priority(self.layer_idx), self._do_update_rows,
-                                                        done, ntok, early, ready=ready)
+                                                        done, ntok, early, ready=self._update_ready(done))
 
     def _do_update_rows(self, d2h_done: torch.cuda.Event, ntok: int, early: Optional[Dict[str, Any]]) -> bool:
         rt = self.runtime

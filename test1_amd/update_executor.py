@@ -181,28 +181,6 @@ class _UpdateReady:
             self.grads_ready.synchronize()
 
 
-class _PolledInput:
-    """Readiness of an input that may land after those of tasks queued later:
-    the embedding's gradient rows.  Its update is queued when the backward's
-    hook for the lookup runs on the host, but the rows land only when the
-    device reaches the end of the backward; with a gradient slot ring the
-    decoders' updates are queued later (once a slot frees) and their inputs
-    land first.  ``poll_interval`` makes the executor keep picking among the
-    queued tasks instead of blocking on this one while it is the oldest."""
-
-    poll_interval = 1e-3
-    poll_fallback_s = 10.0
-
-    def __init__(self, ev):
-        self.ev = ev
-
-    def query(self) -> bool:
-        return self.ev.query()
-
-    def synchronize(self) -> None:
-        self.ev.synchronize()
-
-
 class _LinkQuiet:
     """Ready once ``first`` has completed and no host-to-device copy of a
     unit is queued.  For update work that may wait (the embedding's

@@ -107,28 +107,6 @@ def test_priority_update_executor_skips_tasks_whose_input_is_not_ready():
     ex.shutdown(wait=True)
 
 
-def test_priority_update_executor_picks_around_an_oldest_input_that_lands_late():
-    from test1_amd.update_executor import PriorityUpdateExecutor, _PolledInput
-
-    ex = PriorityUpdateExecutor("test-upd2b")
-    gate = threading.Event()
-    log = []
-    ex.submit(-1, gate.wait, 10)
-    # the oldest task's input (the embedding's gradient rows, queued first)
-    # lands after the inputs of tasks queued after it (decoder gradients
-    # copied once a ring slot freed): those run first, then the oldest
-    late, early = _FakeReady(log, "rows"), _FakeReady(log, "decoder")
-    f0 = ex.submit(0, log.append, 0, ready=_PolledInput(late))
-    f7 = ex.submit(7, log.append, 7, ready=early)
-    threading.Timer(0.05, lambda: setattr(early, "done", True)).start()
-    threading.Timer(0.3, lambda: setattr(late, "done", True)).start()
-    gate.set()
-    for f in (f0, f7):
-        f.result(timeout=10)
-    assert log == [7, 0]
-    ex.shutdown(wait=True)
-
-
 class _PolledReady:
     """Readiness the executor must poll (as a unit whose moments wait for a
     buffer that another queued unit's update frees)."""

@@ -67,14 +67,20 @@ def gpu_bf16_copy(model, dev, dtype=torch.bfloat16):
     return gm
 
 
-def reference_step(gm, ids, vocab, units):
+def reference_step(gm, ids, vocab, units, layer_inputs=None):
     """One forward/backward of the non-offloaded model with transformers' own
     decoder forward (causal mask, rotary) and per-layer recompute; returns the
-    loss and the bf16 gradients of ``units`` (host)."""
+    loss and the bf16 gradients of ``units`` (host).  A list passed as
+    ``layer_inputs`` receives each decoder layer's input hidden states (host)."""
     gm.gradient_checkpointing_enable(gradient_checkpointing_kwargs={"use_reentrant": False})
     gm.train()
     gm.zero_grad(set_to_none=True)
-    hidden = gm.model(input_ids=ids, use_cache=False).last_hidden_state
+    out = gm.model(input_ids=ids, use_cache=False, output_hidden_states=layer_inputs is not None)
+    if layer_inputs is not None:
+        n_dec = len(gm.model.layers)
+        layer_inputs.extend(h.detach().cpu() for h in out.hidden_states[:n_dec])
+    hidden = out.last_hidden_state
+    del out
     logits = gm.lm_head(hidden)
     del hidden
     loss = torch.nn.functional.cross_entropy(logits[..., :-1, :].reshape(-1, vocab), ids[..., 1:].reshape(-1))
@@ -83,6 +89,31 @@ def reference_step(gm, ids, vocab, units):
     ups = unit_params(gm)
     grads = {u: [p.grad.detach().cpu() for p in ups[u]] for u in units}
     return loss.item(), grads
+
+
+def check_checkpoint_slots(sf, layer_inputs):
+    """After a step, the pinned checkpoint slot of every offloaded decoder
+    layer holds that layer's input hidden states bit for bit (the forward is
+    the non-offloaded run's, so its inputs are ``layer_inputs``).  The last
+    decoder keeps its checkpoint on the device.  Returns the layers checked."""
+    checked, bad = [], []
+    for i, h in enumerate(layer_inputs[:-1]):
+        slot = sf.layer_tensors[i][0]
+        assert slot.shape == h.shape, f"decoder {i}: checkpoint slot of shape {tuple(slot.shape)}"
+        if not same_bits(slot, h):
+            bad.append(i)
+        checked.append(i)
+    if bad:
+        i = bad[0]
+        got, exp = u16(sf.layer_tensors[i][0]).reshape(-1), u16(layer_inputs[i]).reshape(-1)
+        diff = np.flatnonzero(got != exp)
+        stale = [j for j, h in enumerate(layer_inputs)
+                 if j != i and np.array_equal(got[diff], u16(h).reshape(-1)[diff])]
+        raise AssertionError(
+            f"checkpoint slots of decoders {bad} differ from the layers' inputs in the non-offloaded forward; "
+            f"decoder {i}: {diff.size} of {got.size} elements, flat [{diff[0]}, {diff[-1]}], "
+            f"zero there: {bool((got[diff] == 0).all())}, equal there to the inputs of decoders {stale}")
+    return checked
 
 
 class CapturedOracle:

@@ -9,7 +9,8 @@ frequencies (the reference model is built parameter by parameter on the GPU;
 * Step 1: the loss and the gradients of the first decoder and the output
   unit equal the non-offloaded run's bit for bit (same kernels on the same
   bits: offload, recompute from the offloaded checkpoints and the staged
-  weights change nothing).
+  weights change nothing), and every offloaded decoder's pinned checkpoint
+  slot holds that layer's input in the non-offloaded forward.
 * Loss: every step within 1e-2 relative (the returned loss, bf16 as the
   reference's).  The loss also recomputed in fp32 from the returned bf16
   logits, where the ten steps' drop is visible (a bf16 loss near 12.5 has a
@@ -35,8 +36,8 @@ import time
 import pytest
 import torch
 
-from fullsize import (CapturedOracle, check_masters, check_moments, check_packed_grads, check_staged,
-                      check_step1_against_reference, gpu_bf16_copy, say, timed, unit_params)
+from fullsize import (CapturedOracle, check_checkpoint_slots, check_masters, check_moments, check_packed_grads,
+                      check_staged, check_step1_against_reference, gpu_bf16_copy, say, timed, unit_params)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -57,17 +58,21 @@ def _fp32_loss(logits, ids, vocab):
 
 def _reference(model, batches, dev, vocab, units):
     """bf16 weights on the GPU, fp32 masters and AdamW moments in HBM.
-    Returns the bf16 losses, the fp32 losses and step 1's gradients of
-    ``units``."""
+    Returns the bf16 losses, the fp32 losses, step 1's gradients of
+    ``units`` and step 1's decoder layer inputs (host)."""
     gm = gpu_bf16_copy(model, dev)
     gparams = list(gm.parameters())
     masters = [p.detach().to(dev, torch.float32) for p in model.parameters()]
     opt = torch.optim.AdamW(masters, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
-    losses, losses32, grads = [], [], None
+    losses, losses32, grads, layer_inputs = [], [], None, None
     for k, ids in enumerate(batches[:STEPS]):
         ids = ids.to(dev)
         gm.zero_grad(set_to_none=True)
-        logits = gm.lm_head(gm.model(input_ids=ids).last_hidden_state)
+        out = gm.model(input_ids=ids, output_hidden_states=k == 0)
+        if k == 0:
+            layer_inputs = [h.detach().cpu() for h in out.hidden_states[:len(gm.model.layers)]]
+        logits = gm.lm_head(out.last_hidden_state)
+        del out
         loss = torch.nn.functional.cross_entropy(logits[..., :-1, :].reshape(-1, vocab), ids[..., 1:].reshape(-1))
         losses32.append(_fp32_loss(logits.detach(), ids, vocab))
         del logits
@@ -87,7 +92,7 @@ def _reference(model, batches, dev, vocab, units):
         say(f"[reference] step {k}: loss {losses[-1]:.5f} (fp32 {losses32[-1]:.6f})")
     del gm, masters, opt, gparams
     torch.cuda.empty_cache()
-    return losses, losses32, grads
+    return losses, losses32, grads, layer_inputs
 
 
 def test_llama31_8b_parity_10_steps(dev):
@@ -100,7 +105,7 @@ def test_llama31_8b_parity_10_steps(dev):
     units = (1, L + 1)
     model = timed("model built", bench.build_model, w)
     batches = _batches(w)
-    ref, ref32, ref_grads = timed("reference run", _reference, model, batches, dev, w["vocab"], units)
+    ref, ref32, ref_grads, layer_inputs = timed("reference run", _reference, model, batches, dev, w["vocab"], units)
 
     orc = CapturedOracle(model, units, LR, BETAS, EPS, WD)
     cfg = SlideFSDPConfig(device=dev, lr=LR, adam_betas=BETAS, adam_eps=EPS, weight_decay=WD,
@@ -125,6 +130,9 @@ def test_llama31_8b_parity_10_steps(dev):
             cap = sf.runtime.capture
             if k == 0:
                 assert got[0] == ref[0] and got32[0] == ref32[0], (got[0], ref[0], got32[0], ref32[0])
+                n = len(check_checkpoint_slots(sf, layer_inputs))
+                del layer_inputs
+                say(f"step 1: checkpoint slots of {n} decoders equal the non-offloaded forward's layer inputs")
                 check_step1_against_reference(cap, ref_grads, units)
                 del ref_grads
                 say(f"step 1: loss and gradients of units {units} equal the non-offloaded run's bit for bit")

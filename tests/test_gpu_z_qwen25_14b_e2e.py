@@ -8,7 +8,8 @@ first and last decoders and the output unit equal, bit for bit, those of a
 non-offloaded bf16 forward/backward of the same weights (transformers' own
 forward with per-layer recompute; same kernels on the same bits, so the
 offload, the recompute from offloaded checkpoints and the staged weights
-change nothing).  Steps 1-3: those units' packed host gradients equal their
+change nothing), and every offloaded decoder's pinned checkpoint slot holds
+that layer's input in the non-offloaded forward.  Steps 1-3: those units' packed host gradients equal their
 device gradients, every update is the oracle AdamW's bit for bit, and so are
 the moments; a forward after step 3 computes with the oracle's bf16 cast of
 the updated masters.
@@ -26,8 +27,8 @@ import time
 import pytest
 import torch
 
-from fullsize import (CapturedOracle, check_masters, check_moments, check_packed_grads, check_staged,
-                      check_step1_against_reference, gpu_bf16_copy, reference_step, say, timed)
+from fullsize import (CapturedOracle, check_checkpoint_slots, check_masters, check_moments, check_packed_grads,
+                      check_staged, check_step1_against_reference, gpu_bf16_copy, reference_step, say, timed)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -50,8 +51,12 @@ def test_qwen25_14b_step_against_reference_and_oracle(dev):
     g = torch.Generator().manual_seed(7)
     batches = [torch.randint(0, w["vocab"], (w["batch"], w["seq"]), generator=g) for _ in range(STEPS + 1)]
 
+    from test1_amd.pinned import pinned_bytes_live
+    say(f"pinned memory live at the start: {pinned_bytes_live() / 2**30:.1f} GiB")
     gm = timed("bf16 copy on the GPU", gpu_bf16_copy, model, dev)
-    ref_loss, ref_grads = timed("reference step", reference_step, gm, batches[0].to(dev), w["vocab"], units)
+    layer_inputs = []
+    ref_loss, ref_grads = timed("reference step", reference_step, gm, batches[0].to(dev), w["vocab"], units,
+                                layer_inputs)
     del gm
     gc.collect()
     torch.cuda.empty_cache()
@@ -61,6 +66,7 @@ def test_qwen25_14b_step_against_reference_and_oracle(dev):
     cfg = SlideFSDPConfig(device=dev, lr=LR, adam_betas=BETAS, adam_eps=EPS, weight_decay=WD,
                           attention_implementation="sdpa")
     sf = timed("SlideFSDP set up", SlideFSDP, model, cfg, wait_timeout=600)
+    say(f"pinned memory live after set-up: {pinned_bytes_live() / 2**30:.1f} GiB")
     ring = sf.runtime.grad_ring
     say(f"gradient slots: {type(ring).__name__}"
         + (f", own slots for units {sorted(ring.big)}, ring of {ring.depth}" if isinstance(ring, GradSlotRing) else ""))
@@ -77,6 +83,9 @@ def test_qwen25_14b_step_against_reference_and_oracle(dev):
             assert sorted(u for u in cap if isinstance(u, int)) == sorted(units)
             if k == 0:
                 assert loss == ref_loss, (loss, ref_loss)
+                n = len(check_checkpoint_slots(sf, layer_inputs))
+                del layer_inputs
+                say(f"step 1: checkpoint slots of {n} decoders equal the non-offloaded forward's layer inputs")
                 check_step1_against_reference(cap, ref_grads, units)
                 del ref_grads
                 say(f"step 1: loss and gradients of units {units} equal the non-offloaded run's bit for bit")

@@ -295,6 +295,7 @@ class SlidingCheckpoint(saved_tensors_hooks):
         spill: Optional[StorageSpill] = None,
         link_timing: Optional[dict] = None,
         on_prefetch_ready=None,
+        before_pin=None,
     ):
         if gds_offload:
             if file_paths is None:
@@ -335,6 +336,11 @@ class SlidingCheckpoint(saved_tensors_hooks):
         # layer's prefetched checkpoint (the recompute starts after it).
         self.link_timing = link_timing
         self.on_prefetch_ready = on_prefetch_ready
+        # Optional callable run before a pinned slot is allocated inside the
+        # forward (the first step, or a new batch shape): SlideFSDP drains its
+        # copies there, since pinning host memory near the driver's limit
+        # while copies into pinned memory ran has left wrong results.
+        self.before_pin = before_pin
 
         def pack_hook(tensor: torch.Tensor) -> Tuple[torch.device, Any]:
             if tensor.size() == torch.Size([0]):
@@ -358,6 +364,8 @@ class SlidingCheckpoint(saved_tensors_hooks):
                 if slot is None or slot.shape != tensor.shape or slot.dtype != tensor.dtype:
                     # First use of this slot (the mask slot is created on demand)
                     # or a new batch shape: (re)allocate it, pinned and exact-size.
+                    if self.before_pin is not None:
+                        self.before_pin()
                     slot = pinned_empty(tensor.shape, tensor.dtype)
                     slots[self.pack_counter] = slot
             cur = torch.cuda.current_stream()

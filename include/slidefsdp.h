@@ -278,6 +278,12 @@ int sf_dma_get_engines(uint32_t* engine_mask);
  * counterpart (its D2H is a torch copy on a stream, layer_state.py:367-393). */
 int sf_dma_set_avoid_held(int mode);
 
+/* The engine choice of sf_dma_copy_d2h as a pure function: from the
+ * selected engines `preferred`, the runtime's free engines `avail` and the
+ * engines with copies of this library pending `ours`, the engines to use
+ * under `mode` (see sf_dma_set_avoid_held).  No GPU access; for tests. */
+uint32_t sf_dma_choose_engines(uint32_t preferred, uint32_t avail, uint32_t ours, int mode);
+
 /* For each segment, copy segs[k].n BYTES from device address segs[k].src
  * to pinned host address segs[k].dst.  Segments of 4 MiB or more are split
  * evenly over the selected engines, others go round-robin.  One completion

@@ -64,7 +64,8 @@ _sz = ctypes.c_size_t
 _i = ctypes.c_int
 _f = ctypes.c_float
 
-# name -> (argtypes) for every entry point; restype is int throughout.
+# name -> (argtypes) for every entry point; restype is int unless listed in
+# _RESTYPES.
 HIP_SIGNATURES = {
     "sf_error_string": [_i],
     "sf_abi_version": [],
@@ -92,6 +93,7 @@ HIP_SIGNATURES = {
     "sf_dma_set_engines": [ctypes.c_uint32],
     "sf_dma_get_engines": [ctypes.POINTER(ctypes.c_uint32)],
     "sf_dma_set_avoid_held": [_i],
+    "sf_dma_choose_engines": [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _i],
     "sf_dma_copy_d2h": [ctypes.POINTER(SfSeg), _i, ctypes.POINTER(ctypes.c_uint64), _i, ctypes.POINTER(_i)],
     "sf_dma_wait": [ctypes.POINTER(ctypes.c_uint64), _i, ctypes.POINTER(ctypes.c_uint64),
                     ctypes.POINTER(ctypes.c_uint64)],
@@ -131,6 +133,8 @@ _lock = threading.Lock()
 _hip = None
 _cpu = None
 
+_RESTYPES = {"sf_error_string": ctypes.c_char_p, "sf_dma_choose_engines": ctypes.c_uint32}
+
 
 def _bind(path: str, sigs: dict) -> ctypes.CDLL:
     if not os.path.exists(path):
@@ -142,7 +146,7 @@ def _bind(path: str, sigs: dict) -> ctypes.CDLL:
     for name, args in sigs.items():
         fn = getattr(lib, name)
         fn.argtypes = args
-        fn.restype = ctypes.c_char_p if name == "sf_error_string" else ctypes.c_int
+        fn.restype = _RESTYPES.get(name, ctypes.c_int)
     return lib
 
 

@@ -810,41 +810,6 @@ struct DmaAgents {
 DmaAgents g_dma;
 std::mutex g_dma_mu;
 
-// Engines for the next device -> host copies.  The runtime reports an engine
-// as unavailable while any copy is pending on it: ours, or one of HIP's.  A
-// HIP copy ordered after an event that has not fired yet sits on its engine
-// until the event fires, and a copy of ours queued on that engine waits
-// behind it (measured: 190 ms behind one such H2D).  So an engine of the
-// preferred set that is busy while none of our copies is pending on it is
-// held by another client: use the free engines among the first four in its
-// place.  Engines 4 and up move host copies at a fraction of the rate; they
-// are taken (twice as many) only when no engine among the first four can
-// be (measured in the fp32 Qwen2.5-14B step: gradient copies had waited
-// ~300 ms behind held engines, and the host AdamW with them).
-// Called with g_dma_mu held.
-uint32_t pick_engines_locked(uint32_t preferred, hsa_agent_t cpu, hsa_agent_t gpu) {
-    if (preferred == 0 || !g_dma.avoid_held) return preferred;
-    uint32_t avail = 0;
-    if (hsa_amd_memory_copy_engine_status(cpu, gpu, &avail) != HSA_STATUS_SUCCESS) return preferred;
-    uint32_t ours = 0;
-    for (const auto& kv : g_dma.outstanding)
-        if (hsa_signal_load_scacquire(hsa_signal_t{kv.first}) >= 1) ours |= kv.second;
-    const uint32_t held = ~avail & ~ours & 0xFFFFu;
-    if ((preferred & held) == 0) return preferred;
-    uint32_t use = preferred & ~held;
-    const int want = __builtin_popcount(preferred);
-    for (int e = 0; e < 4 && __builtin_popcount(use) < want; ++e) {
-        const uint32_t b = 1u << e;
-        if ((avail & b) && !(use & b)) use |= b;
-    }
-    if (use == 0 && g_dma.avoid_held >= 2) {
-        // every fast engine held: free slower ones, twice as many
-        for (int e = 4; e < 16 && __builtin_popcount(use) < 2 * want; ++e)
-            if (avail & (1u << e)) use |= 1u << e;
-    }
-    return use != 0 ? use : preferred;
-}
-
 struct AgentScan {
     uint32_t want_bdf;
     hsa_agent_t gpu{0};
@@ -868,6 +833,51 @@ hsa_status_t scan_agent(hsa_agent_t a, void* data) {
 }
 
 int hsa_status_to_sf(hsa_status_t s) { return s == HSA_STATUS_SUCCESS ? SF_OK : SF_EDMA_BASE + int(s & 0xFFF); }
+}  // namespace
+
+// The runtime reports an engine as unavailable while any copy is pending on
+// it: ours, or one of HIP's.  A HIP copy ordered after an event that has not
+// fired yet sits on its engine until the event fires, and a copy of ours
+// queued on that engine waits behind it (measured: 190 ms behind one such
+// H2D).  So an engine of the preferred set that is busy while none of our
+// copies is pending on it is held by another client: use the free engines
+// among the first four in its place.  Engines 4 and up move host copies at a
+// fraction of the rate; mode 2 takes them (twice as many) only when no
+// engine among the first four can be had (measured in the fp32 Qwen2.5-14B
+// step: gradient copies had waited ~300 ms behind held engines, and the host
+// AdamW with them).  An engine that holds a copy of ours counts as ours even
+// if another client's copy waits behind it; that client's copy then blocks
+// only what is queued after it.
+uint32_t sf_dma_choose_engines(uint32_t preferred, uint32_t avail, uint32_t ours, int mode) {
+    preferred &= 0xFFFFu;
+    if (preferred == 0 || mode <= 0) return preferred;
+    const uint32_t held = ~avail & ~ours & 0xFFFFu;
+    if ((preferred & held) == 0) return preferred;
+    uint32_t use = preferred & ~held;
+    const int want = __builtin_popcount(preferred);
+    for (int e = 0; e < 4 && __builtin_popcount(use) < want; ++e) {
+        const uint32_t b = 1u << e;
+        if ((avail & b) && !(use & b)) use |= b;
+    }
+    if (use == 0 && mode >= 2) {
+        for (int e = 4; e < 16 && __builtin_popcount(use) < 2 * want; ++e)
+            if (avail & (1u << e)) use |= 1u << e;
+    }
+    return use != 0 ? use : preferred;
+}
+
+namespace {
+// Engines for the next device -> host copies, from the runtime's engine
+// status and this library's pending copies.  Called with g_dma_mu held.
+uint32_t pick_engines_locked(uint32_t preferred, hsa_agent_t cpu, hsa_agent_t gpu) {
+    if (preferred == 0 || g_dma.avoid_held <= 0) return preferred;
+    uint32_t avail = 0;
+    if (hsa_amd_memory_copy_engine_status(cpu, gpu, &avail) != HSA_STATUS_SUCCESS) return preferred;
+    uint32_t ours = 0;
+    for (const auto& kv : g_dma.outstanding)
+        if (hsa_signal_load_scacquire(hsa_signal_t{kv.first}) >= 1) ours |= kv.second;
+    return sf_dma_choose_engines(preferred, avail, ours, g_dma.avoid_held);
+}
 }  // namespace
 
 int sf_dma_init(int device) {

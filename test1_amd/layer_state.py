@@ -171,6 +171,9 @@ class StreamingRuntime:
         # models capture a few units instead of copying every one.
         self.capture: Optional[dict] = None
         self.capture_units: Optional[set] = None
+        # Test hook: when a dict, device copies of the checkpoint tensors each
+        # recompute is given, {(decoder index, tensor index): tensor}.
+        self.capture_served: Optional[dict] = None
         self._held: List[Any] = []
         # Optional measurement: when a dict (``enable_link_timing``), timing
         # events of the units' compute on the compute stream and of the host

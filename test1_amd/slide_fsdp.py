@@ -644,7 +644,8 @@ class SlideFSDP(nn.Module):
                                        pack_fence=self.runtime.stager.fence_after_casts,
                                        link_timing=self.runtime.link_timing,
                                        on_prefetch_ready=self._reopen_compute,
-                                       before_pin=self._drain):
+                                       before_pin=self._drain,
+                                       served=self.runtime.capture_served):
                     hidden_states = checkpoint(_layer_forward, hidden_states, causal_mask, self.position_embeddings,
                                                layer_state.layer, **ckpt_kw)
             else:

@@ -296,6 +296,7 @@ class SlidingCheckpoint(saved_tensors_hooks):
         link_timing: Optional[dict] = None,
         on_prefetch_ready=None,
         before_pin=None,
+        served=None,
     ):
         if gds_offload:
             if file_paths is None:
@@ -341,6 +342,10 @@ class SlidingCheckpoint(saved_tensors_hooks):
         # copies there, since pinning host memory near the driver's limit
         # while copies into pinned memory ran has left wrong results.
         self.before_pin = before_pin
+        # Optional dict: (decoder index, tensor index) -> a device copy of each
+        # checkpoint tensor the recompute is given, taken on its stream after
+        # the prefetch wait (what the recompute reads); for checking only.
+        self.served = served
 
         def pack_hook(tensor: torch.Tensor) -> Tuple[torch.device, Any]:
             if tensor.size() == torch.Size([0]):
@@ -461,6 +466,7 @@ class SlidingCheckpoint(saved_tensors_hooks):
                     if self._trace is not None:
                         self._trace("act_h2d", nxt + 1)
             if self.is_last_layer:
+                self._record_served(tensor)
                 self.unpack_counter += 1
                 return tensor
             if not self.fifo:
@@ -477,6 +483,7 @@ class SlidingCheckpoint(saved_tensors_hooks):
                 if self.on_prefetch_ready is not None:
                     self.on_prefetch_ready()
             result = bufs[self.unpack_counter]
+            self._record_served(result)
             self.unpack_counter += 1
             # Pop once every prefetched tensor of this layer has been served.
             # (The reference pops after the first tensor when no_mask is set,
@@ -487,6 +494,10 @@ class SlidingCheckpoint(saved_tensors_hooks):
             return result
 
         super().__init__(pack_hook, unpack_hook)
+
+    def _record_served(self, t: torch.Tensor) -> None:
+        if self.served is not None:
+            self.served[(self.layer_idx, self.unpack_counter)] = t.detach().clone()
 
     def _slots_used(self, layer: int) -> int:
         """Number of tensors layer ``layer`` packed in this step's forward."""

@@ -91,6 +91,33 @@ def reference_step(gm, ids, vocab, units, layer_inputs=None):
     return loss.item(), grads
 
 
+def check_served_checkpoints(served, layer_inputs):
+    """Each decoder layer's recompute was given its input hidden states of
+    the non-offloaded forward, bit for bit (``served`` is the runtime's
+    ``capture_served`` after a step: the first tensor each layer's recompute
+    received, copied on its stream after the prefetch wait).  Returns the
+    layers checked."""
+    checked, bad = [], []
+    for i, h in enumerate(layer_inputs):
+        got = served.get((i, 0))
+        assert got is not None, f"decoder {i}: nothing served to its recompute"
+        assert tuple(got.shape) == tuple(h.shape), f"decoder {i}: served {tuple(got.shape)}"
+        if not same_bits(got, h):
+            bad.append(i)
+        checked.append(i)
+    if bad:
+        i = bad[0]
+        got, exp = u16(served[(i, 0)]).reshape(-1), u16(layer_inputs[i]).reshape(-1)
+        diff = np.flatnonzero(got != exp)
+        stale = [j for j, h in enumerate(layer_inputs)
+                 if j != i and np.array_equal(got[diff], u16(h).reshape(-1)[diff])]
+        raise AssertionError(
+            f"the recompute of decoders {bad} was given other inputs than the non-offloaded forward's; "
+            f"decoder {i}: {diff.size} of {got.size} elements, flat [{diff[0]}, {diff[-1]}], "
+            f"zero there: {bool((got[diff] == 0).all())}, equal there to the inputs of decoders {stale}")
+    return checked
+
+
 def check_checkpoint_slots(sf, layer_inputs):
     """After a step, the pinned checkpoint slot of every offloaded decoder
     layer holds that layer's input hidden states bit for bit (the forward is

@@ -36,7 +36,7 @@ import time
 import pytest
 import torch
 
-from fullsize import (CapturedOracle, check_checkpoint_slots, check_masters, check_moments, check_packed_grads,
+from fullsize import (CapturedOracle, check_checkpoint_slots, check_served_checkpoints, check_masters, check_moments, check_packed_grads,
                       check_staged, check_step1_against_reference, gpu_bf16_copy, say, timed, unit_params)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -118,6 +118,7 @@ def test_llama31_8b_parity_10_steps(dev):
             ids = ids.to(dev)
             checked = k < CHECKED_STEPS
             sf.runtime.capture = {} if checked else None
+            sf.runtime.capture_served = {} if k == 0 else None
             t = time.time()
             out = sf(input_ids=ids, labels=ids)
             got.append(out.loss.item())
@@ -131,8 +132,11 @@ def test_llama31_8b_parity_10_steps(dev):
             if k == 0:
                 assert got[0] == ref[0] and got32[0] == ref32[0], (got[0], ref[0], got32[0], ref32[0])
                 n = len(check_checkpoint_slots(sf, layer_inputs))
-                del layer_inputs
                 say(f"step 1: checkpoint slots of {n} decoders equal the non-offloaded forward's layer inputs")
+                served, sf.runtime.capture_served = sf.runtime.capture_served, None
+                n = len(check_served_checkpoints(served, layer_inputs))
+                del served, layer_inputs
+                say(f"step 1: the recomputes of {n} decoders were given the non-offloaded forward's layer inputs")
                 check_step1_against_reference(cap, ref_grads, units)
                 del ref_grads
                 say(f"step 1: loss and gradients of units {units} equal the non-offloaded run's bit for bit")

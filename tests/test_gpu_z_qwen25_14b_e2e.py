@@ -27,7 +27,7 @@ import time
 import pytest
 import torch
 
-from fullsize import (CapturedOracle, check_checkpoint_slots, check_masters, check_moments, check_packed_grads,
+from fullsize import (CapturedOracle, check_checkpoint_slots, check_served_checkpoints, check_masters, check_moments, check_packed_grads,
                       check_staged, check_step1_against_reference, gpu_bf16_copy, reference_step, say, timed)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -74,6 +74,7 @@ def test_qwen25_14b_step_against_reference_and_oracle(dev):
     try:
         for k in range(STEPS):
             sf.runtime.capture = {}
+            sf.runtime.capture_served = {} if k == 0 else None
             ids = batches[k].to(dev)
             t = time.time()
             loss = sf(input_ids=ids, labels=ids).loss.item()
@@ -84,8 +85,11 @@ def test_qwen25_14b_step_against_reference_and_oracle(dev):
             if k == 0:
                 assert loss == ref_loss, (loss, ref_loss)
                 n = len(check_checkpoint_slots(sf, layer_inputs))
-                del layer_inputs
                 say(f"step 1: checkpoint slots of {n} decoders equal the non-offloaded forward's layer inputs")
+                served, sf.runtime.capture_served = sf.runtime.capture_served, None
+                n = len(check_served_checkpoints(served, layer_inputs))
+                del served, layer_inputs
+                say(f"step 1: the recomputes of {n} decoders were given the non-offloaded forward's layer inputs")
                 check_step1_against_reference(cap, ref_grads, units)
                 del ref_grads
                 say(f"step 1: loss and gradients of units {units} equal the non-offloaded run's bit for bit")

@@ -4,7 +4,7 @@
 a non-offloaded bf16 run and the oracle (reference slide_fsdp.py:507-640).
 
 Step 1: the loss and the gradients SlideFSDP offloads for the embedding, the
-first and last decoders and the output unit equal, bit for bit, those of a
+first, two middle and last decoders and the output unit equal, bit for bit, those of a
 non-offloaded bf16 forward/backward of the same weights (transformers' own
 forward with per-layer recompute; same kernels on the same bits, so the
 offload, the recompute from offloaded checkpoints and the staged weights
@@ -46,7 +46,7 @@ def test_qwen25_14b_step_against_reference_and_oracle(dev):
 
     w = dict(bench.WORKLOADS["qwen2.5-14b"])
     L = w["layers"]
-    units = (0, 1, L, L + 1)
+    units = (0, 1, L // 3, 2 * L // 3, L, L + 1)
     model = timed("model built", bench.build_model, w)
     g = torch.Generator().manual_seed(7)
     batches = [torch.randint(0, w["vocab"], (w["batch"], w["seq"]), generator=g) for _ in range(STEPS + 1)]

@@ -516,8 +516,20 @@ class SlideFSDP(nn.Module):
         if idx - 1 >= 0:
             self.layer_states[idx - 1].to_device_async(is_backward=True)
         layer_state.wait_for_h2d()
+        self._record_weights("weights_start", layer_state)
         if idx > 0:   # the embedding's backward (a gradient scatter) is not timed
             self.runtime.compute_mark(True)
+
+    def _record_weights(self, what: str, layer_state: LayerRuntimeState) -> None:
+        """Test hook (``runtime.capture_served``): a checksum of the unit's
+        device weights, taken on the compute stream (the sum of their 16-bit
+        words)."""
+        served = self.runtime.capture_served
+        unit = layer_state._current_gpu_cache
+        if served is None or unit is None:
+            return
+        served[(what, layer_state.layer_idx)] = unit["param"][:layer_state.total_size].view(torch.int16).sum(
+            dtype=torch.int64)
 
     def _on_post_backward(self, layer_state: LayerRuntimeState, idx: int) -> None:
         """After a unit's last gradient: pack, offload and queue the update
@@ -527,6 +539,7 @@ class SlideFSDP(nn.Module):
                 return
             layer_state._post_called = True
             layer_state._bwd_armed = False
+        self._record_weights("weights_end", layer_state)
         layer_state.to_offload_async(is_backward=True)
 
     def _finish_backward(self) -> None:

@@ -123,6 +123,45 @@ def check_served_checkpoints(served, layer_inputs):
     return checked
 
 
+def unit_weight_sums(gm):
+    """Per unit, the sum of the 16-bit words of its bf16 weights (the
+    checksum the runtime records with ``capture_served``)."""
+    return [int(sum(int(p.detach().view(torch.int16).sum(dtype=torch.int64)) for p in ps))
+            for ps in unit_params(gm)]
+
+
+def check_backward_weights(served, sums, units):
+    """Each unit's device weights at the start and at the end of its
+    backward have the checksum of its bf16 weights in the non-offloaded run
+    (step 1: no update has reached them yet).  Returns the units checked."""
+    bad = []
+    for u in units:
+        for what in ("weights_start", "weights_end"):
+            got = served.get((what, u))
+            assert got is not None, f"unit {u}: no {what} checksum"
+            if int(got) != sums[u]:
+                bad.append(f"unit {u} {what}")
+    assert not bad, "device weights read by the backward differ from the forward's: " + ", ".join(bad)
+    return list(units)
+
+
+def _bits(t):
+    return t.detach().contiguous().view(-1).view(torch.uint8)
+
+
+def check_served_side_inputs(served, n_dec):
+    """The checkpoint tensors after the hidden states (rotary tables, mask)
+    that each decoder's recompute was given equal those of the last decoder,
+    which keeps the forward's own device tensors.  Returns their number."""
+    last, k = n_dec - 1, 1
+    while (last, k) in served:
+        ref = _bits(served[(last, k)])
+        bad = [i for i in range(n_dec) if not torch.equal(_bits(served[(i, k)]), ref)]
+        assert not bad, f"checkpoint tensor {k} given to the recompute of decoders {bad} differs from the forward's"
+        k += 1
+    return k - 1
+
+
 def check_checkpoint_slots(sf, layer_inputs):
     """After a step, the pinned checkpoint slot of every offloaded decoder
     layer holds that layer's input hidden states bit for bit (the forward is

@@ -36,7 +36,8 @@ import time
 import pytest
 import torch
 
-from fullsize import (CapturedOracle, check_checkpoint_slots, check_served_checkpoints, check_masters, check_moments, check_packed_grads,
+from fullsize import (CapturedOracle, check_backward_weights, check_checkpoint_slots, check_served_checkpoints,
+                      check_served_side_inputs, unit_weight_sums, check_masters, check_moments, check_packed_grads,
                       check_staged, check_step1_against_reference, gpu_bf16_copy, say, timed, unit_params)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -61,6 +62,7 @@ def _reference(model, batches, dev, vocab, units):
     Returns the bf16 losses, the fp32 losses, step 1's gradients of
     ``units`` and step 1's decoder layer inputs (host)."""
     gm = gpu_bf16_copy(model, dev)
+    sums = unit_weight_sums(gm)
     gparams = list(gm.parameters())
     masters = [p.detach().to(dev, torch.float32) for p in model.parameters()]
     opt = torch.optim.AdamW(masters, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
@@ -92,7 +94,7 @@ def _reference(model, batches, dev, vocab, units):
         say(f"[reference] step {k}: loss {losses[-1]:.5f} (fp32 {losses32[-1]:.6f})")
     del gm, masters, opt, gparams
     torch.cuda.empty_cache()
-    return losses, losses32, grads, layer_inputs
+    return losses, losses32, grads, layer_inputs, sums
 
 
 def test_llama31_8b_parity_10_steps(dev):
@@ -105,7 +107,8 @@ def test_llama31_8b_parity_10_steps(dev):
     units = (1, L + 1)
     model = timed("model built", bench.build_model, w)
     batches = _batches(w)
-    ref, ref32, ref_grads, layer_inputs = timed("reference run", _reference, model, batches, dev, w["vocab"], units)
+    ref, ref32, ref_grads, layer_inputs, sums = timed("reference run", _reference, model, batches, dev, w["vocab"],
+                                                      units)
 
     orc = CapturedOracle(model, units, LR, BETAS, EPS, WD)
     cfg = SlideFSDPConfig(device=dev, lr=LR, adam_betas=BETAS, adam_eps=EPS, weight_decay=WD,
@@ -135,8 +138,12 @@ def test_llama31_8b_parity_10_steps(dev):
                 say(f"step 1: checkpoint slots of {n} decoders equal the non-offloaded forward's layer inputs")
                 served, sf.runtime.capture_served = sf.runtime.capture_served, None
                 n = len(check_served_checkpoints(served, layer_inputs))
+                n_side = check_served_side_inputs(served, L)
+                n_units = len(check_backward_weights(served, sums, range(1, L + 2)))
                 del served, layer_inputs
-                say(f"step 1: the recomputes of {n} decoders were given the non-offloaded forward's layer inputs")
+                say(f"step 1: the recomputes of {n} decoders were given the non-offloaded forward's layer inputs "
+                    f"and {n_side} more tensors of the forward's; the backward of {n_units} units read the forward's "
+                    f"weights")
                 check_step1_against_reference(cap, ref_grads, units)
                 del ref_grads
                 say(f"step 1: loss and gradients of units {units} equal the non-offloaded run's bit for bit")

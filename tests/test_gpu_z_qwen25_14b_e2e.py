@@ -27,7 +27,8 @@ import time
 import pytest
 import torch
 
-from fullsize import (CapturedOracle, check_checkpoint_slots, check_served_checkpoints, check_masters, check_moments, check_packed_grads,
+from fullsize import (CapturedOracle, check_backward_weights, check_checkpoint_slots, check_served_checkpoints,
+                      check_served_side_inputs, unit_weight_sums, check_masters, check_moments, check_packed_grads,
                       check_staged, check_step1_against_reference, gpu_bf16_copy, reference_step, say, timed)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -57,6 +58,7 @@ def test_qwen25_14b_step_against_reference_and_oracle(dev):
     layer_inputs = []
     ref_loss, ref_grads = timed("reference step", reference_step, gm, batches[0].to(dev), w["vocab"], units,
                                 layer_inputs)
+    sums = unit_weight_sums(gm)
     del gm
     gc.collect()
     torch.cuda.empty_cache()
@@ -88,8 +90,12 @@ def test_qwen25_14b_step_against_reference_and_oracle(dev):
                 say(f"step 1: checkpoint slots of {n} decoders equal the non-offloaded forward's layer inputs")
                 served, sf.runtime.capture_served = sf.runtime.capture_served, None
                 n = len(check_served_checkpoints(served, layer_inputs))
+                n_side = check_served_side_inputs(served, L)
+                n_units = len(check_backward_weights(served, sums, range(1, L + 2)))
                 del served, layer_inputs
-                say(f"step 1: the recomputes of {n} decoders were given the non-offloaded forward's layer inputs")
+                say(f"step 1: the recomputes of {n} decoders were given the non-offloaded forward's layer inputs "
+                    f"and {n_side} more tensors of the forward's; the backward of {n_units} units read the forward's "
+                    f"weights")
                 check_step1_against_reference(cap, ref_grads, units)
                 del ref_grads
                 say(f"step 1: loss and gradients of units {units} equal the non-offloaded run's bit for bit")

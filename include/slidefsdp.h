@@ -267,8 +267,8 @@ int sf_dma_init(int device);
 int sf_dma_set_engines(uint32_t engine_mask);
 int sf_dma_get_engines(uint32_t* engine_mask);
 
-/* Route around held engines: mode 0 no, 1 onto free engines 0-3, 2 (the
- * default) also onto free engines from 4 up when none of 0-3 is free.  Each
+/* Route around held engines: mode 0 no (the default), 1 onto free engines
+ * 0-3, 2 also onto free engines from 4 up when none of 0-3 is free.  Each
  * sf_dma_copy_d2h then asks the runtime which engines are free; an engine
  * of the selected set that is busy while none of this library's copies is
  * pending on it is held by another client (a HIP copy ordered after an

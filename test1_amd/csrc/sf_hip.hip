@@ -801,8 +801,9 @@ struct DmaAgents {
     bool ok = false;
     uint32_t engine_mask = 0;  // one SDMA engine bit; 0: runtime's choice
     uint64_t ts_freq = 0;      // HSA system timestamp ticks per second
-    int avoid_held = 2;        // route around engines another client holds:
-                               // 0 no, 1 onto free engines 0-3, 2 also 4 and up
+    int avoid_held = 0;        // route around engines another client holds:
+                               // 0 no (default), 1 onto free engines 0-3,
+                               // 2 also 4 and up
     // Copies issued here and not yet released by sf_dma_wait: signal handle
     // -> engine bit (0 for a runtime-chosen engine).
     std::unordered_map<uint64_t, uint32_t> outstanding;

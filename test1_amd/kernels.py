@@ -367,9 +367,9 @@ def dma_set_engines(engines: Sequence[int]) -> None:
 
 
 def dma_set_avoid_held(mode: int) -> None:
-    """Route device -> host copies around engines another client holds: 0 no,
-    1 onto free engines 0-3, 2 (default) also onto slower free engines from 4
-    up when none of 0-3 is free."""
+    """Route device -> host copies around engines another client holds: 0 no
+    (default), 1 onto free engines 0-3, 2 also onto slower free engines from
+    4 up when none of 0-3 is free."""
     _native.check(_native.hip().sf_dma_set_avoid_held(int(mode)), "sf_dma_set_avoid_held")
 
 

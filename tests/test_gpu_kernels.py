@@ -275,10 +275,11 @@ def test_sdma_copy_d2h(dev):
 
 def test_sdma_copy_d2h_routes_around_engine_held_by_waiting_hip_copy(dev):
     """A HIP host -> device copy ordered after an event that has not fired
-    holds its SDMA engine until the event fires.  With engines 0 and 1
-    selected (the ones HIP's host -> device copies take first), a device ->
-    host copy issued meanwhile must not queue behind such copies: it
-    completes while the event is still pending, with exact bytes."""
+    holds its SDMA engine until the event fires.  With routing on (mode 1)
+    and engines 0 and 1 selected (the ones HIP's host -> device copies take
+    first), a device -> host copy issued meanwhile must not queue behind such
+    copies: it completes while the event is still pending, with exact
+    bytes."""
     kernels.dma_init(dev)
     saved = kernels.dma_engines()
     nb = 64 << 20
@@ -308,10 +309,12 @@ def test_sdma_copy_d2h_routes_around_engine_held_by_waiting_hip_copy(dev):
         kernels.memcpy_async(d, hsrc, s)
     try:
         kernels.dma_set_engines([0, 1])
+        kernels.dma_set_avoid_held(1)
         h = kernels.dma_copy_d2h([(src, host)])
         kernels.dma_wait(h)
         pending_after_copy = not ev.query()
     finally:
+        kernels.dma_set_avoid_held(0)
         kernels.dma_set_engines(saved)
         torch.cuda.synchronize()
     assert pending_after_copy, "the device -> host copy waited for the held engines"

@@ -49,3 +49,33 @@ def test_off_and_degenerate_selections(choose):
     assert choose(E(2, 3), ALL & ~E(2, 3), 0, 0) == E(2, 3)   # mode 0: routing off
     assert choose(0, 0, 0, 2) == 0                            # runtime's own choice stays
     assert choose(E(2) | (1 << 20), ALL & ~E(2), 0, 1) == E(0)  # bits past engine 15 ignored
+
+
+def test_choice_invariants_over_random_masks(choose):
+    """For random selections, free masks and our-copy masks: mode 0 and any
+    selection without a held engine come back unchanged; otherwise the
+    choice is the selection (nothing better free) or a set with no held
+    engine, made of the selection's unheld engines plus free engines (among
+    0-3, or from 4 up in mode 2 when none of 0-3 could be had), never larger
+    than twice the selection."""
+    import random
+    rng = random.Random(7)
+    for _ in range(20000):
+        preferred = rng.getrandbits(16) & rng.getrandbits(16)
+        avail = rng.getrandbits(16)
+        ours = rng.getrandbits(16) & ~avail & 0xFFFF
+        mode = rng.randrange(3)
+        got = choose(preferred, avail, ours, mode)
+        held = ~avail & ~ours & 0xFFFF
+        if mode == 0 or preferred == 0 or not (preferred & held):
+            assert got == preferred
+            continue
+        if got == preferred:
+            continue   # nothing usable: keep the selection
+        assert not (got & held), (preferred, avail, ours, mode, got)
+        extra = got & ~preferred
+        assert not (extra & ~avail), "an added engine must be free"
+        fast = extra & 0xF
+        assert bin(got).count("1") <= 2 * bin(preferred).count("1")
+        if extra & ~0xF:
+            assert mode == 2 and not (got & preferred & ~held) and not fast, "slow engines only when no fast one"

@@ -666,6 +666,11 @@ def main():
     ap.add_argument("--cast-on-copy", action="store_true",
                     help="cast a unit staged after its update on the cast stream as soon as its copy lands "
                          "(default: where the unit is next used, between the forward's kernels)")
+    ap.add_argument("--hw-queues", type=int, default=8,
+                    help="hardware queues of the HIP runtime (GPU_MAX_HW_QUEUES) for this process, set before "
+                         "the first GPU call; 0 keeps the environment's.  The step drives four streams of its own "
+                         "beside torch's; with the default four queues two of them share one, and the step ran "
+                         "2.5 %% slower")
     ap.add_argument("--wait-timeout", type=float, default=None,
                     help="seconds a host wait of the runtime may take (default: the library's; 0: no limit)")
     ap.add_argument("--no-link-timing", action="store_true",
@@ -677,6 +682,12 @@ def main():
         print("bench.py: this build runs the layer-streaming path on one GPU only; use --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    if not 0 <= args.hw_queues <= 32:
+        print("bench.py: --hw-queues must be in 0..32", file=sys.stderr)
+        sys.exit(2)
+    if args.hw_queues:
+        # Read by the HIP runtime at its first call: set before torch touches the GPU.
+        os.environ["GPU_MAX_HW_QUEUES"] = str(args.hw_queues)
     import torch
 
     w = dict(WORKLOADS[args.workload])
@@ -765,6 +776,7 @@ def main():
                    "global_batch": B, "seq_len": S, "layers": w["layers"], "hidden": w["hidden"],
                    "params": total_params, "parallelism": "none (1 GPU)",
                    "h2d_format": args.h2d_format, "resident_layers": r["resident_layers"],
+                   "hw_queues": int(os.environ.get("GPU_MAX_HW_QUEUES", "4")),
                    "d2h_engine": args.d2h_engine, "fused_cross_entropy": args.fused_ce,
                    "stage_after_update": r["stage_after_update"],
                    "update_piece_elems": args.piece_elems,

@@ -666,11 +666,12 @@ def main():
     ap.add_argument("--cast-on-copy", action="store_true",
                     help="cast a unit staged after its update on the cast stream as soon as its copy lands "
                          "(default: where the unit is next used, between the forward's kernels)")
-    ap.add_argument("--hw-queues", type=int, default=8,
+    ap.add_argument("--hw-queues", type=int, default=None,
                     help="hardware queues of the HIP runtime (GPU_MAX_HW_QUEUES) for this process, set before "
-                         "the first GPU call; 0 keeps the environment's.  The step drives four streams of its own "
-                         "beside torch's; with the default four queues two of them share one, and the step ran "
-                         "2.5 %% slower")
+                         "the first GPU call; 0 keeps the environment's.  Default: 8 for the Llama-3.1-8B "
+                         "workload (the step drives four streams of its own beside torch's; with four queues two "
+                         "of them share one, and the step ran 2.5 %% slower), the environment's otherwise: the "
+                         "extra queues pin memory, and the fp32 Qwen2.5-14B step is at the pinned-memory limit")
     ap.add_argument("--wait-timeout", type=float, default=None,
                     help="seconds a host wait of the runtime may take (default: the library's; 0: no limit)")
     ap.add_argument("--no-link-timing", action="store_true",
@@ -682,6 +683,8 @@ def main():
         print("bench.py: this build runs the layer-streaming path on one GPU only; use --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    if args.hw_queues is None:
+        args.hw_queues = 8 if args.workload == "llama3-8b" else 0
     if not 0 <= args.hw_queues <= 32:
         print("bench.py: --hw-queues must be in 0..32", file=sys.stderr)
         sys.exit(2)

@@ -48,6 +48,7 @@ row-sparse embedding, bf16 H2D, SDMA gradient copies) change no bits.
 from __future__ import annotations
 
 import os
+import warnings
 from typing import List, Optional
 
 import torch
@@ -60,8 +61,7 @@ from .distributed_sync import create_distributed_sync
 from .fused_ce import chunked_linear_cross_entropy
 from .layer_state import GradSlotRing, LayerRuntimeState, StreamingRuntime
 from .optimizer import LayerAdam
-from .pinned import pinned_empty
-from .sliding_checkpoint import ActivationRing, SlidingCheckpoint, StorageSpill
+from .sliding_checkpoint import ActivationRing, KeptOnDevice, SlidingCheckpoint, StorageSpill, pin_or_keep
 
 
 try:  # transformers >= 5: masks are built by a module-level function
@@ -552,13 +552,19 @@ class SlideFSDP(nn.Module):
     # ------------------------------------------------------------------
     def _allocate_activation_tensors(self, batch_size: int, seq_length: int, hidden_size: int) -> None:
         """Pinned host slot of the hidden-state checkpoint per decoder layer
-        (reference slide_fsdp.py:466-505); the mask slot is created on demand."""
+        (reference slide_fsdp.py:466-505); the mask slot is created on demand.
+        A slot the host cannot pin (the driver's pinned-memory limit) keeps
+        that layer's checkpoint in device memory; the reference raises there."""
         if self.config.ac_offload_mode == "none":
             return
         self.layer_tensors = [
-            [pinned_empty((batch_size, seq_length, hidden_size), self.dtype)]
+            [pin_or_keep((batch_size, seq_length, hidden_size), self.dtype)]
             for _ in range(self.num_decoder_layers)
         ]
+        kept = sum(isinstance(t[0], KeptOnDevice) for t in self.layer_tensors)
+        if kept:
+            warnings.warn(f"{kept} of {self.num_decoder_layers} checkpoint slots could not be pinned; "
+                          "those layers keep their checkpoints in device memory")
 
     @staticmethod
     def _first(out):

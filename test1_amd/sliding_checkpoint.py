@@ -56,7 +56,7 @@ from torch.autograd.graph import saved_tensors_hooks
 # (sliding_checkpoint.py:206-231); torch's own class is the same interface.
 from torch.autograd.graph import save_on_cpu  # noqa: F401
 
-from . import kernels, storage
+from . import _native, kernels, storage
 from .pinned import pinned_empty
 
 _offload_streams = {}
@@ -110,6 +110,28 @@ class ActivationRing:
 
     def reset(self) -> None:
         self.fifo.clear()
+
+
+class KeptOnDevice:
+    """A checkpoint slot that could not be pinned (the driver's pinned-memory
+    limit): that checkpoint stays in device memory, as the last decoder's
+    does, and its layer's prefetch has nothing to copy for it."""
+
+    __slots__ = ("shape", "dtype")
+
+    def __init__(self, shape, dtype):
+        self.shape, self.dtype = torch.Size(shape), dtype
+
+
+def pin_or_keep(shape, dtype):
+    """A pinned slot of ``shape``/``dtype``, or ``KeptOnDevice`` when the
+    host cannot pin it."""
+    try:
+        return pinned_empty(shape, dtype)
+    except _native.NativeError as e:
+        if e.status != _native.HIP_ERROR_OUT_OF_MEMORY:
+            raise
+        return KeptOnDevice(shape, dtype)
 
 
 class _OnStorage:
@@ -371,7 +393,7 @@ class SlidingCheckpoint(saved_tensors_hooks):
                     # or a new batch shape: (re)allocate it, pinned and exact-size.
                     if self.before_pin is not None:
                         self.before_pin()
-                    slot = pinned_empty(tensor.shape, tensor.dtype)
+                    slot = pin_or_keep(tensor.shape, tensor.dtype)
                     slots[self.pack_counter] = slot
             cur = torch.cuda.current_stream()
             if self.pack_counter == 0:
@@ -381,6 +403,11 @@ class SlidingCheckpoint(saved_tensors_hooks):
                     self.pack_fence(self.stream)
                 if self._trace is not None:
                     self._trace("act_d2h", self.layer_idx + 1)
+            if isinstance(slot, KeptOnDevice):
+                # no pinned slot: the checkpoint stays in device memory
+                self.pack_counter += 1
+                self._counts[(self._key, self.layer_idx)] = self.pack_counter
+                return (tensor.device, tensor)
             src = tensor.detach()
             if not src.is_contiguous():
                 with torch.cuda.stream(self.stream):
@@ -443,10 +470,15 @@ class SlidingCheckpoint(saved_tensors_hooks):
                             self._trace("act_h2d", nxt + 1)
                 elif nxt >= 0:
                     host = self.layer_tensors[nxt][: self._slots_used(nxt)]
+                    # tensors kept in device memory (KeptOnDevice) get no
+                    # buffer: their entry is None and the packed tensor is served
+                    pinned = [h for h in host if not isinstance(h, KeptOnDevice)]
                     if self.ring is not None:
-                        bufs = self.ring.buffers_like(host)
+                        got = self.ring.buffers_like(pinned)
                     else:
-                        bufs = [torch.empty(t.shape, dtype=t.dtype, device=self.device) for t in host]
+                        got = [torch.empty(t.shape, dtype=t.dtype, device=self.device) for t in pinned]
+                    it = iter(got)
+                    bufs = [None if isinstance(h, KeptOnDevice) else next(it) for h in host]
                     ps = self.prefetch_stream
                     ps.wait_event(self.pre_unpack_event)
                     timed = self.link_timing is not None
@@ -454,6 +486,8 @@ class SlidingCheckpoint(saved_tensors_hooks):
                         t0 = torch.cuda.Event(enable_timing=True)
                         t0.record(ps)
                     for h, d in zip(host, bufs):
+                        if d is None:
+                            continue
                         kernels.memcpy_async(d, h, ps)
                         if self.ring is None:
                             d.record_stream(ps)
@@ -461,7 +495,7 @@ class SlidingCheckpoint(saved_tensors_hooks):
                     ev.record(ps)
                     if timed:
                         self.link_timing["act_h2d"].append(
-                            (t0, ev, sum(h.numel() * h.element_size() for h in host)))
+                            (t0, ev, sum(h.numel() * h.element_size() for h in pinned)))
                     self.fifo.append((bufs, ev))
                     if self._trace is not None:
                         self._trace("act_h2d", nxt + 1)
@@ -483,6 +517,8 @@ class SlidingCheckpoint(saved_tensors_hooks):
                 if self.on_prefetch_ready is not None:
                     self.on_prefetch_ready()
             result = bufs[self.unpack_counter]
+            if result is None:
+                result = tensor   # kept in device memory by the pack hook
             self._record_served(result)
             self.unpack_counter += 1
             # Pop once every prefetched tensor of this layer has been served.

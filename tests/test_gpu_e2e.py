@@ -400,6 +400,38 @@ def test_fallback_slot_ring_when_per_unit_slots_do_not_fit(dev, monkeypatch):
     sf.close()
 
 
+@pytest.mark.parametrize("refused", [(1,), (0, 1)])
+def test_checkpoints_kept_on_device_when_slots_cannot_be_pinned(dev, monkeypatch, refused):
+    """Pinning the checkpoint slot of decoders ``refused`` fails (the
+    driver's pinned-memory limit): those decoders keep their checkpoints in
+    HBM, the others still go through pinned slots; updates stay the
+    oracle's, bit for bit, over 3 steps, and the first-step gradients and 10
+    losses are the non-offloaded run's, bit for bit."""
+    from test1_amd import _native, sliding_checkpoint
+    from test1_amd.sliding_checkpoint import KeptOnDevice
+
+    real = sliding_checkpoint.pinned_empty
+    calls = []
+
+    def pinned_empty(shape, dtype):
+        calls.append(tuple(shape))
+        # the per-decoder slots come first, in decoder order, once per run
+        if (len(calls) - 1) % L in refused:
+            raise _native.NativeError("sf_host_alloc failed: out of memory", _native.HIP_ERROR_OUT_OF_MEMORY)
+        return real(shape, dtype)
+
+    monkeypatch.setattr(sliding_checkpoint, "pinned_empty", pinned_empty)
+    with pytest.warns(UserWarning, match="could not be pinned"):
+        sf = check_updates_against_oracle(dev, "llama", "fp32", {}, {}, keep=True)
+    kept = [i for i, t in enumerate(sf.layer_tensors) if isinstance(t[0], KeptOnDevice)]
+    assert kept == list(refused)
+    assert all(isinstance(t[0], torch.Tensor) for i, t in enumerate(sf.layer_tensors) if i not in refused)
+    sf.close()
+    calls.clear()
+    with pytest.warns(UserWarning, match="could not be pinned"):
+        check_loss_parity(dev, "llama", False, {}, {})
+
+
 def check_updates_against_oracle(dev, arch, h2d_format, cfg_kw, sf_kw, steps=3, nvme_buffers=None, shapes=None,
                                  vocab=V, keep=False, timing=False, setup=None, between=None):
     from test1_amd import SlideFSDP, SlideFSDPConfig

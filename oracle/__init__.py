@@ -1,8 +1,8 @@
 """CPU oracle for the layer-streaming path.
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
-the CPU-baseline leg of ``bench.py`` may import this package, and only as the
-checker.  The product (``test1_amd``) never imports, links or runs it.
+the CPU-baseline leg of ``bench.py`` may import this package, and only to
+check results.  The product (``test1_amd``) never imports, links or runs it.
 
 Contents (each function cites the reference file:line it restates):
   cast_f32_bf16    layer_state.py:301                fp32 -> bf16 RNE cast

@@ -1,7 +1,7 @@
 """Scalar / numpy restatement of the reference's layer-streaming arithmetic.
 
-TEST INFRASTRUCTURE ONLY (see the package docstring): the checker, never the
-thing measured or shipped.
+TEST INFRASTRUCTURE ONLY (see the package docstring): results are checked
+against it; it is never the thing measured or shipped.
 """
 
 from __future__ import annotations

@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the layer-streaming path: a plain scalar C restatement of
  * the reference's arithmetic.  TEST INFRASTRUCTURE ONLY -- tests, the smoke
- * check and the benchmark's CPU-baseline leg may call it, as the checker;
+ * check and the benchmark's CPU-baseline leg may call it, to check results;
  * the product never links or loads it.
  *
  * Built by oracle/Makefile with -ffp-contract=off so that every operation

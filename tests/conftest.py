@@ -12,7 +12,7 @@ REF_ADAM = os.path.join(ROOT, "oracle", "_ref", "cpu_adam_ref.so")
 
 
 def pytest_configure(config):
-    config.addinivalue_line("markers", "gpu: needs an MI355X (runs on the GPU box)")
+    config.addinivalue_line("markers", "gpu: needs an MI355X GPU")
     config.addinivalue_line("markers", "slow: long-running GPU test at full layer size")
 
 

@@ -110,6 +110,12 @@ def traffic_factor():
     return float(m.group(1)) if m else None
 
 
+def _untimed(rec) -> bool:
+    """("untimed", bytes): SDMA copies whose engine timestamps were not
+    available (a profiler tracing async copies takes them over)."""
+    return isinstance(rec[0], str) and rec[0] == "untimed"
+
+
 def elapsed_stats(records):
     """(busy ms, total bytes or elements) from (start_event, end_event, amount)
     or (KernelTimer, None, amount) records (summed) or ("interval_ns", start,
@@ -118,6 +124,8 @@ def elapsed_stats(records):
     ms = amt = 0.0
     intervals = []
     for r in records or []:
+        if _untimed(r):
+            continue
         if len(r) == 4:
             intervals.append((r[1], r[2]))
             amt += r[3]
@@ -442,6 +450,8 @@ def link_timeline(rt, anchor, anchor_ns: int) -> dict:
     def spans(records):
         out = []
         for rec in records or []:
+            if _untimed(rec):
+                continue
             if len(rec) == 4:                      # ("interval_ns", start, end, bytes)
                 out.append((rec[1], rec[2], rec[3]))
             else:                                  # (start event, end event, bytes)
@@ -456,6 +466,7 @@ def link_timeline(rt, anchor, anchor_ns: int) -> dict:
                 "rows": spans(lt.get("rows_d2h"))},
         "compute": [(ns(a), ns(b)) for a, b in lt.get("compute", [])],
         "common_clock": anchor_ns != 0,
+        "untimed_d2h_bytes": sum(rec[1] for rec in rt.d2h_timing or [] if _untimed(rec)),
     }
 
 
@@ -516,6 +527,11 @@ def link_stats(r: dict, steps: int, alone: Optional[dict] = None) -> dict:
             "busy_frac_of_step": busy_ns * 1e-9 / r["elapsed"],
             "under_compute_frac": (_overlap(u, comp) / busy_ns) if (busy_ns > 0 and lk["common_clock"]) else None,
         }
+        untimed = lk.get(f"untimed_{d}_bytes", 0)
+        if untimed:
+            out[d]["untimed_bytes_per_step"] = untimed / steps
+            out[d]["untimed_note"] = ("gradient copies without SDMA engine timestamps (a profiler tracing async "
+                                      "copies takes them over): the rates above cover the timed transfers only")
     out["compute_busy_frac_of_step"] = _length(comp) * 1e-9 / r["elapsed"]
     out["note"] = ("rates over the union of all transfers of a direction (h2d: parameter copies, checkpoint "
                    "prefetches, embedding lookup rows; d2h: SDMA gradient copies, checkpoint packs, embedding "

@@ -932,6 +932,10 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
                 del keep
                 if rt.d2h_timing is not None and state["t0"] is not None:
                     rt.d2h_timing.append(("interval_ns", state["t0"], state["t1"], nbytes))
+                elif rt.d2h_timing is not None and any(ch is not None for ch in chunks):
+                    # SDMA copies without engine timestamps (a profiler that
+                    # traces async copies takes them over)
+                    rt.d2h_timing.append(("untimed", nbytes))
                 rt.grad_ring.release(slot)
             finally:
                 self.update_finished.set()

@@ -408,3 +408,10 @@ def test_bench_link_arithmetic():
     assert abs(st["compute_busy_frac_of_step"] - 0.3) < 1e-9
     r["link"]["common_clock"] = False                          # no SDMA clock: no overlap figure
     assert bench.link_stats(r, steps=1)["h2d"]["under_compute_frac"] is None
+    assert "untimed_bytes_per_step" not in st["d2h"]
+    # gradient copies without engine timestamps are reported, not counted as 0 B
+    r["link"]["untimed_d2h_bytes"] = 600_000_000
+    d = bench.link_stats(r, steps=2)["d2h"]
+    assert d["untimed_bytes_per_step"] == 3e8 and d["bytes_per_step_by_kind"]["grads"] == 2e8
+    recs = [("untimed", 600_000_000), ("interval_ns", 0, 10 * ms, 400_000_000)]
+    assert bench.elapsed_stats(recs) == (10.0, 400_000_000)

@@ -699,6 +699,12 @@ def main():
         print("bench.py: this build runs the layer-streaming path on one GPU only; use --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    # stdout carries the one JSON line only: everything else printed there
+    # (the wrapper's model summary, the host AdamW's banner from C) goes to stderr.
+    sys.stdout.flush()
+    json_out = os.fdopen(os.dup(1), "w")
+    os.dup2(2, 1)
+
     if args.hw_queues is None:
         args.hw_queues = 8 if args.workload == "llama3-8b" else 0
     if not 0 <= args.hw_queues <= 32:
@@ -843,7 +849,7 @@ def main():
         "losses_finite": all(math.isfinite(x) for x in losses),
         "variants": variants,
     }
-    print(json.dumps(res), flush=True)
+    print(json.dumps(res), file=json_out, flush=True)
 
 
 if __name__ == "__main__":

@@ -166,7 +166,9 @@ class StreamingRuntime:
         # Test hook: when a dict, each update stores {unit: (host grads, fp32
         # master before the update)} and each gradient offload stores
         # {("device_grads", unit): [param.grad clones]}, for checking the
-        # pack and the update against the oracle.  ``capture_units`` (a set)
+        # pack and the update against the oracle, and for every unit but the
+        # row-sparse embedding {("grad_sums", unit): [int64 sum of each
+        # gradient's 16-bit words]}.  ``capture_units`` (a set)
         # limits it to those units (None: every unit), so that full-size
         # models capture a few units instead of copying every one.
         self.capture: Optional[dict] = None
@@ -658,6 +660,12 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
         if self.runtime.capturing(self.layer_idx):
             self.runtime.capture[("device_grads", self.layer_idx)] = [
                 None if p.grad is None else p.grad.detach().clone() for p in self._params]
+        if self.runtime.capture is not None:
+            # every unit, also outside ``capture_units``: the sum of each
+            # gradient's 16-bit words (exact, a few bytes per parameter)
+            self.runtime.capture[("grad_sums", self.layer_idx)] = [
+                None if p.grad is None else p.grad.detach().view(torch.int16).sum(dtype=torch.int64)
+                for p in self._params]
         grad_ready = _new_event()
         grad_ready.record(cur)
         # The cast issued last before these gradients existed (the next unit's

@@ -31,11 +31,30 @@ def same_bits(a, b) -> bool:
     return np.array_equal(u16(a).reshape(-1), u16(b).reshape(-1))
 
 
-def check_step1_against_reference(cap, ref_grads, units):
+def grad_word_sums(grads):
+    """Per gradient, the sum of its 16-bit words (None for a missing one):
+    the checksum the runtime records as ``("grad_sums", unit)``."""
+    return [None if g is None else int(g.detach().view(torch.int16).sum(dtype=torch.int64)) for g in grads]
+
+
+def check_step1_against_reference(cap, ref_grads, units, ref_sums=None):
     """SlideFSDP's step-1 device gradients of ``units`` equal the
-    non-offloaded run's, bit for bit.  A failure lists every unit that
-    differs with the fraction of its elements that still match."""
+    non-offloaded run's, bit for bit, and (with ``ref_sums``, per unit the
+    reference's ``grad_word_sums``) every other unit's gradients have the
+    reference's checksums.  A failure lists every unit that differs, with
+    the fraction of its elements that still match or the parameters whose
+    checksums differ, so that the highest unit listed is where the
+    backward first went apart."""
     bad = []
+    if ref_sums is not None:
+        for u in sorted(ref_sums, reverse=True):
+            got = cap.get(("grad_sums", u))
+            if got is None:
+                continue      # the row-sparse embedding records none
+            got = [None if t is None else int(t) for t in got]
+            diff = [j for j, (a, b) in enumerate(zip(got, ref_sums[u])) if a != b]
+            if len(got) != len(ref_sums[u]) or diff:
+                bad.append(f"unit {u} checksums of parameters {diff}")
     for u in units:
         got, exp = cap[("device_grads", u)], ref_grads[u]
         assert len(got) == len(exp), f"unit {u}: {len(got)} gradients, expected {len(exp)}"
@@ -72,11 +91,12 @@ def gpu_bf16_copy(model, dev, dtype=torch.bfloat16):
     return gm
 
 
-def reference_step(gm, ids, vocab, units, layer_inputs=None):
+def reference_step(gm, ids, vocab, units, layer_inputs=None, grad_sums=None):
     """One forward/backward of the non-offloaded model with transformers' own
     decoder forward (causal mask, rotary) and per-layer recompute; returns the
     loss and the bf16 gradients of ``units`` (host).  A list passed as
-    ``layer_inputs`` receives each decoder layer's input hidden states (host)."""
+    ``layer_inputs`` receives each decoder layer's input hidden states (host);
+    a dict passed as ``grad_sums`` receives every unit's ``grad_word_sums``."""
     gm.gradient_checkpointing_enable(gradient_checkpointing_kwargs={"use_reentrant": False})
     gm.train()
     gm.zero_grad(set_to_none=True)
@@ -93,6 +113,8 @@ def reference_step(gm, ids, vocab, units, layer_inputs=None):
     loss.backward()
     ups = unit_params(gm)
     grads = {u: [p.grad.detach().cpu() for p in ups[u]] for u in units}
+    if grad_sums is not None:
+        grad_sums.update({u: grad_word_sums([p.grad for p in ps]) for u, ps in enumerate(ups)})
     return loss.item(), grads
 
 

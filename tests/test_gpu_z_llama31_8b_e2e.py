@@ -37,7 +37,7 @@ import pytest
 import torch
 
 from fullsize import (CapturedOracle, check_backward_weights, check_checkpoint_slots, check_served_checkpoints,
-                      check_served_side_inputs, unit_weight_sums, check_masters, check_moments, check_packed_grads,
+                      check_served_side_inputs, grad_word_sums, unit_weight_sums, check_masters, check_moments, check_packed_grads,
                       check_staged, check_step1_against_reference, gpu_bf16_copy, say, timed, unit_params)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -60,13 +60,14 @@ def _fp32_loss(logits, ids, vocab):
 def _reference(model, batches, dev, vocab, units):
     """bf16 weights on the GPU, fp32 masters and AdamW moments in HBM.
     Returns the bf16 losses, the fp32 losses, step 1's gradients of
-    ``units`` and step 1's decoder layer inputs (host)."""
+    ``units``, step 1's decoder layer inputs (host), the weight checksums
+    and step 1's gradient checksums of every unit."""
     gm = gpu_bf16_copy(model, dev)
     sums = unit_weight_sums(gm)
     gparams = list(gm.parameters())
     masters = [p.detach().to(dev, torch.float32) for p in model.parameters()]
     opt = torch.optim.AdamW(masters, lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
-    losses, losses32, grads, layer_inputs = [], [], None, None
+    losses, losses32, grads, layer_inputs, grad_sums = [], [], None, None, None
     for k, ids in enumerate(batches[:STEPS]):
         ids = ids.to(dev)
         gm.zero_grad(set_to_none=True)
@@ -83,6 +84,7 @@ def _reference(model, batches, dev, vocab, units):
         if k == 0:
             ups = unit_params(gm)
             grads = {u: [p.grad.detach().cpu() for p in ups[u]] for u in units}
+            grad_sums = {u: grad_word_sums([p.grad for p in ps]) for u, ps in enumerate(ups)}
         with torch.no_grad():
             for m, p in zip(masters, gparams):
                 m.grad = p.grad.float()
@@ -94,7 +96,7 @@ def _reference(model, batches, dev, vocab, units):
         say(f"[reference] step {k}: loss {losses[-1]:.5f} (fp32 {losses32[-1]:.6f})")
     del gm, masters, opt, gparams
     torch.cuda.empty_cache()
-    return losses, losses32, grads, layer_inputs, sums
+    return losses, losses32, grads, layer_inputs, sums, grad_sums
 
 
 def test_llama31_8b_parity_10_steps(dev):
@@ -107,8 +109,8 @@ def test_llama31_8b_parity_10_steps(dev):
     units = (1, L + 1)
     model = timed("model built", bench.build_model, w)
     batches = _batches(w)
-    ref, ref32, ref_grads, layer_inputs, sums = timed("reference run", _reference, model, batches, dev, w["vocab"],
-                                                      units)
+    ref, ref32, ref_grads, layer_inputs, sums, ref_sums = timed("reference run", _reference, model, batches, dev,
+                                                                w["vocab"], units)
 
     orc = CapturedOracle(model, units, LR, BETAS, EPS, WD)
     cfg = SlideFSDPConfig(device=dev, lr=LR, adam_betas=BETAS, adam_eps=EPS, weight_decay=WD,
@@ -144,9 +146,10 @@ def test_llama31_8b_parity_10_steps(dev):
                 say(f"step 1: the recomputes of {n} decoders were given the non-offloaded forward's layer inputs "
                     f"and {n_side} more tensors of the forward's; the backward of {n_units} units read the forward's "
                     f"weights")
-                check_step1_against_reference(cap, ref_grads, units)
+                check_step1_against_reference(cap, ref_grads, units, ref_sums)
                 del ref_grads
-                say(f"step 1: loss and gradients of units {units} equal the non-offloaded run's bit for bit")
+                say(f"step 1: loss and gradients of units {units} equal the non-offloaded run's bit for bit, and every "
+                    f"unit's gradient checksums")
             check_packed_grads(cap, units)
             orc.step(cap)
             check_masters(sf, orc, units)

@@ -55,9 +55,9 @@ def test_qwen25_14b_step_against_reference_and_oracle(dev):
     from test1_amd.pinned import pinned_bytes_live
     say(f"pinned memory live at the start: {pinned_bytes_live() / 2**30:.1f} GiB")
     gm = timed("bf16 copy on the GPU", gpu_bf16_copy, model, dev)
-    layer_inputs = []
+    layer_inputs, ref_sums = [], {}
     ref_loss, ref_grads = timed("reference step", reference_step, gm, batches[0].to(dev), w["vocab"], units,
-                                layer_inputs)
+                                layer_inputs, ref_sums)
     sums = unit_weight_sums(gm)
     del gm
     gc.collect()
@@ -96,9 +96,10 @@ def test_qwen25_14b_step_against_reference_and_oracle(dev):
                 say(f"step 1: the recomputes of {n} decoders were given the non-offloaded forward's layer inputs "
                     f"and {n_side} more tensors of the forward's; the backward of {n_units} units read the forward's "
                     f"weights")
-                check_step1_against_reference(cap, ref_grads, units)
+                check_step1_against_reference(cap, ref_grads, units, ref_sums)
                 del ref_grads
-                say(f"step 1: loss and gradients of units {units} equal the non-offloaded run's bit for bit")
+                say(f"step 1: loss and gradients of units {units} equal the non-offloaded run's bit for bit, and every "
+                    f"unit's gradient checksums")
             check_packed_grads(cap, units)
             timed(f"oracle step {k + 1}", orc.step, cap)
             check_masters(sf, orc, units)

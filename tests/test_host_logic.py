@@ -415,3 +415,23 @@ def test_bench_link_arithmetic():
     assert d["untimed_bytes_per_step"] == 3e8 and d["bytes_per_step_by_kind"]["grads"] == 2e8
     recs = [("untimed", 600_000_000), ("interval_ns", 0, 10 * ms, 400_000_000)]
     assert bench.elapsed_stats(recs) == (10.0, 400_000_000)
+
+
+def test_checkpoint_slot_kept_on_device_only_when_pinning_runs_out(monkeypatch):
+    """A checkpoint slot the host cannot pin (out of memory) becomes a
+    ``KeptOnDevice`` marker of the slot's shape and dtype; any other failure
+    of the pinned allocation still raises."""
+    from test1_amd import _native, sliding_checkpoint as sc
+
+    def refuse(status):
+        def pinned_empty(shape, dtype):
+            raise _native.NativeError("sf_host_alloc failed", status)
+        return pinned_empty
+
+    monkeypatch.setattr(sc, "pinned_empty", refuse(_native.HIP_ERROR_OUT_OF_MEMORY))
+    kept = sc.pin_or_keep((4, 16, 32), torch.bfloat16)
+    assert isinstance(kept, sc.KeptOnDevice)
+    assert kept.shape == (4, 16, 32) and kept.dtype == torch.bfloat16
+    monkeypatch.setattr(sc, "pinned_empty", refuse(1))
+    with pytest.raises(_native.NativeError):
+        sc.pin_or_keep((4, 16, 32), torch.bfloat16)

@@ -14,7 +14,9 @@
  *     nothing and keep no global mutable state, so any host thread may call
  *     them concurrently on different streams.  The one exception is
  *     sf_stage_f32_bf16_noalloc, whose device scratch buffer is shared by
- *     all its calls on a device (calls must not overlap there).
+ *     all its calls on a device: the library orders each call after the
+ *     previous one on that device (an event it records), whatever stream
+ *     each runs on.
  *   - Sizes are element counts unless the name says bytes.
  *
  * Each declaration names the reference interface (file:line in the
@@ -45,6 +47,7 @@ typedef void* sf_event_t;
 #define SF_ENOREQ 9006      /* unknown or already released I/O ticket */
 #define SF_EALIGN 9007      /* O_DIRECT transfer not aligned to SF_IO_ALIGN */
 #define SF_ETOOBIG 9008     /* larger than the library's device scratch */
+#define SF_ETIMEDOUT 9009   /* a bounded wait ended before the work completed */
 #define SF_EDMA_BASE 10000  /* + (hsa_status_t & 0xFFF): a ROCr DMA call failed */
 #define SF_EIO_BASE 20000   /* + errno: a file operation failed */
 
@@ -69,8 +72,9 @@ const char* sf_error_string(int status);
 
 /* ABI version, bumped on any incompatible change (SF_ABI_VERSION).
  * 2: row_slot markers of the row-wise AdamW (SF_ROW_SKIP; other values
- *    below SF_ROW_SKIP are an error). */
-#define SF_ABI_VERSION 2
+ *    below SF_ROW_SKIP are an error).
+ * 3: sf_dma_wait takes a deadline (timeout_ns; SF_ETIMEDOUT). */
+#define SF_ABI_VERSION 3
 int sf_abi_version(void);
 
 /* ---------------------------------------------------------------------
@@ -130,14 +134,18 @@ int sf_stage_f32_bf16(const float* host_src, uint16_t* dst, size_t n,
 /* sf_stage_f32_bf16 that allocates nothing: the pieces (chunk_elems fp32
  * elements; 0 selects SF_STAGE_SCRATCH_ELEMS, more is refused with
  * SF_ETOOBIG before anything is enqueued) go through a device buffer of the
- * library's own, one static array per device, whose address is looked up on
- * the first call on each device.  `stream` must belong to the current
- * device.  No hipMalloc, hipFree or other allocating call is made.  Every
- * call on a device uses that device's one buffer: calls on one stream (or
- * otherwise ordered) are safe; calls that overlap on one device race.  No
- * counterpart in the reference (its staging allocates nothing on the device
- * but runs on the host, layer_state.py:299-314); for callers that cannot
- * allocate device memory: code under HIP graph capture, serving loops. */
+ * library's own, one static array per device, whose address is looked up
+ * (and one ordering event created) on the first call on each device.
+ * `stream` must belong to the current device.  No hipMalloc, hipFree or
+ * other allocating call is made after that first call.  Every call on a
+ * device uses that device's one buffer, so the library orders the calls:
+ * each call's stream first waits for the last cast of the previous call on
+ * that device (an event recorded after it), then the call records the event
+ * after its own last cast.  Calls on different streams are therefore
+ * serialised on the device, in the order their host calls enter the
+ * library.  No counterpart in the reference; for callers that cannot
+ * allocate device memory (tight serving loops, harnesses that forbid
+ * allocation). */
 int sf_stage_f32_bf16_noalloc(const float* host_src, uint16_t* dst, size_t n,
                               size_t chunk_elems, sf_stream_t stream);
 
@@ -297,12 +305,16 @@ uint32_t sf_dma_choose_engines(uint32_t preferred, uint32_t avail, uint32_t ours
 int sf_dma_copy_d2h(const sf_seg* segs, int nsegs, uint64_t* signals,
                     int max_signals, int* nsignals);
 
-/* Block until every handle completed, then release them.  If start_ns and
- * end_ns are non-null and timing is enabled, they receive the earliest start
- * and the latest end of the copies, in ns of the HSA system clock (both 0
- * when timing is off). */
-int sf_dma_wait(const uint64_t* signals, int nsignals, uint64_t* start_ns,
-                uint64_t* end_ns);
+/* Wait until every handle has completed, then release them.  timeout_ns
+ * bounds the wait (0: no limit); when it passes with a copy still pending,
+ * SF_ETIMEDOUT is returned and no handle is released (each stays valid for
+ * a later sf_dma_query or sf_dma_wait; the copies keep running).  The wait
+ * polls the completion signals with 50 us sleeps.  If start_ns and end_ns
+ * are non-null and timing is enabled, they receive the earliest start and
+ * the latest end of the copies, in ns of the HSA system clock (both 0 when
+ * timing is off). */
+int sf_dma_wait(const uint64_t* signals, int nsignals, uint64_t timeout_ns,
+                uint64_t* start_ns, uint64_t* end_ns);
 
 /* Non-blocking completion test of copies started by sf_dma_copy_d2h:
  * *done = 1 when every signal has completed, else 0.  The signals stay

@@ -36,6 +36,7 @@ SF_EINVAL = 9001
 SF_ETOOMANY = 9002
 SF_EALIGN = 9007
 SF_ETOOBIG = 9008
+SF_ETIMEDOUT = 9009
 SF_STAGE_SCRATCH_ELEMS = 16 << 20
 # row_slot markers of the row-wise AdamW: a zero-gradient row, a row left as it is
 SF_ROW_ZERO = -1
@@ -95,7 +96,7 @@ HIP_SIGNATURES = {
     "sf_dma_set_avoid_held": [_i],
     "sf_dma_choose_engines": [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _i],
     "sf_dma_copy_d2h": [ctypes.POINTER(SfSeg), _i, ctypes.POINTER(ctypes.c_uint64), _i, ctypes.POINTER(_i)],
-    "sf_dma_wait": [ctypes.POINTER(ctypes.c_uint64), _i, ctypes.POINTER(ctypes.c_uint64),
+    "sf_dma_wait": [ctypes.POINTER(ctypes.c_uint64), _i, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64),
                     ctypes.POINTER(ctypes.c_uint64)],
     "sf_dma_query": [ctypes.POINTER(ctypes.c_uint64), _i, ctypes.POINTER(ctypes.c_int)],
     "sf_dma_enable_timing": [_i],

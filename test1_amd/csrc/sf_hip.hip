@@ -454,6 +454,7 @@ const char* sf_error_string(int status) {
         case SF_ENOOPT: return "sf: unknown optimizer id";
         case SF_EOVERLAP: return "sf: source and destination overlap";
         case SF_ETOOBIG: return "sf: piece larger than the library's device scratch (SF_STAGE_SCRATCH_ELEMS)";
+        case SF_ETIMEDOUT: return "sf: wait ended at its deadline with work still pending";
         default:
             if (status >= SF_EDMA_BASE && status < SF_EDMA_BASE + 0x1000) return "sf: ROCr DMA call failed";
             return hipGetErrorString(hipError_t(status));
@@ -707,12 +708,21 @@ namespace {
 __device__ __align__(256) float scratch[SF_STAGE_SCRATCH_ELEMS];
 
 constexpr int kMaxDevices = 64;
+// Per device: the address of `scratch`, and an event recorded after the last
+// cast of the previous call (the next call's stream waits on it).  The
+// mutex is held from the wait to the record, so the calls of several host
+// threads are ordered one after the other.
+struct ScratchState {
+    float* ptr = nullptr;
+    hipEvent_t last = nullptr;
+    bool recorded = false;
+};
 std::mutex g_scratch_mu;
-float* g_scratch_ptr[kMaxDevices] = {};
+ScratchState g_scratch[kMaxDevices];
 
-// Device address of `scratch` on the current device, which must be the
-// device of `st` (the null stream: the current device).
-int scratch_for_stream(hipStream_t st, float** out) {
+// The current device, which must be the device of `st` (the null stream:
+// the current device), after the one-time set-up of its scratch state.
+int scratch_device_for_stream(hipStream_t st, int* dev) {
     int cur = 0;
     hipError_t e = hipGetDevice(&cur);
     if (e != hipSuccess) return hip_status(e);
@@ -723,15 +733,19 @@ int scratch_for_stream(hipStream_t st, float** out) {
         if (int(sd) != cur) return SF_EINVAL;
     }
     if (cur < 0 || cur >= kMaxDevices) return SF_EINVAL;
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    if (g_scratch_ptr[cur] == nullptr) {
+    ScratchState& s = g_scratch[cur];
+    if (s.ptr == nullptr) {
         void* p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return hip_status(e);
         if (p == nullptr) return SF_EINVAL;
-        g_scratch_ptr[cur] = static_cast<float*>(p);
+        if (s.last == nullptr) {
+            e = hipEventCreateWithFlags(&s.last, hipEventDisableTiming);
+            if (e != hipSuccess) return hip_status(e);
+        }
+        s.ptr = static_cast<float*>(p);
     }
-    *out = g_scratch_ptr[cur];
+    *dev = cur;
     return SF_OK;
 }
 
@@ -745,10 +759,22 @@ int sf_stage_f32_bf16_noalloc(const float* host_src, uint16_t* dst, size_t n, si
     if (n == 0) return SF_OK;
     if (host_src == nullptr || dst == nullptr) return SF_EINVAL;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    float* buf = nullptr;
-    const int rc = scratch_for_stream(st, &buf);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    int dev = 0;
+    int rc = scratch_device_for_stream(st, &dev);
     if (rc != SF_OK) return rc;
-    return stage_launch(host_src, dst, n, buf, chunk_elems == 0 ? SF_STAGE_SCRATCH_ELEMS : chunk_elems, st);
+    ScratchState& s = g_scratch[dev];
+    if (s.recorded) {
+        const hipError_t e = hipStreamWaitEvent(st, s.last, 0);
+        if (e != hipSuccess) return hip_status(e);
+    }
+    rc = stage_launch(host_src, dst, n, s.ptr, chunk_elems == 0 ? SF_STAGE_SCRATCH_ELEMS : chunk_elems, st);
+    // Recorded also after a failed launch: whatever was enqueued before the
+    // failure still uses the scratch buffer and must precede the next call.
+    const hipError_t e = hipEventRecord(s.last, st);
+    if (e == hipSuccess) s.recorded = true;
+    if (rc != SF_OK) return rc;
+    return hip_status(e);
 }
 
 int sf_memcpy_async(void* dst, const void* src, size_t bytes, int kind, sf_stream_t stream) {
@@ -1010,19 +1036,28 @@ int sf_dma_copy_d2h(const sf_seg* segs, int nsegs, uint64_t* signals, int max_si
     return SF_OK;
 }
 
-int sf_dma_wait(const uint64_t* signals, int nsignals, uint64_t* start_ns, uint64_t* end_ns) {
+int sf_dma_wait(const uint64_t* signals, int nsignals, uint64_t timeout_ns, uint64_t* start_ns,
+                uint64_t* end_ns) {
     if (nsignals < 0 || (nsignals > 0 && signals == nullptr)) return SF_EINVAL;
+    // Every copy must be complete before any handle is released, so that a
+    // wait that ends at its deadline leaves all of them valid.  Poll with
+    // short sleeps: an SDMA completion does not reliably wake a thread
+    // blocked in the runtime's interrupt wait (measured: a blocked wait
+    // returned 350 ms after the copy had finished).
+    const auto deadline = std::chrono::steady_clock::now() + std::chrono::nanoseconds(timeout_ns);
+    for (int i = 0; i < nsignals; ++i) {
+        if (signals[i] == 0) continue;
+        const hsa_signal_t sig{signals[i]};
+        while (hsa_signal_load_scacquire(sig) >= 1) {
+            if (timeout_ns != 0 && std::chrono::steady_clock::now() >= deadline) return SF_ETIMEDOUT;
+            std::this_thread::sleep_for(std::chrono::microseconds(50));
+        }
+    }
     uint64_t t0 = UINT64_MAX, t1 = 0;
     int rc = SF_OK;
     for (int i = 0; i < nsignals; ++i) {
         if (signals[i] == 0) continue;
         hsa_signal_t sig{signals[i]};
-        // Poll with short sleeps: an SDMA completion does not reliably wake
-        // a thread blocked in the runtime's interrupt wait (measured: a
-        // blocked wait returned 350 ms after the copy had finished).
-        while (hsa_signal_load_scacquire(sig) >= 1) {
-            std::this_thread::sleep_for(std::chrono::microseconds(50));
-        }
         if (start_ns != nullptr && end_ns != nullptr) {
             hsa_amd_profiling_async_copy_time_t tm;
             if (hsa_amd_profiling_get_async_copy_time(sig, &tm) == HSA_STATUS_SUCCESS && tm.end > 0) {

@@ -5,9 +5,11 @@ Reference distributed_sync.py:313-377.  With one GPU the reference picks
 of the gradients (``reduce_gradients_to_master``).  Here those copies are
 issued by ``layer_state`` itself on dedicated streams, so ``NoOpSync`` only
 keeps the reference's object and method names for code that calls them
-directly.  Several GPUs (``DistributedSync``: shard-mode all-gather, grad
-reduce) are not part of this build; ``create_distributed_sync`` raises when a
-multi-rank process group is initialised.
+directly; ``SlideFSDP.close`` calls its ``cleanup`` as the reference's
+``__del__`` does (slide_fsdp.py:744).  Several GPUs (``DistributedSync``:
+shard-mode all-gather, grad reduce) are not part of this build;
+``create_distributed_sync`` raises when a multi-rank process group is
+initialised.
 """
 
 from __future__ import annotations
@@ -29,6 +31,8 @@ class NoOpSync:
         self.world_size = 1
         self.rank = 0
         self.is_distributed = False
+        # the reference reads it for its CPU-side barriers (layer_state.py:270, 433)
+        self.cpu_group = None
 
     def gather_params_to_gpu(self, cpu_params: torch.Tensor, gpu_buffer: torch.Tensor, layer_state=None) -> None:
         n = cpu_params.numel()
@@ -40,9 +44,6 @@ class NoOpSync:
         torch.cuda.current_stream().synchronize()
 
     sync_gradients_to_cpu = reduce_gradients_to_master
-
-    def barrier(self) -> None:
-        pass
 
     def cleanup(self) -> None:
         pass

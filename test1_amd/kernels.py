@@ -330,9 +330,39 @@ def memcpy_async(dst: torch.Tensor, src: torch.Tensor, stream: Optional[torch.cu
 # SDMA device -> pinned host copies (not stream-ordered; see include/slidefsdp.h)
 # ---------------------------------------------------------------------------
 _dma_ready = set()
+# Routing mode last set through ``dma_set_avoid_held`` (0: off).
+_avoid_held_mode = 0
+
+
+def avoid_held_from_env(value: Optional[str]) -> int:
+    """The routing mode an ``SF_DMA_AVOID_HELD`` value asks for: unset or
+    empty is 0; otherwise an integer in 0..2 (``ValueError`` for anything
+    else)."""
+    if value is None or value.strip() == "":
+        return 0
+    try:
+        mode = int(value.strip())
+    except ValueError:
+        raise ValueError(f"SF_DMA_AVOID_HELD={value!r}: expected 0, 1 or 2") from None
+    if mode not in (0, 1, 2):
+        raise ValueError(f"SF_DMA_AVOID_HELD={value!r}: expected 0, 1 or 2")
+    return mode
+
+
+ROUTING_DISABLED = (
+    "SDMA engine routing (SF_DMA_AVOID_HELD 1 or 2, sf_dma_set_avoid_held) is disabled for training: with it "
+    "on, the step-1 gradients of the full-size Qwen2.5-14B step differed from a non-offloaded run's in about a "
+    "third of the test runs, for a cause not found; unset SF_DMA_AVOID_HELD or set it to 0")
 
 
 def dma_init(device: Optional[torch.device] = None) -> None:
+    """Bind the SDMA copies to ``device`` (once per process); engines from
+    ``SF_DMA_ENGINES`` (e.g. "2,3") if set.  ``SF_DMA_AVOID_HELD`` other than
+    0 raises ``RuntimeError``: engine routing is disabled (see
+    ``ROUTING_DISABLED``)."""
+    mode = avoid_held_from_env(os.environ.get("SF_DMA_AVOID_HELD"))
+    if mode != 0:
+        raise RuntimeError(ROUTING_DISABLED)
     idx = (device.index if device is not None and device.index is not None else torch.cuda.current_device())
     if idx in _dma_ready:
         return
@@ -343,10 +373,15 @@ def dma_init(device: Optional[torch.device] = None) -> None:
         for e in env.split(","):
             mask |= 1 << int(e)
         _native.check(_native.hip().sf_dma_set_engines(mask), "sf_dma_set_engines")
-    mode = os.environ.get("SF_DMA_AVOID_HELD", "")
-    if mode not in ("", "1"):
-        _native.check(_native.hip().sf_dma_set_avoid_held(int(mode)), "sf_dma_set_avoid_held")
     _dma_ready.add(idx)
+
+
+def require_routing_off() -> None:
+    """Raise ``RuntimeError`` if engine routing is on (set through
+    ``dma_set_avoid_held`` or the environment): the training runtime does
+    not run with it."""
+    if _avoid_held_mode != 0 or avoid_held_from_env(os.environ.get("SF_DMA_AVOID_HELD")) != 0:
+        raise RuntimeError(ROUTING_DISABLED)
 
 
 def dma_engines() -> list:
@@ -369,8 +404,11 @@ def dma_set_engines(engines: Sequence[int]) -> None:
 def dma_set_avoid_held(mode: int) -> None:
     """Route device -> host copies around engines another client holds: 0 no
     (default), 1 onto free engines 0-3, 2 also onto slower free engines from
-    4 up when none of 0-3 is free."""
+    4 up when none of 0-3 is free.  For single-copy tests of the engine
+    choice only: ``SlideFSDP`` refuses to run while it is not 0."""
+    global _avoid_held_mode
     _native.check(_native.hip().sf_dma_set_avoid_held(int(mode)), "sf_dma_set_avoid_held")
+    _avoid_held_mode = int(mode)
 
 
 def dma_enable_timing(on: bool) -> None:
@@ -502,10 +540,16 @@ class DmaReady:
             return dma_wait(self.handle)
 
 
-def dma_wait(handle) -> Tuple[int, int]:
-    """Wait for the copies of ``handle``; returns (start_ns, end_ns) when timing
-    is enabled, else (0, 0)."""
+def dma_wait(handle, timeout: Optional[float] = None) -> Tuple[int, int]:
+    """Wait for the copies of ``handle`` (at most ``timeout`` seconds, then
+    ``DmaCopiesOutstanding`` with every copy still held; None: no limit)
+    and release them; returns (start_ns, end_ns) when timing is enabled,
+    else (0, 0)."""
     handles, n = handle
     t0, t1 = ctypes.c_uint64(0), ctypes.c_uint64(0)
-    _native.check(_native.hip().sf_dma_wait(handles, n, ctypes.byref(t0), ctypes.byref(t1)), "sf_dma_wait")
+    ns = 0 if timeout is None else max(1, int(timeout * 1e9))
+    rc = _native.hip().sf_dma_wait(handles, n, ns, ctypes.byref(t0), ctypes.byref(t1))
+    if rc == _native.SF_ETIMEDOUT:
+        raise DmaCopiesOutstanding(f"{n} SDMA copies not complete after {timeout:g} s")
+    _native.check(rc, "sf_dma_wait")
     return t0.value, t1.value

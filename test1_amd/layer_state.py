@@ -109,6 +109,9 @@ class StreamingRuntime:
         self.d2h_engine = d2h_engine
         if d2h_engine == "sdma":
             kernels.dma_init(device)
+            # SDMA engine routing coincided with wrong step-1 gradients at
+            # full size, cause not found: the runtime does not run with it.
+            kernels.require_routing_off()
         # Host AdamW team size (0: leave the library's setting alone); see
         # set_adam_threads.
         self.adam_threads = 0

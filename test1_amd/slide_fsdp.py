@@ -855,6 +855,7 @@ class SlideFSDP(nn.Module):
                 self._spill = None
             if self.layer_optimizer.offloader is not None:
                 self.layer_optimizer.offloader.flush()
+            self.dist_sync.cleanup()
 
     def __del__(self):
         rt = getattr(self, "runtime", None)

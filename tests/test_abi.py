@@ -40,7 +40,7 @@ def test_error_strings_and_version():
     from test1_amd import _native
 
     hip, cpu = _native.hip(), _native.cpu()
-    assert hip.sf_abi_version() == cpu.sf_abi_version() == 2
+    assert hip.sf_abi_version() == cpu.sf_abi_version() == 3
     assert b"invalid" in hip.sf_error_string(9001)
     assert b"optimizer" in cpu.sf_error_string(9004)
 

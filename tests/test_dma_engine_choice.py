@@ -79,3 +79,84 @@ def test_choice_invariants_over_random_masks(choose):
         assert bin(got).count("1") <= 2 * bin(preferred).count("1")
         if extra & ~0xF:
             assert mode == 2 and not (got & preferred & ~held) and not fast, "slow engines only when no fast one"
+
+
+# ---------------------------------------------------------------------------
+# SF_DMA_AVOID_HELD: parsed strictly, and any mode but 0 refused for training
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("value,mode", [(None, 0), ("", 0), ("  ", 0), ("0", 0), ("1", 1), ("2", 2), (" 2 ", 2)])
+def test_avoid_held_env_values(value, mode):
+    from test1_amd import kernels
+    assert kernels.avoid_held_from_env(value) == mode
+
+
+@pytest.mark.parametrize("value", ["3", "-1", "yes", "1.5", "0x1"])
+def test_avoid_held_env_rejects_other_values(value):
+    from test1_amd import kernels
+    with pytest.raises(ValueError, match="SF_DMA_AVOID_HELD"):
+        kernels.avoid_held_from_env(value)
+
+
+class _InitStub:
+    """The sf_dma_* entry points dma_init calls, recording them."""
+
+    def __init__(self):
+        self.calls = []
+
+    def sf_dma_init(self, dev):
+        self.calls.append(("init", dev))
+        return 0
+
+    def sf_dma_set_engines(self, mask):
+        self.calls.append(("engines", mask))
+        return 0
+
+    def sf_dma_set_avoid_held(self, mode):
+        self.calls.append(("avoid_held", mode))
+        return 0
+
+
+@pytest.mark.parametrize("value", ["1", "2"])
+def test_dma_init_refuses_routing(monkeypatch, value):
+    """Mode 1 used to be skipped silently and mode 2 turned routing on; both
+    now raise before the library is touched."""
+    from test1_amd import _native, kernels
+    stub = _InitStub()
+    monkeypatch.setattr(_native, "hip", lambda: stub)
+    monkeypatch.setattr(kernels, "_dma_ready", set())
+    monkeypatch.setenv("SF_DMA_AVOID_HELD", value)
+    with pytest.raises(RuntimeError, match="routing"):
+        kernels.dma_init(__import__("torch").device("cuda", 0))
+    assert stub.calls == []
+
+
+@pytest.mark.parametrize("value", [None, "", "0"])
+def test_dma_init_with_routing_off(monkeypatch, value):
+    from test1_amd import _native, kernels
+    stub = _InitStub()
+    monkeypatch.setattr(_native, "hip", lambda: stub)
+    monkeypatch.setattr(kernels, "_dma_ready", set())
+    if value is None:
+        monkeypatch.delenv("SF_DMA_AVOID_HELD", raising=False)
+    else:
+        monkeypatch.setenv("SF_DMA_AVOID_HELD", value)
+    monkeypatch.setenv("SF_DMA_ENGINES", "4,5")
+    kernels.dma_init(__import__("torch").device("cuda", 3))
+    assert stub.calls == [("init", 3), ("engines", (1 << 4) | (1 << 5))]
+    kernels.require_routing_off()
+
+
+def test_runtime_refuses_routing_set_through_the_api(monkeypatch):
+    from test1_amd import _native, kernels
+    stub = _InitStub()
+    monkeypatch.setattr(_native, "hip", lambda: stub)
+    monkeypatch.delenv("SF_DMA_AVOID_HELD", raising=False)
+    monkeypatch.setattr(kernels, "_avoid_held_mode", 0)
+    kernels.dma_set_avoid_held(2)
+    try:
+        with pytest.raises(RuntimeError, match="routing"):
+            kernels.require_routing_off()
+    finally:
+        kernels.dma_set_avoid_held(0)
+    kernels.require_routing_off()

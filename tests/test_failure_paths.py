@@ -32,7 +32,9 @@ class _StubHip:
         done._obj.value = int(self.polls_to_done is not None and self.queries >= self.polls_to_done)
         return 0
 
-    def sf_dma_wait(self, handles, n, t0, t1):
+    def sf_dma_wait(self, handles, n, timeout_ns, t0, t1):
+        if self.polls_to_done is None and timeout_ns:
+            return _native.SF_ETIMEDOUT       # still pending at the deadline: nothing released
         self.waited.append([handles[i] for i in range(n)])
         return 0
 
@@ -67,6 +69,15 @@ def test_dma_ready_wait_is_bounded(monkeypatch):
     r = kernels.DmaReady((handles, 1), timeout=0.05)
     with pytest.raises(kernels.DmaCopiesOutstanding):
         r.release()
+    assert stub.waited == []
+
+
+def test_dma_wait_deadline_keeps_the_copies(monkeypatch):
+    stub = _StubHip(polls_to_done=None)
+    monkeypatch.setattr(_native, "hip", lambda: stub)
+    handles = (kernels.ctypes.c_uint64 * 2)(5, 6)
+    with pytest.raises(kernels.DmaCopiesOutstanding):
+        kernels.dma_wait((handles, 2), timeout=0.01)
     assert stub.waited == []
 
 

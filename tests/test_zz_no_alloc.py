@@ -70,3 +70,34 @@ def test_noalloc_stage_matches_workspace_stage(dev):
     x, a = bufs[1][0], bufs[1][1]
     rc = lib.sf_stage_f32_bf16_noalloc(x.data_ptr(), a.data_ptr(), x.numel(), scratch + 8, st.cuda_stream)
     assert rc == _native.SF_ETOOBIG and b"scratch" in lib.sf_error_string(rc)
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(dev):
+    """Calls on two streams, issued back to back with nothing between them on
+    the host: the second call's copies into the shared scratch buffer wait
+    for the first call's last cast (the library's ordering event), so both
+    outputs are the oracle's cast.  Without that ordering the second
+    stream's copies would overwrite pieces the first stream had not cast."""
+    lib = _native.hip()
+    scratch = _native.SF_STAGE_SCRATCH_ELEMS
+    g = torch.Generator().manual_seed(12)
+    sizes = (3 * scratch + 17, 2 * scratch + 5)
+    xs, outs = [], []
+    for n in sizes:
+        x = pinned_empty(n, torch.float32)
+        x.copy_(torch.randn(n, generator=g) * 0.02)
+        xs.append(x)
+        outs.append(torch.full((n + 8,), 7.0, dtype=torch.bfloat16, device=dev))
+    streams = [torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)]
+    torch.cuda.synchronize()
+    for rnd in range(2):
+        for k, (x, out, st) in enumerate(zip(xs, outs, streams)):
+            print(f"round {rnd} call {k}: {x.numel()} elements on stream {k}", flush=True)
+            assert lib.sf_stage_f32_bf16_noalloc(x.data_ptr(), out.data_ptr(), x.numel(), 0, st.cuda_stream) == 0
+        torch.cuda.synchronize()
+        for k, (x, out) in enumerate(zip(xs, outs)):
+            n = x.numel()
+            assert np.array_equal(_bits(out[:n]), oracle.cast_f32_bf16(x.numpy())), f"round {rnd} call {k}"
+            assert bool((out[n:] == 7.0).all()), f"round {rnd} call {k}: wrote past the end"
+            out.fill_(7.0)
+        torch.cuda.synchronize()

@@ -156,9 +156,9 @@ class StreamingRuntime:
         # has landed, and each updated piece is copied to the device while
         # the next one is being updated.
         self.piece_elems = 0
-        # Units staged after their update (fp32 H2D) are cast where they are
-        # next used, on that stream between its kernels, instead of on the
-        # cast stream as soon as their copy lands.
+        # fp32 H2D: units are copied whole into a device fp32 slot and cast
+        # where they are next used, on that stream between its kernels,
+        # instead of on the cast stream as soon as their copy lands.
         self.cast_at_use = False
         self.wait_timeout = wait_timeout
         self.trace: Optional[List[Tuple]] = None
@@ -543,6 +543,24 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
             self._h2d_done = unit["ready"] if skip else stager.load(self._cpu_params_bf16, unit["param"], unit["ready"])
             self._bind_unit(unit, is_backward)
             return
+        if not skip and self.runtime.cast_at_use:
+            # The whole unit is copied into a device fp32 slot now, before the
+            # pool wait, and cast where it is used (``wait_for_h2d``, on the
+            # forward's or the backward's stream right before the unit's
+            # kernels), so the cast does not share the HBM with the GEMMs of
+            # the unit computing meanwhile.
+            pc = stager.copy_for_later(self._cpu_params_flat, None)
+            if pc is not None:
+                try:
+                    unit = self._acquire_unit()
+                except BaseException:
+                    stager.drop_pending(pc)
+                    raise
+                pc.wait_event = unit["ready"]   # the unit's previous reader
+                self._drop_pending_cast()
+                self._pending_cast, self._h2d_done = pc, None
+                self._bind_unit(unit, is_backward)
+                return
         ticket = None if skip else stager.begin(self._cpu_params_flat)
         try:
             unit = self._acquire_unit()

@@ -207,15 +207,18 @@ class SlideFSDP(nn.Module):
                          starts, while the host AdamW would otherwise wait
                          for the first gradients; the batch's rows follow
                          once their gradient has landed.  Same bits.
-      cast_at_use        True (default): with fp32 H2D, a unit staged right
-                         after its update is copied into a device fp32 slot
-                         of its own size, and its cast to bf16 runs where the
-                         unit is next used, on the forward's stream between
-                         its kernels, with the HBM to itself.  False: the cast
+      cast_at_use        True (default): with fp32 H2D, a unit's fp32 master
+                         is copied into a device fp32 slot of its own size
+                         (right after its update for a unit with its own
+                         buffer, else when the unit is loaded), and its cast
+                         to bf16 runs where the unit is next used, on the
+                         forward's or the backward's stream right before its
+                         kernels, with the HBM to itself.  False: the cast
                          runs on a stream of its own as soon as the copy has
-                         landed, mostly beside the backward's GEMMs.  Same
-                         bits; costs up to 4 bytes of HBM per parameter (at
-                         most a quarter of the device memory, else the ring).
+                         landed, beside the GEMMs of the unit computing
+                         meanwhile.  Same bits; costs up to 4 bytes of HBM
+                         per parameter (at most a quarter of the device
+                         memory, else the ring).
     """
 
     def __init__(self, model, config: SlideFSDPConfig, *, stage_chunk_elems: Optional[int] = None,

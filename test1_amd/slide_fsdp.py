@@ -577,27 +577,7 @@ class SlideFSDP(nn.Module):
                 labels: Optional[torch.Tensor] = None, **kwargs) -> CausalLMOutputWithPast:
         """One training step (reference slide_fsdp.py:507-640)."""
         batch_size, seq_length = input_ids.shape
-        hidden_size = self.model_config.hidden_size
-        if self._ring_grow_pending:
-            self._ring_grow_pending = False
-            self._drain()
-            self._grow_grad_ring()
-        # Pinned buffers sized by the batch are allocated here, before the
-        # step's first copy; the ones they replace may still be read or
-        # written by the previous step's copies and updates, so those finish
-        # first.
-        act_alloc = (self.config.ac_offload_mode == "cpu" and self.config.enable_activation_checkpoint
-                     and (self.layer_tensors is None
-                          or self.layer_tensors[0][0].shape != (batch_size, seq_length, hidden_size)))
-        embed_rows = self.layer_states[0].row_sparse and not self.layer_states[0].host_buffers_fit(input_ids.numel())
-        if act_alloc or embed_rows:
-            if (act_alloc and self.layer_tensors is not None) or (
-                    embed_rows and self.layer_states[0].has_host_buffers()):
-                self._drain()
-            if act_alloc:
-                self._allocate_activation_tensors(batch_size, seq_length, hidden_size)
-            if embed_rows:
-                self.layer_states[0].alloc_host_buffers(input_ids.numel())
+        self._prepare_host_buffers(batch_size, seq_length)
         self._act_ring.reset()
 
         embed_state = self.layer_states[0]
@@ -692,6 +672,31 @@ class SlideFSDP(nn.Module):
             if isinstance(self.runtime.grad_ring, GradSlotRing) and not self._ring_grown:
                 self._ring_grow_pending = True
         return CausalLMOutputWithPast(loss=loss, logits=logits)
+
+    def _prepare_host_buffers(self, batch_size: int, seq_length: int) -> None:
+        """Before a step's first copy: widen the gradient slot ring once (after
+        the first step), and pin the buffers sized by the batch (checkpoint
+        slots, embedding row buffers) on the first step or for a new batch
+        shape.  Pinned memory is allocated only after ``_drain``, with no copy
+        into or out of pinned memory in flight: copies of a previous step, or
+        of forwards without a backward, may still run, and pinning near the
+        driver's limit while copies ran has left wrong results."""
+        hidden_size = self.model_config.hidden_size
+        if self._ring_grow_pending:
+            self._ring_grow_pending = False
+            self._drain()
+            self._grow_grad_ring()
+        act_alloc = (self.config.ac_offload_mode == "cpu" and self.config.enable_activation_checkpoint
+                     and (self.layer_tensors is None
+                          or self.layer_tensors[0][0].shape != (batch_size, seq_length, hidden_size)))
+        embed_rows = (self.layer_states[0].row_sparse
+                      and not self.layer_states[0].host_buffers_fit(batch_size * seq_length))
+        if act_alloc or embed_rows:
+            self._drain()
+            if act_alloc:
+                self._allocate_activation_tensors(batch_size, seq_length, hidden_size)
+            if embed_rows:
+                self.layer_states[0].alloc_host_buffers(batch_size * seq_length)
 
     def _after_failed_backward(self) -> None:
         """The backward raised part-way (a hook, an out-of-memory error, an

@@ -528,8 +528,9 @@ def link_stats(r: dict, steps: int, alone: Optional[dict] = None) -> dict:
         # copy's rate while the other direction is busy too, the one-way
         # copy's rate while it is not.
         model_bytes = None
-        if measured and duplex and busy_ns > 0:
-            model_bytes = both_ns * duplex[f"{d}_gbs"] + (busy_ns - both_ns) * measured
+        dup = (duplex or {}).get(f"{d}_gbs")
+        if measured and dup and busy_ns > 0:
+            model_bytes = both_ns * dup + (busy_ns - both_ns) * measured
         out[d] = {
             "bytes_per_step": nbytes / steps,
             "bytes_per_step_by_kind": {k: sum(sp[2] for sp in v) / steps for k, v in parts.items()},
@@ -538,7 +539,7 @@ def link_stats(r: dict, steps: int, alone: Optional[dict] = None) -> dict:
             "gbs_while_busy": gbs,
             "frac": None if gbs is None else gbs / LINK_PEAK_GBS,
             "frac_of_measured_copy": None if gbs is None or not measured else gbs / measured,
-            "frac_of_duplex_copy": None if gbs is None or not duplex else gbs / duplex[f"{d}_gbs"],
+            "frac_of_duplex_copy": None if gbs is None or not dup else gbs / dup,
             "frac_of_copy_model": None if not model_bytes else nbytes / model_bytes,
             "busy_frac_of_step": busy_ns * 1e-9 / r["elapsed"],
             "under_compute_frac": (_overlap(u, comp) / busy_ns) if (busy_ns > 0 and lk["common_clock"]) else None,
@@ -827,39 +828,51 @@ def activation_round_trip(dev, L: int = 32, shape=(4, 1024, 4096), rounds: int =
 
 
 def link_duplex(dev, nbytes: int = 1 << 30, reps: int = 4) -> dict:
-    """Plain pinned copies of ``nbytes`` in both directions at once, on two
-    streams (``reps`` each after one warmup each): the rate each direction
-    keeps while the other is busy, the ceiling of a step whose copies run in
-    both directions together."""
+    """Both directions at once, with the step's own copy paths: ``reps``
+    host-to-device copies of ``nbytes`` (hipMemcpyAsync on a stream, as the
+    parameter copies) and, issued right behind them, ``reps`` device-to-host
+    copies of ``nbytes`` on the SDMA engines of the gradient copies.  Each
+    direction's rate over its own span (HIP events; SDMA engine timestamps),
+    and the share of the device-to-host span the host-to-device copies
+    covered: the rate each direction keeps while the other is busy."""
     import torch
 
+    from test1_amd import kernels
     from test1_amd.pinned import pinned_empty
 
+    kernels.dma_init(dev)
+    kernels.dma_enable_timing(True)
     h_src = pinned_empty(nbytes, torch.uint8)
-    h_dst = pinned_empty(nbytes, torch.uint8)
+    h_dst = pinned_empty(reps * nbytes, torch.uint8)
     h_src.fill_(1)
     d_dst = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     d_src = torch.ones(nbytes, dtype=torch.uint8, device=dev)
-    s_up, s_down = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
-    with torch.cuda.stream(s_up):
+    up = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(up):
         d_dst.copy_(h_src, non_blocking=True)
-    with torch.cuda.stream(s_down):
-        h_dst.copy_(d_src, non_blocking=True)
+    kernels.DmaReady(kernels.dma_copy_d2h([(d_src, h_dst[:nbytes])]), timeout=60).release()
     torch.cuda.synchronize()
-    go = torch.cuda.Event(enable_timing=True)
-    go.record()
-    ends = {}
-    for name, st, (dst, src) in (("h2d", s_up, (d_dst, h_src)), ("d2h", s_down, (h_dst, d_src))):
-        st.wait_event(go)
-        with torch.cuda.stream(st):
-            for _ in range(reps):
-                dst.copy_(src, non_blocking=True)
-        e = torch.cuda.Event(enable_timing=True)
-        e.record(st)
-        ends[name] = e
+    anchor = torch.cuda.Event(enable_timing=True)
+    anchor.record(up)
+    anchor.synchronize()
+    anchor_ns = kernels.dma_clock_ns()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(up)
+    with torch.cuda.stream(up):
+        for _ in range(reps):
+            d_dst.copy_(h_src, non_blocking=True)
+    e1.record(up)
+    handle = kernels.dma_copy_d2h([(d_src, h_dst[k * nbytes:(k + 1) * nbytes]) for k in range(reps)])
+    t0, t1 = kernels.DmaReady(handle, timeout=60).release()
     torch.cuda.synchronize()
-    out = {f"{d}_gbs": nbytes * reps / (go.elapsed_time(e) * 1e-3) / 1e9 for d, e in ends.items()}
-    out["aggregate_gbs"] = out["h2d_gbs"] + out["d2h_gbs"]
+    h2d_s = (anchor_ns + anchor.elapsed_time(e0) * 1e6, anchor_ns + anchor.elapsed_time(e1) * 1e6)
+    out = {"h2d_gbs": nbytes * reps / ((h2d_s[1] - h2d_s[0]) * 1e-9) / 1e9}
+    if t1 > t0:
+        out["d2h_gbs"] = nbytes * reps / ((t1 - t0) * 1e-9) / 1e9
+        out["d2h_span_under_h2d_frac"] = max(0.0, min(t1, h2d_s[1]) - max(t0, h2d_s[0])) / (t1 - t0)
+        out["aggregate_gbs"] = out["h2d_gbs"] + out["d2h_gbs"]
+    out["note"] = ("host-to-device: hipMemcpyAsync on a stream; device-to-host: the gradient copies' SDMA "
+                   "engines, issued right after; each rate over its own span")
     del h_src, h_dst, d_dst, d_src
     torch.cuda.empty_cache()
     return out

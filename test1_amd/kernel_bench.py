@@ -15,6 +15,11 @@ Default N is one Llama-3-8B decoder layer (218,112,000 parameters).
 With ``--rotate K`` the cast cycles through K source/destination pairs, so
 that a launch does not find its input in the 256 MB Infinity Cache left by
 the previous one (pick K with K * 6 * N well above that size for small N).
+
+With ``--gap-ms G`` the cast is also timed alone after G ms with the GPU
+idle before each launch (a host sleep after a synchronisation), as a unit's
+cast runs in a step whose compute stream waited for the unit's copy: each
+launch timed by the events the runtime stamps around the kernel itself.
 """
 
 from __future__ import annotations
@@ -46,6 +51,10 @@ def main(argv=None):
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--rotate", type=int, default=1, help="source/destination pairs the cast cycles through")
+    ap.add_argument("--gap-ms", type=float, default=0.0,
+                    help="also time the cast after this many ms of idle GPU before each launch")
+    ap.add_argument("--beside-h2d", action="store_true",
+                    help="also time the cast while a host-to-device copy runs on another stream")
     args = ap.parse_args(argv)
     n, reps = args.elements, args.reps
     dev = torch.device("cuda", 0)
@@ -75,6 +84,48 @@ def main(argv=None):
     ms = _time(cast_next, s, reps)
     res["cast"] = {"ms": ms, "GB/s": 6 * n / ms / 1e6, "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS,
                    "algorithmic_bytes": 6 * n, "rotated_pairs": len(pairs)}
+    if args.gap_ms > 0:
+        import time
+
+        timers = []
+        for k in range(reps):
+            torch.cuda.synchronize()
+            time.sleep(args.gap_ms * 1e-3)
+            t = kernels.KernelTimer()
+            a, b = pairs[k % len(pairs)]
+            kernels.cast_f32_bf16_(b, a, s, timer=t)
+            timers.append(t)
+        torch.cuda.synchronize()
+        each = [t.elapsed_ms() for t in timers]
+        ms = sum(each) / len(each)
+        res["cast_after_idle"] = {"gap_ms": args.gap_ms, "ms": ms, "min_ms": min(each), "max_ms": max(each),
+                                  "GB/s": 6 * n / ms / 1e6, "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS}
+        timers = []
+        for k in range(reps):
+            t = kernels.KernelTimer()
+            a, b = pairs[k % len(pairs)]
+            kernels.cast_f32_bf16_(b, a, s, timer=t)
+            timers.append(t)
+        torch.cuda.synchronize()
+        ms = sum(t.elapsed_ms() for t in timers) / reps
+        res["cast_back_to_back"] = {"ms": ms, "GB/s": 6 * n / ms / 1e6, "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS}
+    if args.beside_h2d:
+        other = torch.cuda.Stream(device=dev)
+        dev_w2 = torch.empty(n, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(other):
+            for _ in range(4):       # ~65 ms of copying, longer than the casts below
+                dev_w2.copy_(host_w, non_blocking=True)
+        timers = []
+        for k in range(reps):
+            t = kernels.KernelTimer()
+            a, b = pairs[k % len(pairs)]
+            kernels.cast_f32_bf16_(b, a, s, timer=t)
+            timers.append(t)
+        torch.cuda.synchronize()
+        ms = sum(t.elapsed_ms() for t in timers) / reps
+        res["cast_beside_h2d"] = {"ms": ms, "GB/s": 6 * n / ms / 1e6, "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS}
+        del dev_w2
     ms = _time(lambda: cp_dst.copy_(cp_src), s, reps)
     res["copy"] = {"ms": ms, "GB/s": 8 * half / ms / 1e6, "bytes_read": 4 * half, "bytes_written": 4 * half}
     ms = _time(lambda: kernels.pack_b16([g], host_g, s, max_workgroups=16), s, max(1, reps // 4))

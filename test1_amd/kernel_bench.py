@@ -55,6 +55,8 @@ def main(argv=None):
                     help="also time the cast after this many ms of idle GPU before each launch")
     ap.add_argument("--beside-h2d", action="store_true",
                     help="also time the cast while a host-to-device copy runs on another stream")
+    ap.add_argument("--beside-sdma-d2h", action="store_true",
+                    help="also time the cast while device-to-host copies run on the gradient SDMA engines")
     args = ap.parse_args(argv)
     n, reps = args.elements, args.reps
     dev = torch.device("cuda", 0)
@@ -126,6 +128,26 @@ def main(argv=None):
         ms = sum(t.elapsed_ms() for t in timers) / reps
         res["cast_beside_h2d"] = {"ms": ms, "GB/s": 6 * n / ms / 1e6, "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS}
         del dev_w2
+    if args.beside_sdma_d2h:
+        kernels.dma_init(dev)
+        host_big = pinned_empty(4 * n, torch.bfloat16)
+        src_big = torch.ones(n, dtype=torch.bfloat16, device=dev)
+        torch.cuda.synchronize()
+        # ~4 x 436 MB at ~50 GB/s: longer than the casts below
+        handle = kernels.dma_copy_d2h([(src_big, host_big[k * n:(k + 1) * n]) for k in range(4)])
+        timers = []
+        for k in range(reps):
+            t = kernels.KernelTimer()
+            a, b = pairs[k % len(pairs)]
+            kernels.cast_f32_bf16_(b, a, s, timer=t)
+            timers.append(t)
+        torch.cuda.synchronize()
+        busy = not kernels.dma_query(handle)
+        kernels.DmaReady(handle, timeout=60).release()
+        ms = sum(t.elapsed_ms() for t in timers) / reps
+        res["cast_beside_sdma_d2h"] = {"ms": ms, "GB/s": 6 * n / ms / 1e6, "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS,
+                                       "copies_still_running_after_the_casts": busy}
+        del host_big, src_big
     ms = _time(lambda: cp_dst.copy_(cp_src), s, reps)
     res["copy"] = {"ms": ms, "GB/s": 8 * half / ms / 1e6, "bytes_read": 4 * half, "bytes_written": 4 * half}
     ms = _time(lambda: kernels.pack_b16([g], host_g, s, max_workgroups=16), s, max(1, reps // 4))

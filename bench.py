@@ -261,7 +261,8 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
         kw["wait_timeout"] = args.wait_timeout if args.wait_timeout > 0 else None
     sf = SlideFSDP(model, cfg, d2h_engine=d2h_engine, h2d_format=h2d_format, resident_layers=resident_layers,
                    fused_cross_entropy=args.fused_ce, update_piece_elems=args.piece_elems,
-                   cast_at_use=not args.cast_on_copy, early_embedding_update=not args.no_early_embedding, **kw)
+                   cast_at_use=not args.cast_on_copy, early_embedding_update=not args.no_early_embedding,
+                   bf16_reload=False if args.no_bf16_reload else None, **kw)
     uses_storage = args.ac_offload == "nvme" or args.opt_nvme_fraction > 0
     log(f"[bench] SlideFSDP ({h2d_format} H2D, {sf.resident_layers} resident decoders, {d2h_engine} D2H) "
         f"ready in {time.time() - t0:.1f}s")
@@ -329,6 +330,7 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
         "stage_after_update": sf.runtime.stage_after_update,
         "cast_at_use": sf.runtime.cast_at_use,
         "row_sparse_embedding": sf.layer_states[0].row_sparse,
+        "bf16_reload_units": len(sf.bf16_reload_units),
         "layer_numel": sum(p.numel() for p in sf.decoder_layers[0].parameters()),
         "output_numel": sum(p.numel() for p in sf.output_layer.parameters()),
         "storage": storage_stats,
@@ -396,6 +398,7 @@ def variant_summary(v: dict, h2d_format: str, d2h_engine: str, alone: Optional[d
     return {"value": v["tokens"] / v["elapsed"], "ms_per_step": v["elapsed"] / v["steps"] * 1e3,
             "steps": v["steps"], "warmup": v["warmup"], "h2d_format": h2d_format,
             "resident_layers": v["resident_layers"], "d2h_engine": d2h_engine,
+            "bf16_reload_units": v["bf16_reload_units"],
             "cast_frac": None if cast_gbs is None else cast_gbs / HBM_PEAK_GBS,
             "host_link": link_stats(v, v["steps"], alone), "losses": v["losses"],
             "losses_finite": all(math.isfinite(x) for x in v["losses"])}
@@ -981,6 +984,9 @@ def main():
     ap.add_argument("--cast-on-copy", action="store_true",
                     help="cast a unit staged after its update on the cast stream as soon as its copy lands "
                          "(default: where the unit is next used, between the forward's kernels)")
+    ap.add_argument("--no-bf16-reload", action="store_true",
+                    help="units reloaded for their backward come back as fp32 + GPU cast instead of from the "
+                         "bf16 copy their update writes")
     ap.add_argument("--hw-queues", type=int, default=None,
                     help="hardware queues of the HIP runtime (GPU_MAX_HW_QUEUES) for this process, set before "
                          "the first GPU call; 0 keeps the environment's.  Default: 8 for the Llama-3.1-8B "
@@ -1142,6 +1148,7 @@ def main():
                    "stage_after_update": r["stage_after_update"],
                    "update_piece_elems": args.piece_elems,
                    "cast_at_use": r["cast_at_use"],
+                   "bf16_reload_units": r["bf16_reload_units"],
                    "early_embedding_update": not args.no_early_embedding,
                    "row_sparse_embedding": r["row_sparse_embedding"],
                    "ac_offload_mode": args.ac_offload,

@@ -134,6 +134,11 @@ class StreamingRuntime:
             cap = torch.cuda.get_device_properties(device).total_memory // 4
             self.stager = H2DStager(device, stage_chunk_elems, stage_depth, self.h2d_stream, self.cast_stream,
                                     slot_cap_bytes=cap)
+        # bf16 copies on the H2D stream: the loads of bf16 H2D, or the
+        # backward's reloads of units with a bf16 reload copy (fp32 H2D); its
+        # copies are timed in the stager's list
+        self.bf16_loader = (self.stager if h2d_format == "bf16"
+                            else BF16Loader(self.h2d_stream, timing_source=self.stager))
         # Gradient host slots: a ring of ``grad_ring_depth`` max-size slots,
         # or (None) one slot per unit, set up by ``init_grad_slots``.
         self.grad_ring = None if grad_ring_depth is None else GradStagingRing(grad_ring_depth, max_param_size, dtype)
@@ -233,11 +238,18 @@ class StreamingRuntime:
         (yielding there measured 1.5 % slower)."""
         if not self.adam_threads or self.h2d_format != "fp32":
             return
-        few = self.stager.backlog() >= 2
+        few = self.h2d_backlog() >= 2
         n = max(1, (self.adam_threads + 1) // 2) if few else self.adam_threads
         if n != self._adam_threads_set:
             _cpu_adam.set_num_threads(n)
             self._adam_threads_set = n
+
+    def h2d_backlog(self) -> int:
+        """Host-to-device unit copies issued and not yet complete."""
+        n = self.stager.backlog()
+        if self.bf16_loader is not self.stager:
+            n += self.bf16_loader.backlog()
+        return n
 
     def init_grad_slots(self, unit_sizes: Dict[int, int], fallback_depth: int = 3) -> None:
         """One pinned slot per unit; if the host cannot pin that much (the
@@ -391,6 +403,9 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
                     "and this host cannot pin that much"
                 ) from e
             self.refresh_host_copy()
+        # fp32 H2D, units reloaded for their backward: a pinned bf16 copy of
+        # the master that the update keeps current (``enable_bf16_reload``).
+        self._reload_bf16: Optional[torch.Tensor] = None
         self._grad_params = [p for p in self._params if p.requires_grad]
         self._grads_seen = 0
         self._grad_lock = threading.Lock()
@@ -418,12 +433,41 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
         return zip(self._param_maps.items(), self._params)
 
     def refresh_host_copy(self) -> None:
-        """Recompute the bf16 host copy from the fp32 master (bf16 H2D only)
-        and drop a staging made for the next forward.  Updates keep both
-        current; call this after writing the master directly."""
+        """Recompute the bf16 host copy from the fp32 master (bf16 H2D, or the
+        backward's bf16 reload copy) and drop a staging made for the next
+        forward.  Updates keep both current; call this after writing the
+        master directly."""
         self._drop_prefetched()
-        if self._cpu_params_bf16 is not None and self.total_size:
-            _cpu_adam.cast_f32_bf16(self._cpu_params_flat, self._cpu_params_bf16)
+        host = self._bf16_host()
+        if host is not None and self.total_size:
+            _cpu_adam.cast_f32_bf16(self._cpu_params_flat, host)
+
+    def _bf16_host(self) -> Optional[torch.Tensor]:
+        """The pinned bf16 copy of the master that updates rewrite, if any."""
+        return self._cpu_params_bf16 if self._cpu_params_bf16 is not None else self._reload_bf16
+
+    def enable_bf16_reload(self) -> bool:
+        """fp32 H2D: keep a pinned bf16 copy of this unit's master, written by
+        each update in the same pass, and reload the unit for its backward
+        from it: 2 bytes per parameter over the host link instead of 4, and
+        no cast.  Same bits: the master does not change between a unit's
+        forward and its backward, and the copy is the RNE cast of it.  Returns
+        False (the unit keeps reloading fp32) when the host cannot pin it."""
+        if (self._reload_bf16 is not None or self._cpu_params_bf16 is not None or self.row_sparse
+                or not self.backward_reads_params or self.buffer_pool.dtype != torch.bfloat16
+                or self.runtime.h2d_format != "fp32" or not self.total_size):
+            return self._reload_bf16 is not None
+        try:
+            copy = pinned_empty(self.total_size, torch.bfloat16)
+        except _native.NativeError as e:
+            if e.status != _native.HIP_ERROR_OUT_OF_MEMORY:
+                raise
+            return False
+        self.wait_for_update()
+        with self.update_lock:
+            _cpu_adam.cast_f32_bf16(self._cpu_params_flat, copy)
+            self._reload_bf16 = copy
+        return True
 
     def _drop_prefetched(self) -> None:
         """Forget a staging made for the next forward (its master changed): a
@@ -541,6 +585,13 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
         if self._cpu_params_bf16 is not None:
             unit = self._acquire_unit()
             self._h2d_done = unit["ready"] if skip else stager.load(self._cpu_params_bf16, unit["param"], unit["ready"])
+            self._bind_unit(unit, is_backward)
+            return
+        if is_backward and not skip and self._reload_bf16 is not None:
+            # the backward's reload: the bf16 copy the last update wrote
+            unit = self._acquire_unit()
+            self._drop_pending_cast()
+            self._h2d_done = self.runtime.bf16_loader.load(self._reload_bf16, unit["param"], unit["ready"])
             self._bind_unit(unit, is_backward)
             return
         if not skip and self.runtime.cast_at_use:
@@ -874,9 +925,10 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
         return {p: self._param_views[name] for (name, _), p in self._named()}
 
     def _bf16_views(self) -> Optional[Dict[nn.Parameter, torch.Tensor]]:
-        if self._cpu_params_bf16 is None:
+        host = self._bf16_host()
+        if host is None:
             return None
-        return self._grad_views(self._cpu_params_bf16)
+        return self._grad_views(host)
 
     def _grad_views(self, host: torch.Tensor) -> Dict[nn.Parameter, torch.Tensor]:
         views = {}

@@ -219,6 +219,17 @@ class SlideFSDP(nn.Module):
                          meanwhile.  Same bits; costs up to 4 bytes of HBM
                          per parameter (at most a quarter of the device
                          memory, else the ring).
+      bf16_reload        None (default: True with fp32 H2D and bf16 units):
+                         a unit reloaded for its backward (no device buffer
+                         of its own) comes back as bf16 from a pinned bf16
+                         copy of its master, which its update writes in the
+                         same pass, instead of as fp32 plus a cast: half the
+                         host-link bytes of the backward's reloads.  Same
+                         bits (the master does not change between a unit's
+                         forward and its backward).  Costs 2 bytes per
+                         parameter of pinned host memory for those units,
+                         pinned after the gradient slots; units the host
+                         cannot pin reload fp32.
     """
 
     def __init__(self, model, config: SlideFSDPConfig, *, stage_chunk_elems: Optional[int] = None,
@@ -227,7 +238,8 @@ class SlideFSDP(nn.Module):
                  d2h_engine: str = "sdma", h2d_format: str = "fp32",
                  resident_layers: Optional[int] = None, row_sparse_embedding: bool = True,
                  fused_cross_entropy: bool = False, stage_after_update: bool = True,
-                 update_piece_elems: int = 0, cast_at_use: bool = True, early_embedding_update: bool = True):
+                 update_piece_elems: int = 0, cast_at_use: bool = True, early_embedding_update: bool = True,
+                 bf16_reload: Optional[bool] = None):
         super().__init__()
         if config.param_transfer_mode != "full":
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
@@ -268,6 +280,9 @@ class SlideFSDP(nn.Module):
         self.runtime.update_priority = lambda u: 1 - u if u <= 1 else u
         self.runtime.stage_after_update = bool(stage_after_update)
         self._make_resident(self._auto_resident() if resident_layers is None else int(resident_layers))
+        if bf16_reload is None:
+            bf16_reload = h2d_format == "fp32" and self.dtype == torch.bfloat16
+        self.bf16_reload_units = self._enable_bf16_reloads() if bf16_reload else []
         if not config.enable_activation_checkpoint and not self._all_units_own_buffers():
             # Without checkpoints the backward reads the weights the forward
             # saved, so no unit may go back to the 2-unit pool in between
@@ -409,6 +424,22 @@ class SlideFSDP(nn.Module):
             if sum(st.total_size for st in extra) * elem < free // 4:
                 for st in extra:
                     st.make_resident(torch.empty(st.total_size, dtype=self.dtype, device=self.device))
+
+    def _enable_bf16_reloads(self) -> List[int]:
+        """Give every decoder the backward reloads (no device buffer of its
+        own; the last decoder stays loaded) a pinned bf16 copy of its master,
+        until the host cannot pin more.  Returns the units that got one."""
+        n_dec = len(self.layer_states) - 2
+        got = []
+        for st in self.layer_states[1:n_dec]:
+            if st.resident_across_steps:
+                continue
+            if not st.enable_bf16_reload():
+                print(f"SlideFSDP: bf16 reload copies pinned for {len(got)} units; the host cannot pin more, "
+                      f"the others reload their fp32 masters", flush=True)
+                break
+            got.append(st.layer_idx)
+        return got
 
     def _all_units_own_buffers(self) -> bool:
         return all(st._own_unit is not None for st in self.layer_states[1:])

@@ -476,12 +476,27 @@ class BF16Loader:
     interface; there are no casts to fence behind.
     """
 
-    def __init__(self, h2d_stream: torch.cuda.Stream):
+    def __init__(self, h2d_stream: torch.cuda.Stream, timing_source=None):
         self.h2d_stream = h2d_stream
         self._copies: deque = deque()
         self.last_cast_done: Optional[torch.cuda.Event] = None
         self.cast_timing: Optional[list] = None
-        self.copy_timing: Optional[list] = None
+        self._copy_timing: Optional[list] = None
+        # With a ``timing_source`` (the fp32 stager whose backward reloads
+        # this loader takes over), copies are timed in that object's list.
+        self._timing_source = timing_source
+
+    @property
+    def copy_timing(self) -> Optional[list]:
+        src = self._timing_source
+        return self._copy_timing if src is None else src.copy_timing
+
+    @copy_timing.setter
+    def copy_timing(self, value: Optional[list]) -> None:
+        if self._timing_source is None:
+            self._copy_timing = value
+        else:
+            self._timing_source.copy_timing = value
 
     def fence_after_casts(self, stream: torch.cuda.Stream) -> None:
         return None
@@ -493,7 +508,8 @@ class BF16Loader:
             raise ValueError("BF16Loader.load: destination smaller than source")
         if wait_event is not None:
             self.h2d_stream.wait_event(wait_event)
-        timing = self.copy_timing is not None
+        timing_list = self.copy_timing
+        timing = timing_list is not None
         if timing:
             t0 = torch.cuda.Event(enable_timing=True)
             t0.record(self.h2d_stream)
@@ -501,7 +517,7 @@ class BF16Loader:
         done = torch.cuda.Event(enable_timing=True) if timing else _new_event()
         done.record(self.h2d_stream)
         if timing:
-            self.copy_timing.append((t0, done, n * 2))
+            timing_list.append((t0, done, n * 2))
         self._copies.append(done)
         if len(self._copies) > 64:
             _backlog(self._copies)

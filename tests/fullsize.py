@@ -152,6 +152,19 @@ def unit_weight_sums(gm):
             for ps in unit_params(gm)]
 
 
+def master_weight_sums(sf):
+    """Per unit, the checksum of the RNE bf16 cast of SlideFSDP's current
+    fp32 master (torch's CPU cast, the oracle's rounding): the weights a
+    step computes with, taken before the step (after the previous step's
+    updates)."""
+    sf.wait_for_updates()
+    out = []
+    for st in sf.layer_states:
+        m = st._cpu_params_flat
+        out.append(int(m.to(torch.bfloat16).view(torch.int16).sum(dtype=torch.int64)))
+    return out
+
+
 def check_backward_weights(served, sums, units):
     """Each unit's device weights at the start and at the end of its
     backward have the checksum of its bf16 weights in the non-offloaded run

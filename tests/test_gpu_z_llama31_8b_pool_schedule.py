@@ -22,6 +22,10 @@ the weight reloads, as in the reference.
   gradients, every update and moment is the oracle AdamW's bit for bit, and a
   forward after step 3 computes with the oracle's cast of the updated masters
   in the units it leaves loaded (the last decoder and the output unit).
+* The backward's reloads come from the bf16 copies the updates write
+  (``bf16_reload``, the default with fp32 H2D): in every step each unit's
+  weights at the start and end of its backward have the checksum of the RNE
+  cast of its current master, so a copy an update left stale fails.
 
 Host memory ~140 GB; the file sorts after the other GPU tests."""
 
@@ -35,7 +39,8 @@ import torch
 
 from fullsize import (CapturedOracle, check_backward_weights, check_checkpoint_slots, check_masters, check_moments,
                       check_packed_grads, check_served_checkpoints, check_served_side_inputs, check_staged,
-                      check_step1_against_reference, gpu_bf16_copy, reference_step, say, timed, unit_weight_sums)
+                      check_step1_against_reference, gpu_bf16_copy, master_weight_sums, reference_step, say, timed,
+                      unit_weight_sums)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -74,11 +79,14 @@ def test_llama31_8b_reference_schedule_parity(dev):
                wait_timeout=600)
     assert sf.resident_layers == 0 and not any(st.resident_across_steps for st in sf.layer_states)
     assert sf._act_prefetch_stream() is sf.runtime.h2d_stream
+    assert sf.bf16_reload_units == list(range(1, L)), sf.bf16_reload_units
     sf.runtime.capture_units = set(units)
     try:
         for k in range(STEPS):
             sf.runtime.capture = {}
-            sf.runtime.capture_served = {} if k == 0 else None
+            sf.runtime.capture_served = {}
+            if k > 0:
+                sums = timed(f"master checksums before step {k + 1}", master_weight_sums, sf)
             sf.runtime.trace = [] if k == 0 else None
             ids = batches[k].to(dev)
             t = time.time()
@@ -111,6 +119,11 @@ def test_llama31_8b_reference_schedule_parity(dev):
                 del ref_grads
                 say(f"step 1: loss and gradients of units {units} equal the non-offloaded run's bit for bit, and "
                     f"every unit's gradient checksums")
+            else:
+                served, sf.runtime.capture_served = sf.runtime.capture_served, None
+                n_units = len(check_backward_weights(served, sums, range(1, L + 2)))
+                del served
+                say(f"step {k + 1}: the backward of {n_units} units read the cast of their current masters")
             check_packed_grads(cap, units)
             timed(f"oracle step {k + 1}", orc.step, cap)
             check_masters(sf, orc, units)

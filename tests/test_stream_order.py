@@ -143,22 +143,24 @@ def _unit_state(dev, idx, runtime, master):
         layer_idx=idx, runtime=runtime, buffer_pool=runtime.pool, row_sparse=False, _own_unit=None,
         _current_gpu_cache=None, _prefetched=None, _prefetch_lock=threading.Lock(), _pending_cast=None,
         _h2d_done=None, _cpu_params_bf16=None, _cpu_params_flat=master, backward_reads_params=True,
-        _param_maps={}, _params=[], _bwd_compute_done=False, _grads_offloaded=False)
+        _param_maps={}, _params=[], _bwd_compute_done=False, _grads_offloaded=False, _reload_bf16=None)
     st.wait_for_update = lambda timeout=None: None
     return st
 
 
 def _runtime(dev, stager, pool_size=2):
-    from test1_amd.staging import LayerBufferPool
+    from test1_amd.staging import BF16Loader, LayerBufferPool
 
     return SimpleNamespace(stager=stager, pool=LayerBufferPool(N, torch.bfloat16, "cuda:0", pool_size),
+                           bf16_loader=BF16Loader(stager.h2d_stream, timing_source=stager),
                            cast_at_use=True, wait_timeout=1.0, log=lambda *a: None, mark=lambda *a: None)
 
 
-def test_pool_loads_cast_at_use_forward_and_backward(dev):
-    rt = _runtime(dev, _stager(dev))
-    L = 5
-    states = [_unit_state(dev, i, rt, torch.randn(N)) for i in range(L)]
+def _pool_step(dev, rt, states):
+    """One step of the reference's schedule through ``to_device_async`` /
+    ``wait_for_h2d``: forward loads one ahead, backward reloads the unit
+    below before each unit's backward, units released after their use."""
+    L = len(states)
     comp = dev.default
     # forward: the next unit's load issued before this unit's forward
     states[0].to_device_async()
@@ -179,8 +181,40 @@ def test_pool_loads_cast_at_use_forward_and_backward(dev):
         dev.op(comp, reads=[st._current_gpu_cache["param"]], what=f"unit {i} backward")
         st._bwd_compute_done = st._grads_offloaded = True
         st._maybe_release_after_backward()
+
+
+def test_pool_loads_cast_at_use_forward_and_backward(dev):
+    rt = _runtime(dev, _stager(dev))
+    _pool_step(dev, rt, [_unit_state(dev, i, rt, torch.randn(N)) for i in range(5)])
     assert dev.races == []
     assert rt.pool.available() == 2
+
+
+def test_backward_reloads_from_the_bf16_copy(dev):
+    """Units with a bf16 reload copy: the forward's fp32 copy and cast at
+    use, the backward's bf16 copy straight into the pool unit after the
+    unit's last reader."""
+    rt = _runtime(dev, _stager(dev))
+    states = [_unit_state(dev, i, rt, torch.randn(N)) for i in range(5)]
+    for st in states:
+        st._reload_bf16 = torch.zeros(N, dtype=torch.bfloat16)
+    _pool_step(dev, rt, states)
+    assert dev.races == []
+    assert rt.pool.available() == 2
+    assert any("copy on h2d" in a[5] and a[4] for a in dev.accesses)
+
+
+def test_backward_bf16_reload_without_the_units_fence_races(dev, monkeypatch):
+    from test1_amd.staging import BF16Loader
+
+    rt = _runtime(dev, _stager(dev))
+    real = BF16Loader.load
+    monkeypatch.setattr(BF16Loader, "load", lambda self, h, d, w: real(self, h, d, None))
+    states = [_unit_state(dev, i, rt, torch.randn(N)) for i in range(5)]
+    for st in states:
+        st._reload_bf16 = torch.zeros(N, dtype=torch.bfloat16)
+    _pool_step(dev, rt, states)
+    assert any("copy on h2d" in r and "forward" in r for r in dev.races), dev.races
 
 
 # ---------------------------------------------------------------------------
@@ -338,7 +372,7 @@ def _grad_offload(dev, units=3, skip_dma_waits=False):
         st.__dict__.update(runtime=rt, layer_idx=unit, layer_optimizer=opt, update_finished=threading.Event(),
                            update_lock=threading.Lock(), _param_maps={"w": (0, torch.Size([N]), N)}, _params=[p],
                            _param_views={"w": p.data}, _cpu_params_flat=p.data, _cpu_params_bf16=None,
-                           _plan_key=0, _plan=None, total_size=N)
+                           _reload_bf16=None, _plan_key=0, _plan=None, total_size=N)
         st._update_ready = lambda ready: ready
         with dev.as_host("offload"):
             st._d2h_task(None, [(g, 0)], [], ev, None)

@@ -321,11 +321,20 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
             "read_bytes_per_step": rd / n_steps, "write_bytes_per_step": wr / n_steps,
             "busy_frac": busy / elapsed, "gbs_while_busy": (rd + wr) / busy / 1e9 if busy > 0 else None})
         log(f"[bench] storage: {storage_stats}")
+    link = link_timeline(rt, anchor, anchor_ns)
+    if timeline:
+        # the host-link and compute intervals on the host timeline's clock
+        # (ms since the first timed step; the SDMA clock was read at t_start)
+        with open(timeline + ".link.json", "w") as f:
+            json.dump({d: {k: [((a - anchor_ns) * 1e-6, (b - anchor_ns) * 1e-6, n) for a, b, n in v]
+                           for k, v in link[d].items()} for d in ("h2d", "d2h")}
+                      | {"compute": [((a - anchor_ns) * 1e-6, (b - anchor_ns) * 1e-6) for a, b in link["compute"]],
+                         "elapsed_ms": elapsed * 1e3, "steps": n_steps}, f)
     r = {
         "elapsed": elapsed, "losses": losses, "tokens": B * S * n_steps, "steps": n_steps, "warmup": n_warm,
         "cast": elapsed_stats(rt.stager.cast_timing), "ncast": len(rt.stager.cast_timing or []),
         "h2d": elapsed_stats(rt.stager.copy_timing), "d2h": elapsed_stats(rt.d2h_timing),
-        "link": link_timeline(rt, anchor, anchor_ns),
+        "link": link,
         "total_params": sf.total_params, "resident_layers": sf.resident_layers,
         "stage_after_update": sf.runtime.stage_after_update,
         "cast_at_use": sf.runtime.cast_at_use,

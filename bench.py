@@ -322,6 +322,11 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
             "busy_frac": busy / elapsed, "gbs_while_busy": (rd + wr) / busy / 1e9 if busy > 0 else None})
         log(f"[bench] storage: {storage_stats}")
     link = link_timeline(rt, anchor, anchor_ns)
+    h2d_idle = None
+    if timeline and link["common_clock"]:
+        h2d_idle = h2d_idle_attribution([(t - t_start, th, what, u) for t, th, what, u in rt.timeline], link,
+                                        anchor_ns, elapsed)
+        log(f"[bench] H2D idle: {h2d_idle}")
     if timeline:
         # the host-link and compute intervals on the host timeline's clock
         # (ms since the first timed step; the SDMA clock was read at t_start)
@@ -334,7 +339,7 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
         "elapsed": elapsed, "losses": losses, "tokens": B * S * n_steps, "steps": n_steps, "warmup": n_warm,
         "cast": elapsed_stats(rt.stager.cast_timing), "ncast": len(rt.stager.cast_timing or []),
         "h2d": elapsed_stats(rt.stager.copy_timing), "d2h": elapsed_stats(rt.d2h_timing),
-        "link": link,
+        "link": link, "h2d_idle": h2d_idle,
         "total_params": sf.total_params, "resident_layers": sf.resident_layers,
         "stage_after_update": sf.runtime.stage_after_update,
         "cast_at_use": sf.runtime.cast_at_use,
@@ -484,6 +489,49 @@ def link_timeline(rt, anchor, anchor_ns: int) -> dict:
         "common_clock": anchor_ns != 0,
         "untimed_d2h_bytes": sum(rec[1] for rec in rt.d2h_timing or [] if _untimed(rec)),
     }
+
+
+def h2d_idle_attribution(events, link: dict, anchor_ns: int, elapsed_s: float) -> dict:
+    """Where the H2D direction idles in the timed steps: each gap between
+    its transfers (parameter copies, checkpoint prefetches, lookup rows) is
+    attributed to what the copy that ends it waited for.  ``events`` is the
+    host timeline (perf_counter seconds since the first timed step, thread,
+    event, unit); a copy whose issue (``staged_after_update`` by the update
+    thread, ``h2d_issued`` by the forward) came less than 1 ms before it
+    started waited for the host to issue it; one issued earlier waited on the
+    device (its stream's order or an event)."""
+    spans = sorted(((a - anchor_ns) * 1e-6, (b - anchor_ns) * 1e-6) for v in link["h2d"].values() for a, b, _ in v)
+    union = []
+    for a, b in spans:
+        if union and a <= union[-1][1]:
+            union[-1][1] = max(union[-1][1], b)
+        else:
+            union.append([a, b])
+    total = elapsed_s * 1e3
+    issues = sorted((t * 1e3, what) for t, _, what, _ in events if what in ("staged_after_update", "h2d_issued"))
+    out = {"window_ms": total, "idle_ms": 0.0, "waiting_on_device_ms": 0.0, "waiting_for_update_thread_ms": 0.0,
+           "waiting_for_forward_ms": 0.0, "gaps": 0}
+    import bisect
+
+    times = [t for t, _ in issues]
+    prev_end = 0.0
+    for a, b in union + [[total, total]]:
+        gap = min(a, total) - prev_end
+        prev_end = max(prev_end, b)
+        if gap <= 0:
+            continue
+        out["gaps"] += 1
+        out["idle_ms"] += gap
+        k = bisect.bisect_right(times, a + 0.05) - 1
+        if a >= total - 1e-6:
+            continue
+        if k >= 0 and a - times[k] < 1.0:
+            key = "waiting_for_update_thread_ms" if issues[k][1] == "staged_after_update" else "waiting_for_forward_ms"
+        else:
+            key = "waiting_on_device_ms"
+        out[key] += gap
+    out["idle_frac"] = out["idle_ms"] / total if total > 0 else None
+    return out
 
 
 def _union(spans):
@@ -1187,7 +1235,7 @@ def main():
                      + "; alone: one decoder layer's cast on an idle GPU after the timed steps"),
         },
         "roofline_secondary": secondary_rooflines(r, kernels_alone),
-        "host_link": link_stats(r, args.steps, link_alone_gbs),
+        "host_link": dict(link_stats(r, args.steps, link_alone_gbs), h2d_idle=r["h2d_idle"]),
         "model_tflops": {
             "flops_per_step": megatron_flops_per_step(w),
             "tflops": megatron_flops_per_step(w) / (elapsed / args.steps) / 1e12,

@@ -55,6 +55,8 @@ def main(argv=None):
                     help="also time the cast after this many ms of idle GPU before each launch")
     ap.add_argument("--beside-h2d", action="store_true",
                     help="also time the cast while a host-to-device copy runs on another stream")
+    ap.add_argument("--after-h2d", action="store_true",
+                    help="also time the cast right after a host-to-device copy wrote its source (same stream)")
     ap.add_argument("--beside-sdma-d2h", action="store_true",
                     help="also time the cast while device-to-host copies run on the gradient SDMA engines")
     args = ap.parse_args(argv)
@@ -128,6 +130,32 @@ def main(argv=None):
         ms = sum(t.elapsed_ms() for t in timers) / reps
         res["cast_beside_h2d"] = {"ms": ms, "GB/s": 6 * n / ms / 1e6, "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS}
         del dev_w2
+    if args.after_h2d:
+        timers = []
+        for k in range(reps):
+            a, b = pairs[k % len(pairs)]
+            kernels.memcpy_async(a, host_w, s)      # the source freshly written by DMA
+            t = kernels.KernelTimer()
+            kernels.cast_f32_bf16_(b, a, s, timer=t)
+            timers.append(t)
+        torch.cuda.synchronize()
+        ms = sum(t.elapsed_ms() for t in timers) / reps
+        res["cast_after_h2d_of_its_source"] = {"ms": ms, "GB/s": 6 * n / ms / 1e6,
+                                               "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS}
+        # the same launches with the copy into the other pair's source: the
+        # cast reads data written long before
+        timers = []
+        for k in range(reps):
+            a, b = pairs[k % len(pairs)]
+            c, _ = pairs[(k + 1) % len(pairs)]
+            kernels.memcpy_async(c, host_w, s)
+            t = kernels.KernelTimer()
+            kernels.cast_f32_bf16_(b, a, s, timer=t)
+            timers.append(t)
+        torch.cuda.synchronize()
+        ms = sum(t.elapsed_ms() for t in timers) / reps
+        res["cast_after_h2d_of_another_buffer"] = {"ms": ms, "GB/s": 6 * n / ms / 1e6,
+                                                   "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS}
     if args.beside_sdma_d2h:
         kernels.dma_init(dev)
         host_big = pinned_empty(4 * n, torch.bfloat16)

@@ -56,6 +56,7 @@ import torch.nn as nn
 from torch.utils.checkpoint import checkpoint
 from transformers.modeling_outputs import CausalLMOutputWithPast
 
+from . import _native
 from .config import SlideFSDPConfig
 from .distributed_sync import create_distributed_sync
 from .fused_ce import chunked_linear_cross_entropy
@@ -425,20 +426,37 @@ class SlideFSDP(nn.Module):
                 for st in extra:
                     st.make_resident(torch.empty(st.total_size, dtype=self.dtype, device=self.device))
 
-    def _enable_bf16_reloads(self) -> List[int]:
+    def _enable_bf16_reloads(self, reserve_bytes: int = 2 << 30) -> List[int]:
         """Give every decoder the backward reloads (no device buffer of its
         own; the last decoder stays loaded) a pinned bf16 copy of its master,
-        until the host cannot pin more.  Returns the units that got one."""
+        until the host cannot pin more.  ``reserve_bytes`` of pinned memory
+        are held meanwhile, so that the buffers pinned later (checkpoint
+        slots, embedding rows) still fit under the driver's limit.  Returns
+        the units that got one."""
+        from .pinned import pinned_empty
+
         n_dec = len(self.layer_states) - 2
+        todo = [st for st in self.layer_states[1:n_dec] if not st.resident_across_steps]
+        if not todo:
+            return []
+        try:
+            reserve = pinned_empty(reserve_bytes, torch.uint8)
+        except _native.NativeError as e:
+            if e.status != _native.HIP_ERROR_OUT_OF_MEMORY:
+                raise
+            print("SlideFSDP: no pinned memory left for bf16 reload copies; units reload their fp32 masters",
+                  flush=True)
+            return []
         got = []
-        for st in self.layer_states[1:n_dec]:
-            if st.resident_across_steps:
-                continue
-            if not st.enable_bf16_reload():
-                print(f"SlideFSDP: bf16 reload copies pinned for {len(got)} units; the host cannot pin more, "
-                      f"the others reload their fp32 masters", flush=True)
-                break
-            got.append(st.layer_idx)
+        try:
+            for st in todo:
+                if not st.enable_bf16_reload():
+                    print(f"SlideFSDP: bf16 reload copies pinned for {len(got)} units; the host cannot pin more, "
+                          f"the others reload their fp32 masters", flush=True)
+                    break
+                got.append(st.layer_idx)
+        finally:
+            del reserve
         return got
 
     def _all_units_own_buffers(self) -> bool:

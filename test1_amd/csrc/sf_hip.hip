@@ -1044,7 +1044,9 @@ int sf_dma_wait(const uint64_t* signals, int nsignals, uint64_t timeout_ns, uint
     // short sleeps: an SDMA completion does not reliably wake a thread
     // blocked in the runtime's interrupt wait (measured: a blocked wait
     // returned 350 ms after the copy had finished).
-    const auto deadline = std::chrono::steady_clock::now() + std::chrono::nanoseconds(timeout_ns);
+    // at most ~30 years: the signed duration cannot wrap to a deadline in the past
+    const uint64_t capped_ns = timeout_ns < (uint64_t(1) << 60) ? timeout_ns : (uint64_t(1) << 60);
+    const auto deadline = std::chrono::steady_clock::now() + std::chrono::nanoseconds(int64_t(capped_ns));
     for (int i = 0; i < nsignals; ++i) {
         if (signals[i] == 0) continue;
         const hsa_signal_t sig{signals[i]};

@@ -57,6 +57,9 @@ def main(argv=None):
                     help="also time the cast while a host-to-device copy runs on another stream")
     ap.add_argument("--after-h2d", action="store_true",
                     help="also time the cast right after a host-to-device copy wrote its source (same stream)")
+    ap.add_argument("--streamed", action="store_true",
+                    help="also time casts that each wait (cross-stream event) for the copy of their source, with "
+                         "the copies queued back to back on another stream, as in the pool schedule's forward")
     ap.add_argument("--beside-sdma-d2h", action="store_true",
                     help="also time the cast while device-to-host copies run on the gradient SDMA engines")
     args = ap.parse_args(argv)
@@ -156,6 +159,28 @@ def main(argv=None):
         ms = sum(t.elapsed_ms() for t in timers) / reps
         res["cast_after_h2d_of_another_buffer"] = {"ms": ms, "GB/s": 6 * n / ms / 1e6,
                                                    "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS}
+    if args.streamed:
+        up = torch.cuda.Stream(device=dev)
+        torch.cuda.synchronize()
+        evs = []
+        for k in range(reps):
+            a, _ = pairs[k % len(pairs)]
+            if k >= len(pairs):
+                up.wait_event(evs[k - len(pairs)][1])   # the source's previous cast has read it
+            kernels.memcpy_async(a, host_w, up)
+            ev = torch.cuda.Event()
+            ev.record(up)
+            t = kernels.KernelTimer()
+            s.wait_event(ev)
+            kernels.cast_f32_bf16_(pairs[k % len(pairs)][1], a, s, timer=t)
+            done = torch.cuda.Event()
+            done.record(s)
+            evs.append((t, done))
+        torch.cuda.synchronize()
+        each = [t.elapsed_ms() for t, _ in evs]
+        ms = sum(each) / len(each)
+        res["cast_streamed"] = {"ms": ms, "min_ms": min(each), "max_ms": max(each), "GB/s": 6 * n / ms / 1e6,
+                                "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS}
     if args.beside_sdma_d2h:
         kernels.dma_init(dev)
         host_big = pinned_empty(4 * n, torch.bfloat16)

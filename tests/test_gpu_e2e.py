@@ -97,6 +97,24 @@ def test_updates_match_oracle_bit_exact(dev, h2d_format, resident, d2h_engine, r
         resident_layers=resident, d2h_engine=d2h_engine, grad_ring_depth=ring, fused_cross_entropy=fused))
 
 
+@pytest.mark.parametrize("bf16_reload", [False, True])
+def test_pool_schedule_reloads(dev, bf16_reload):
+    """The reference's schedule (every unit in the 2-unit pool, reloaded for
+    its backward) with the backward's reloads as fp32 + cast at use
+    (``bf16_reload=False``) or from the bf16 copy each update writes (the
+    default with fp32 H2D): every update bit-exact vs the oracle over 3 steps,
+    and step-1 gradients and the 10-step losses equal to the non-offloaded
+    run's (a reload copy an update left stale would change a later step's
+    gradients)."""
+    sf = check_updates_against_oracle(dev, "llama", "fp32", {}, dict(resident_layers=0, bf16_reload=bf16_reload),
+                                      keep=True)
+    try:
+        assert sf.bf16_reload_units == (list(range(1, L)) if bf16_reload else [])
+    finally:
+        sf.close()
+    check_loss_parity(dev, "llama", False, {}, dict(resident_layers=0, bf16_reload=bf16_reload))
+
+
 # Updates in pieces of 40,000 elements: a decoder (590,336 elements) comes back, is
 # updated and is staged in 15 pieces, the output unit in 7, cutting parameters
 # inside their vector body.  (H2D format, resident decoders, D2H engine, slot ring, family)

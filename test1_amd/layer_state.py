@@ -79,6 +79,49 @@ def _no_slot() -> None:
     return None
 
 
+# The runtime's (h2d, cast, d2h) streams per device index, shared by every
+# runtime of the process (see ``runtime_streams``).
+_RUNTIME_STREAMS: Dict[int, Tuple[Any, Any, Any]] = {}
+_RUNTIME_STREAMS_LOCK = threading.Lock()
+
+
+def runtime_streams(device: torch.device) -> Tuple[Any, Any, Any]:
+    """The ``(h2d, cast, d2h)`` streams of ``device``, made once per process.
+
+    The HIP runtime gives a stream its hardware queue when the stream is
+    first used: a new queue while fewer than GPU_MAX_HW_QUEUES exist, then
+    the existing ones again.  An event recorded on a stream behind a copy in
+    flight holds a packet in that stream's queue until the copy ends, and
+    while it is held, kernels of some other queues run slower.  Measured on
+    MI355X, the default stream's queue created first: with 8 queues the
+    staging cast on the default stream ran at 0.65-0.68 of HBM peak beside
+    such a copy from the fifth queue and at 0.75-0.76 beside one from any
+    other; with 16 queues it was slow beside the fifth, ninth and
+    thirteenth; with 4, beside none.  Copies without an event behind them,
+    and SDMA copies issued outside HIP streams, did not slow it.  So the
+    default stream and the three streams here are first used together, in
+    that order, when they are made: in a process that has used no other
+    stream they take the first four queues.  Every later runtime of the
+    process reuses them: a second runtime whose streams were new came after
+    the first's queues, and its casts ran at 0.64 of peak against 0.74
+    when it reused the first's streams (the 2-unit pool schedule after the
+    default one, Llama-3-8B).  Sharing the streams between runtimes only
+    adds order between their copies."""
+    dev = torch.device(device)
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    with _RUNTIME_STREAMS_LOCK:
+        got = _RUNTIME_STREAMS.get(key)
+        if got is None:
+            dev = torch.device("cuda", key)
+            h2d, cast, d2h = (torch.cuda.Stream(device=dev) for _ in range(3))
+            with torch.cuda.device(dev):
+                for s in (torch.cuda.current_stream(dev), h2d, d2h, cast):
+                    torch.cuda.Event().record(s)   # the stream's first use: its queue
+            got = (h2d, cast, d2h)
+            _RUNTIME_STREAMS[key] = got
+        return got
+
+
 class StreamingRuntime:
     """Objects shared by all units of one model: streams, pool, stager, grad
     ring, worker threads and the optional event trace."""
@@ -122,9 +165,7 @@ class StreamingRuntime:
         # cost to the casts and GEMMs beside them; many more slow HBM-bound
         # kernels beside them (the staging cast: 10x beside 64).
         self.d2h_workgroups = d2h_workgroups
-        self.h2d_stream = torch.cuda.Stream(device=device)
-        self.cast_stream = torch.cuda.Stream(device=device)
-        self.d2h_stream = torch.cuda.Stream(device=device)
+        self.h2d_stream, self.cast_stream, self.d2h_stream = runtime_streams(device)
         self.pool = LayerBufferPool(max_param_size, dtype, device, pool_size)
         if h2d_format == "bf16":
             self.stager = BF16Loader(self.h2d_stream)

@@ -1,0 +1,55 @@
+"""The runtime's streams: made once per process and device, first used in a
+fixed order right after the default stream (the HIP runtime hands out
+hardware queues at a stream's first use)."""
+
+import contextlib
+from types import SimpleNamespace
+
+import torch
+
+
+class _Stream:
+    def __init__(self, log, name):
+        self.log, self.name = log, name
+
+
+class _Event:
+    def __init__(self, log):
+        self.log = log
+
+    def record(self, stream):
+        self.log.append(stream.name)
+
+
+def _fake_torch(log):
+    made = []
+    default = _Stream(log, "default")
+
+    def Stream(device=None):
+        s = _Stream(log, f"s{len(made)}")
+        made.append(s)
+        return s
+
+    cuda = SimpleNamespace(Stream=Stream, Event=lambda: _Event(log), current_stream=lambda device=None: default,
+                           device=lambda d: contextlib.nullcontext(), current_device=lambda: 0)
+    return SimpleNamespace(cuda=cuda, device=torch.device), made
+
+
+def test_streams_made_once_and_first_used_in_order(monkeypatch):
+    from test1_amd import layer_state
+
+    log = []
+    ft, made = _fake_torch(log)
+    monkeypatch.setattr(layer_state, "torch", ft)
+    monkeypatch.setattr(layer_state, "_RUNTIME_STREAMS", {})
+    h2d, cast, d2h = layer_state.runtime_streams(torch.device("cuda", 0))
+    assert [s.name for s in (h2d, cast, d2h)] == ["s0", "s1", "s2"]
+    # the default stream first, then the copy streams, then the cast stream
+    assert log == ["default", "s0", "s2", "s1"]
+    # a second runtime on the same device gets the same streams, touching none
+    assert layer_state.runtime_streams(torch.device("cuda", 0)) == (h2d, cast, d2h)
+    assert layer_state.runtime_streams("cuda:0") == (h2d, cast, d2h)
+    assert len(made) == 3 and len(log) == 4
+    # another device gets its own
+    other = layer_state.runtime_streams(torch.device("cuda", 1))
+    assert other != (h2d, cast, d2h) and len(made) == 6

@@ -20,6 +20,11 @@ With ``--gap-ms G`` the cast is also timed alone after G ms with the GPU
 idle before each launch (a host sleep after a synchronisation), as a unit's
 cast runs in a step whose compute stream waited for the unit's copy: each
 launch timed by the events the runtime stamps around the kernel itself.
+
+With ``--beside-h2d-streams K`` the cast on the default stream is timed
+beside a layer's host-to-device copy issued on each of K new streams in turn,
+with and without an event recorded behind the copy (the hardware queue a
+stream gets at its first use decides whether such a copy slows the cast).
 """
 
 from __future__ import annotations
@@ -62,6 +67,10 @@ def main(argv=None):
                          "the copies queued back to back on another stream, as in the pool schedule's forward")
     ap.add_argument("--beside-sdma-d2h", action="store_true",
                     help="also time the cast while device-to-host copies run on the gradient SDMA engines")
+    ap.add_argument("--beside-h2d-streams", type=int, default=0, metavar="K",
+                    help="also time the cast on the default stream beside a host-to-device copy with an event "
+                         "recorded behind it, from each of K new streams first used in turn (the HIP runtime "
+                         "gives a stream its hardware queue at first use), and without the event")
     args = ap.parse_args(argv)
     n, reps = args.elements, args.reps
     dev = torch.device("cuda", 0)
@@ -201,6 +210,34 @@ def main(argv=None):
         res["cast_beside_sdma_d2h"] = {"ms": ms, "GB/s": 6 * n / ms / 1e6, "frac_hbm": 6 * n / ms / 1e6 / HBM_PEAK_GBS,
                                        "copies_still_running_after_the_casts": busy}
         del host_big, src_big
+    if args.beside_h2d_streams > 0:
+        streams = []
+        for _ in range(args.beside_h2d_streams):
+            st = torch.cuda.Stream(device=dev)
+            torch.cuda.Event().record(st)         # first use: the stream's hardware queue
+            streams.append(st)
+        torch.cuda.synchronize()
+        nc = min(reps, 8)                          # ~2 ms of casts, inside one ~17 ms copy of a layer
+
+        def beside(st, with_event):
+            torch.cuda.synchronize()
+            kernels.memcpy_async(dev_w, host_w, st)
+            if with_event:
+                torch.cuda.Event().record(st)
+            timers = []
+            for k in range(nc):
+                t = kernels.KernelTimer()
+                a, b = pairs[k % len(pairs)]
+                kernels.cast_f32_bf16_(b, a, s, timer=t)
+                timers.append(t)
+            torch.cuda.synchronize()
+            ms = sum(t.elapsed_ms() for t in timers) / nc
+            return round(6 * n / ms / 1e6 / HBM_PEAK_GBS, 4)
+
+        res["cast_beside_h2d_streams"] = {
+            "frac_hbm_with_event": [beside(st, True) for st in streams],
+            "frac_hbm_without_event": [beside(st, False) for st in streams],
+            "streams_in_first_use_order": len(streams)}
     ms = _time(lambda: cp_dst.copy_(cp_src), s, reps)
     res["copy"] = {"ms": ms, "GB/s": 8 * half / ms / 1e6, "bytes_read": 4 * half, "bytes_written": 4 * half}
     ms = _time(lambda: kernels.pack_b16([g], host_g, s, max_workgroups=16), s, max(1, reps // 4))

@@ -795,8 +795,8 @@ def activation_round_trip(dev, L: int = 32, shape=(4, 1024, 4096), rounds: int =
     """The activation-offload configuration: ``L`` checkpointed layers whose
     bf16 inputs of ``shape`` (N(0,1)) go to pinned host slots through
     ``SlidingCheckpoint`` in the forward (pack kernel on the offload stream)
-    and come back one layer ahead in the backward (prefetch on a copy stream,
-    reference sliding_checkpoint.py:51-131).  The layers compute an
+    and come back one layer ahead in the backward (prefetch on the H2D stream,
+    reference sliding_checkpoint.py:51-131), on the runtime's streams.  The layers compute an
     elementwise ``tanh(x) * w``, so the copies dominate.  Round 0 warms up;
     the last round also checks that every recompute was given its forward
     input bit for bit.  Reports each direction's rate over the union of its
@@ -804,11 +804,13 @@ def activation_round_trip(dev, L: int = 32, shape=(4, 1024, 4096), rounds: int =
     import torch
     from torch.utils.checkpoint import checkpoint
 
+    from test1_amd.layer_state import runtime_streams
     from test1_amd.pinned import pinned_empty
     from test1_amd.sliding_checkpoint import ActivationRing, SlidingCheckpoint
 
     slots = [[pinned_empty(shape, torch.bfloat16)] for _ in range(L)]
-    d2h, h2d = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+    # the streams SlideFSDP gives the checkpoint offload and its prefetch
+    h2d, _, d2h = runtime_streams(dev)
     ws = [torch.full((shape[-1],), 1.0 + 1e-3 * i, dtype=torch.bfloat16, device=dev, requires_grad=True)
           for i in range(L)]
     h = torch.randn(shape, generator=torch.Generator(device=dev).manual_seed(42), device=dev).bfloat16()

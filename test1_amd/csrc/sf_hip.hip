@@ -932,23 +932,27 @@ int sf_dma_init(int device) {
     if (hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP_FREQUENCY, &freq) != HSA_STATUS_SUCCESS) freq = 0;
     g_dma.ts_freq = freq;
     g_dma.ok = true;
-    // Engines for device -> host copies.  HIP's own host<->device copies run
-    // on the first SDMA engines, and a copy queued on the same engine waits
-    // behind them (measured: a D2H on engine 0 or 1 waited for eight queued
-    // H2D copies; on engine 2 or 3 it ran at once).  One engine moves ~29
-    // GB/s device -> host while the host link is busy the other way, two
-    // ~41 GB/s, four no more.  Take the first two available engines from 2
-    // upward, else let the runtime choose.
+    // Engine for device -> host copies.  HIP puts each of its own
+    // host<->device copies on the first SDMA engine that is free: engine 0,
+    // then 1 while 0 is held, then 2.  A HIP copy whose stream waits on an
+    // event holds its engine until the event completes, and a copy queued
+    // behind it on that engine waits as long (measured on MI355X: with
+    // engines 0 and 1 held, a HIP copy waiting for 250 ms of GEMMs took
+    // engine 2, and a 1 GiB device -> host copy split over engines 2 and 3
+    // took 206 ms instead of 19-21; in the Qwen2.5-14B step the gradient
+    // copies on engines 2 and 3 moved 20-28 GB/s while busy, on engine 3
+    // alone 52-53).  Engines 0-3 each move 57 GB/s device -> host alone and
+    // 52 beside a host -> device copy on another engine, as much as two of
+    // them; engines 4-7 move ~25 GB/s together.  So the copies use engine 3
+    // alone, the last fast engine HIP reaches, else engine 2, else the
+    // runtime's choice.
     uint32_t avail = 0;
     g_dma.engine_mask = 0;
     if (hsa_amd_memory_copy_engine_status(g_dma.cpu, g_dma.gpu, &avail) == HSA_STATUS_SUCCESS) {
-        int taken = 0;
-        for (int e = 2; e < 16 && taken < 2; ++e) {
-            if (avail & (1u << e)) {
-                g_dma.engine_mask |= 1u << e;
-                ++taken;
-            }
-        }
+        if (avail & (1u << 3))
+            g_dma.engine_mask = 1u << 3;
+        else if (avail & (1u << 2))
+            g_dma.engine_mask = 1u << 2;
     }
     return SF_OK;
 }

@@ -356,8 +356,10 @@ ROUTING_DISABLED = (
 
 
 def dma_init(device: Optional[torch.device] = None) -> None:
-    """Bind the SDMA copies to ``device`` (once per process); engines from
-    ``SF_DMA_ENGINES`` (e.g. "2,3") if set.  ``SF_DMA_AVOID_HELD`` other than
+    """Bind the SDMA copies to ``device`` (once per process).  The library
+    picks engine 3 (HIP's own copies take engines 0, 1, 2 in turn, and a copy
+    queued behind one of them that waits on an event waits as long);
+    ``SF_DMA_ENGINES`` (e.g. "3" or "2,3") overrides it.  ``SF_DMA_AVOID_HELD`` other than
     0 raises ``RuntimeError``: engine routing is disabled (see
     ``ROUTING_DISABLED``)."""
     mode = avoid_held_from_env(os.environ.get("SF_DMA_AVOID_HELD"))
@@ -367,7 +369,7 @@ def dma_init(device: Optional[torch.device] = None) -> None:
     if idx in _dma_ready:
         return
     _native.check(_native.hip().sf_dma_init(int(idx)), "sf_dma_init")
-    env = os.environ.get("SF_DMA_ENGINES")  # e.g. "2,3"
+    env = os.environ.get("SF_DMA_ENGINES")  # e.g. "3"
     if env not in (None, ""):
         mask = 0
         for e in env.split(","):

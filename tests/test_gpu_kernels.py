@@ -321,6 +321,52 @@ def test_sdma_copy_d2h_routes_around_engine_held_by_waiting_hip_copy(dev):
     assert torch.equal(host, src.cpu())
 
 
+def test_sdma_copy_d2h_default_engine_clear_of_waiting_hip_copies(dev):
+    """HIP puts a host -> device copy on the first free SDMA engine (0, then
+    1, then 2), and a copy ordered after an event that has not fired holds
+    its engine until the event fires.  With three such copies pending (on
+    engines 0, 1 and 2), a device -> host copy on the library's default
+    engine completes while the event is still pending, with exact bytes."""
+    kernels.dma_init(dev)
+    if os.environ.get("SF_DMA_ENGINES"):
+        pytest.skip("SF_DMA_ENGINES overrides the default engine")
+    assert kernels.dma_engines() == [3]
+    nb = 64 << 20
+    hsrc = pinned_empty(nb, torch.uint8)
+    dbufs = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(3)]
+    src = torch.randint(0, 256, (nb // 4,), dtype=torch.int32, device=dev).view(torch.uint8)
+    host = pinned_empty(nb, torch.uint8)
+    host.zero_()
+    spin = torch.cuda.Stream(dev)
+    streams = [torch.cuda.Stream(dev) for _ in range(3)]
+    # spin length for about 0.3 s, from a short timed spin
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(spin):
+        t0.record()
+        torch.cuda._sleep(5_000_000)
+        t1.record()
+    t1.synchronize()
+    cycles = int(min(5_000_000 * 300.0 / max(t0.elapsed_time(t1), 1e-3), 2_000_000_000))
+    for s in streams:  # first copies on these streams, outside the test window
+        kernels.memcpy_async(dbufs[0], hsrc, s)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(spin):
+        torch.cuda._sleep(cycles)
+    ev = torch.cuda.Event()
+    ev.record(spin)
+    for s, d in zip(streams, dbufs):
+        s.wait_event(ev)
+        kernels.memcpy_async(d, hsrc, s)
+    try:
+        h = kernels.dma_copy_d2h([(src, host)])
+        kernels.dma_wait(h)
+        pending_after_copy = not ev.query()
+    finally:
+        torch.cuda.synchronize()
+    assert pending_after_copy, "the device -> host copy waited behind HIP copies held by a pending event"
+    assert torch.equal(host, src.cpu())
+
+
 @pytest.mark.parametrize("row_len", [4096, 5120, 8192, 8200, 24, 13])
 def test_gather_rows_from_pinned_host_table(dev, row_len):
     # fp32 rows read by the kernel from pinned host memory, rounded to bf16:

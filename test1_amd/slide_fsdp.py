@@ -301,7 +301,7 @@ class SlideFSDP(nn.Module):
         self._layer_uses_rng = self._decoders_use_rng()
         self.layer_tensors: Optional[List[List[torch.Tensor]]] = None
         self.position_embeddings = None
-        self._act_ring = ActivationRing(self.device)
+        self._act_ring = ActivationRing(self.device, wait_timeout=wait_timeout)
         self._spill: Optional[StorageSpill] = None
         self._ring_grown = False
         self._ring_grow_pending = False

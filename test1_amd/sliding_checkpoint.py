@@ -89,13 +89,35 @@ class ActivationRing:
     waits on an event recorded on the compute stream after layer j+1's
     backward has been enqueued."""
 
-    def __init__(self, device):
+    def __init__(self, device, host_lead: int = 2, wait_timeout: Optional[float] = 600.0):
         self.device = torch.device(device)
         self.sets: List[Optional[List[torch.Tensor]]] = [None, None]
         self.next = 0
         self.fifo: deque = deque()
         self.packed_counts = {}
         self.packed_meta = {}
+        # The compute-stream events recorded at each layer's first unpack in
+        # this backward, most recent last; see ``throttle``.
+        self.unpack_events: deque = deque(maxlen=8)
+        self.host_lead = int(host_lead)
+        self.wait_timeout = wait_timeout
+
+    def throttle(self, what: str) -> None:
+        """Before a prefetch is issued: hold the host until the compute
+        stream has reached the first unpack ``host_lead`` layers back (0: no
+        hold).  Each prefetch copy waits on the compute stream, and the HIP
+        runtime puts a copy on the first SDMA engine not already held, a
+        waiting copy holding its engine until its event fires.  With the
+        host many layers ahead of the device in the backward, the waiting
+        prefetches held up to nine engines at once (Qwen2.5-14B step), and
+        the parameter and gradient copies queued behind them.  Measured
+        (tokens/s, same box): Qwen2.5-14B 3,939 with no hold, 5,000-5,034
+        with a lead of 1 layer, 5,162 with 2, 5,019 with 3; Llama-3.1-8B
+        5,591 with no hold, 4,683 with 1 (the host then starves the device
+        of queued work), 5,759-5,788 with 2, 5,785 with 3."""
+        if self.host_lead <= 0 or len(self.unpack_events) < self.host_lead:
+            return
+        kernels.wait_event(self.unpack_events[-self.host_lead], self.wait_timeout, what)
 
     def buffers_like(self, host_tensors: List[torch.Tensor]) -> List[torch.Tensor]:
         i = self.next
@@ -110,6 +132,7 @@ class ActivationRing:
 
     def reset(self) -> None:
         self.fifo.clear()
+        self.unpack_events.clear()
 
 
 class KeptOnDevice:
@@ -479,6 +502,10 @@ class SlidingCheckpoint(saved_tensors_hooks):
                         got = [torch.empty(t.shape, dtype=t.dtype, device=self.device) for t in pinned]
                     it = iter(got)
                     bufs = [None if isinstance(h, KeptOnDevice) else next(it) for h in host]
+                    if self.ring is not None:
+                        self.ring.throttle(f"decoder {self.layer_idx}: the backward before its checkpoint "
+                                           f"prefetch")
+                        self.ring.unpack_events.append(self.pre_unpack_event)
                     ps = self.prefetch_stream
                     ps.wait_event(self.pre_unpack_event)
                     timed = self.link_timing is not None

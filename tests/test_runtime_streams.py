@@ -53,3 +53,29 @@ def test_streams_made_once_and_first_used_in_order(monkeypatch):
     # another device gets its own
     other = layer_state.runtime_streams(torch.device("cuda", 1))
     assert other != (h2d, cast, d2h) and len(made) == 6
+
+
+def test_prefetch_throttle_waits_for_the_unpack_two_layers_back(monkeypatch):
+    """Before each checkpoint prefetch the host waits until the compute
+    stream has reached the first unpack ``host_lead`` layers back, so that at
+    most that many prefetch copies wait on the device at once."""
+    from test1_amd import sliding_checkpoint as sc
+
+    waited = []
+    monkeypatch.setattr(sc.kernels, "wait_event", lambda ev, timeout, what: waited.append((ev, timeout)))
+    ring = sc.ActivationRing("cpu", wait_timeout=7.0)
+    assert ring.host_lead == 2
+    events = [f"unpack of layer {i}" for i in range(5, 0, -1)]   # the backward's order
+    for ev in events:
+        ring.throttle("test")
+        ring.unpack_events.append(ev)
+    # the first two prefetches do not wait; then each waits two layers back
+    assert waited == [(events[0], 7.0), (events[1], 7.0), (events[2], 7.0)]
+    ring.reset()
+    ring.throttle("test")
+    assert len(waited) == 3           # a new backward starts with nothing to wait for
+    ring.host_lead = 0
+    for ev in events:
+        ring.throttle("test")
+        ring.unpack_events.append(ev)
+    assert len(waited) == 3

@@ -266,9 +266,12 @@ int sf_host_device_pointer(void* host_ptr, void** device_ptr);
  * ------------------------------------------------------------------- */
 
 /* Bind to the ROCr agents of HIP device `device` (once per process) and
- * pick the SDMA engines for device -> host copies: the first two available
- * engines from index 2 up (HIP's own copies use the first engines, and a
- * copy queued behind them waits), else the runtime's choice. */
+ * pick the SDMA engine for device -> host copies: engine 3 if available,
+ * else engine 2, else the runtime's choice.  HIP puts each of its own
+ * host<->device copies on the first free engine (0, then 1, then 2); one
+ * of them ordered after an event that has not fired holds its engine until
+ * then, and a copy queued behind it waits as long.  One of engines 0-3
+ * moves as much device -> host as two. */
 int sf_dma_init(int device);
 
 /* Override the engines (bit e = SDMA engine e; 0 = runtime's choice). */

@@ -946,14 +946,21 @@ int sf_dma_init(int device) {
     // them; engines 4-7 move ~25 GB/s together.  So the copies use engine 3
     // alone, the last fast engine HIP reaches, else engine 2, else the
     // runtime's choice.
-    uint32_t avail = 0;
+    // An engine the status reports busy may only be running a copy at this
+    // moment: ask again for up to 100 ms before settling for another one.
     g_dma.engine_mask = 0;
-    if (hsa_amd_memory_copy_engine_status(g_dma.cpu, g_dma.gpu, &avail) == HSA_STATUS_SUCCESS) {
-        if (avail & (1u << 3))
-            g_dma.engine_mask = 1u << 3;
-        else if (avail & (1u << 2))
-            g_dma.engine_mask = 1u << 2;
+    uint32_t seen = 0;
+    for (int tries = 0; tries < 100; ++tries) {
+        uint32_t avail = 0;
+        if (hsa_amd_memory_copy_engine_status(g_dma.cpu, g_dma.gpu, &avail) != HSA_STATUS_SUCCESS) break;
+        seen |= avail;
+        if (seen & (1u << 3)) break;
+        std::this_thread::sleep_for(std::chrono::milliseconds(1));
     }
+    if (seen & (1u << 3))
+        g_dma.engine_mask = 1u << 3;
+    else if (seen & (1u << 2))
+        g_dma.engine_mask = 1u << 2;
     return SF_OK;
 }
 

@@ -98,8 +98,8 @@ class ActivationRing:
         self.packed_meta = {}
         # The compute-stream events recorded at each layer's first unpack in
         # this backward, most recent last; see ``throttle``.
-        self.unpack_events: deque = deque(maxlen=8)
         self.host_lead = int(host_lead)
+        self.unpack_events: deque = deque(maxlen=max(8, self.host_lead))
         self.wait_timeout = wait_timeout
 
     def throttle(self, what: str) -> None:

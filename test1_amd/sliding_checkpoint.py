@@ -480,6 +480,9 @@ class SlidingCheckpoint(saved_tensors_hooks):
                         like = [torch.empty(shape, dtype=dt, device="meta") for _, shape, dt in meta]
                         if self.ring is not None:
                             bufs = self.ring.buffers_like(like)
+                            self.ring.throttle(f"decoder {self.layer_idx}: the backward before its checkpoint "
+                                               f"prefetch")
+                            self.ring.unpack_events.append(self.pre_unpack_event)
                         else:
                             bufs = [torch.empty(shape, dtype=dt, device=self.device) for _, shape, dt in meta]
                         ps = self.prefetch_stream

@@ -347,7 +347,9 @@ class StreamingRuntime:
     def release_slots(self, states) -> None:
         """Give back the whole-unit slots of stagings not yet cast (their units
         are then staged from the master if used again) and free the pool's
-        buffers once the copy and cast streams have drained."""
+        buffers once the copy and cast streams have drained and each slot's
+        last cast (on the forward's stream, with casts at use) has
+        completed."""
         slots = getattr(self.stager, "slots", None)
         if slots is None:
             return
@@ -363,7 +365,7 @@ class StreamingRuntime:
             st._drop_pending_cast()
         self.h2d_stream.synchronize()
         self.cast_stream.synchronize()
-        slots.release()
+        slots.release(self.wait_timeout)
 
 
 class LayerRuntimeState(RowSparseEmbedding, nn.Module):

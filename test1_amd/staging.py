@@ -197,13 +197,22 @@ class _SlotPool:
         with self._lock:
             self._free.setdefault(t.numel(), []).append((t, free_event))
 
-    def release(self) -> None:
-        """Drop the free buffers (the caller has made sure nothing still copies
-        into or reads from them); buffers still out stay with their holders."""
+    def release(self, timeout: Optional[float] = None) -> None:
+        """Drop the free buffers once the work that last read each one has
+        completed (its event: a cast, on whatever stream ran it); buffers
+        still out stay with their holders.  The caller has drained the copy
+        stream.  A dropped buffer goes back to the caching allocator on the
+        copy stream, which every runtime of the process shares: the next
+        runtime's copy into it would not wait for a cast still queued on
+        another stream."""
         with self._lock:
-            for lst in self._free.values():
-                self.bytes -= sum(4 * t.numel() for t, _ in lst)
+            dropped = [b for lst in self._free.values() for b in lst]
             self._free.clear()
+        for t, ev in dropped:
+            if ev is not None:
+                kernels.wait_event(ev, timeout, "a staging slot's last cast")
+        with self._lock:
+            self.bytes -= sum(4 * t.numel() for t, _ in dropped)
 
 
 class H2DStager:

@@ -454,3 +454,46 @@ def test_step_preamble_pins_only_after_draining(monkeypatch, row_sparse):
     assert pins.count("pin slot") == 2 * sf.num_decoder_layers and pins.count("pin ring") == 1
     assert pins.count("pin rows") == (2 if row_sparse else 0)
     assert events[1] == "drain"                      # drained on the very first step too
+
+
+# ---------------------------------------------------------------------------
+# Slots given back at close; the next runtime on the same (shared) streams
+# ---------------------------------------------------------------------------
+
+def _close_then_next_runtime(dev, wait_casts: bool):
+    from test1_amd.staging import H2DStager
+
+    comp = dev.default
+    h2d, cast = hb_model.FakeStream(dev, "h2d"), hb_model.FakeStream(dev, "cast")
+    a = H2DStager("cuda:0", N, 3, h2d, cast, slot_cap_bytes=1 << 30)
+    with dev.as_host("update"):
+        pc = a.copy_for_later(torch.randn(N), None)
+    with dev.as_host("autograd"):
+        unit = dev.alloc((N,), torch.bfloat16)
+        a.cast_pending(pc, unit, comp)            # reads the slot on the forward's stream
+    with dev.as_host("main"):
+        # runtime A closes: release_slots drains the copy and cast streams
+        h2d.synchronize()
+        cast.synchronize()
+        dropped = [t for lst in a.slots._free.values() for t, _ in lst]
+        if wait_casts:
+            a.slots.release(timeout=None)
+        else:
+            a.slots._free.clear()                 # the release before it waited for the casts
+        for t in dropped:
+            dev.free(t)                           # the last reference goes
+        b = H2DStager("cuda:0", N, 3, h2d, cast, slot_cap_bytes=1 << 30)
+    with dev.as_host("update"):
+        assert b.copy_for_later(torch.randn(N), None) is not None
+
+
+def test_slots_released_after_their_last_cast(dev):
+    _close_then_next_runtime(dev, wait_casts=True)
+    assert dev.races == []
+
+
+def test_slots_released_before_their_last_cast_race(dev):
+    """Without waiting for the casts, the next runtime's copy on the shared
+    copy stream reuses a slot's block while the old cast may still read it."""
+    _close_then_next_runtime(dev, wait_casts=False)
+    assert any("copy on h2d" in r and "cast" in r for r in dev.races), dev.races

@@ -23,8 +23,40 @@ import statistics
 import sys
 
 
-def main() -> None:
-    d, warm, steps, bj = sys.argv[1], int(sys.argv[2]), int(sys.argv[3]), sys.argv[4]
+def union(spans):
+    """Merged, sorted ``[start, end]`` intervals covering ``spans``."""
+    out = []
+    for s, e in sorted(tuple(x) for x in spans):
+        if out and s <= out[-1][1]:
+            out[-1][1] = max(out[-1][1], e)
+        else:
+            out.append([s, e])
+    return out
+
+
+def length(u) -> int:
+    """Total length of disjoint intervals."""
+    return sum(e - s for s, e in u)
+
+
+def inter(a, b) -> int:
+    """Length of the intersection of two sorted lists of disjoint intervals."""
+    i = j = 0
+    tot = 0
+    while i < len(a) and j < len(b):
+        lo, hi = max(a[i][0], b[j][0]), min(a[i][1], b[j][1])
+        if hi > lo:
+            tot += hi - lo
+        if a[i][1] < b[j][1]:
+            i += 1
+        else:
+            j += 1
+    return tot
+
+
+def main(argv=None) -> None:
+    d, warm, steps, bj = (sys.argv[1:] if argv is None else argv)[:4]
+    warm, steps = int(warm), int(steps)
     B = json.loads([ln for ln in open(bj) if ln.startswith("{")][-1])
     rows = sorted(csv.DictReader(open(f"{d}/run_kernel_trace.csv")), key=lambda r: int(r["Start_Timestamp"]))
     iv = lambda r: (int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
@@ -54,38 +86,8 @@ def main() -> None:
     grow = sorted(iv(r) for r in rows if "gather_rows_kernel<false" in r["Kernel_Name"])
     w0, w1 = look[warm][0], grow[warm + steps - 1][1]
 
-
-    def union(sp):
-        out = []
-        for s, e in sorted(tuple(x) for x in sp):
-            if out and s <= out[-1][1]:
-                out[-1][1] = max(out[-1][1], e)
-            else:
-                out.append([s, e])
-        return out
-
-
     def clip(sp):
         return [(max(s, w0), min(e, w1)) for s, e in sp if e > w0 and s < w1]
-
-
-    def length(u):
-        return sum(e - s for s, e in u)
-
-
-    def inter(a, b):
-        i = j = 0
-        tot = 0
-        while i < len(a) and j < len(b):
-            lo, hi = max(a[i][0], b[j][0]), min(a[i][1], b[j][1])
-            if hi > lo:
-                tot += hi - lo
-            if a[i][1] < b[j][1]:
-                i += 1
-            else:
-                j += 1
-        return tot
-
 
     h2d = union(clip([iv(r) for r in C if r["Direction"].endswith("HOST_TO_DEVICE")] + look))
     d2h = union(clip([iv(r) for r in C if r["Direction"].endswith("DEVICE_TO_HOST")] + grow +

@@ -417,6 +417,44 @@ def test_bench_link_arithmetic():
     assert bench.elapsed_stats(recs) == (10.0, 400_000_000)
 
 
+def test_bench_copy_model_and_h2d_idle_attribution():
+    """``frac_of_copy_model``: bytes over what plain copies move in the same
+    busy time, at the duplex rate while the other direction is busy and the
+    one-way rate otherwise.  ``h2d_idle_attribution``: each H2D gap goes to
+    what the copy ending it waited for (issued under 1 ms before it started:
+    the thread that issued it; earlier: the device)."""
+    import bench
+
+    ms = 1_000_000   # ns
+    # H2D busy [0, 10] ms, D2H busy [5, 20] ms: 5 ms duplex, 5 ms one way for H2D
+    alone = {"h2d_gbs": 50.0, "d2h_gbs": 56.0, "duplex": {"h2d_gbs": 40.0, "d2h_gbs": 52.0}}
+    r = {"elapsed": 0.02, "link": {
+        "h2d": {"params": [(0, 10 * ms, 450_000_000)], "checkpoints": [], "rows": []},
+        "d2h": {"grads": [(5 * ms, 20 * ms, 700_000_000)], "checkpoints": [], "rows": []},
+        "compute": [], "common_clock": True}}
+    st = bench.link_stats(r, steps=1, alone=alone)
+    # H2D: 5 ms x 40 GB/s + 5 ms x 50 GB/s = 450 MB; D2H: 5 x 52 + 10 x 56 = 820 MB
+    assert abs(st["h2d"]["frac_of_copy_model"] - 1.0) < 1e-12
+    assert abs(st["d2h"]["frac_of_copy_model"] - 700 / 820) < 1e-12
+    assert st["h2d"]["both_directions_busy_ms_per_step"] == 5
+    assert abs(st["h2d"]["frac_of_duplex_copy"] - 45 / 40) < 1e-12
+    assert bench.link_stats(r, steps=1, alone={"h2d_gbs": 50.0})["h2d"]["frac_of_copy_model"] is None
+
+    # H2D copies (ms on the host timeline's clock) [2, 4], [6, 8], [8.5, 9.5] in a 12 ms window
+    anchor = 1_000 * ms
+    link = {"h2d": {"params": [(anchor + 2 * ms, anchor + 4 * ms, 1), (anchor + 6 * ms, anchor + 8 * ms, 1)],
+                    "checkpoints": [(anchor + int(8.5 * ms), anchor + int(9.5 * ms), 1)], "rows": []}}
+    events = [(0.0015, "sf-update", "staged_after_update", 3),     # 1.5 ms: issued 0.5 ms before its copy
+              (0.0030, "MainThread", "h2d_issued", 4),             # 3 ms: 3 ms before the copy at 6 ms
+              (0.0082, "MainThread", "h2d_issued", 5)]             # 8.2 ms: 0.3 ms before the one at 8.5
+    out = bench.h2d_idle_attribution(events, link, anchor, 0.012)
+    assert out["gaps"] == 4 and abs(out["idle_ms"] - (2 + 2 + 0.5 + 2.5)) < 1e-9
+    assert abs(out["waiting_for_update_thread_ms"] - 2) < 1e-9        # [0, 2] ended by unit 3's copy
+    assert abs(out["waiting_on_device_ms"] - 2) < 1e-9                # [4, 6]: issued at 3 ms
+    assert abs(out["waiting_for_forward_ms"] - 0.5) < 1e-9            # [8, 8.5]
+    assert abs(out["idle_frac"] - 7 / 12) < 1e-9                       # the tail [9.5, 12] is idle, unattributed
+
+
 def test_checkpoint_slot_kept_on_device_only_when_pinning_runs_out(monkeypatch):
     """A checkpoint slot the host cannot pin (out of memory) becomes a
     ``KeptOnDevice`` marker of the slot's shape and dtype; any other failure

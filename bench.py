@@ -436,14 +436,20 @@ def megatron_flops_per_step(w: dict) -> float:
 
 def host_dram_stats(r: dict, args, cpu: Optional[dict]) -> dict:
     """Host DRAM traffic of one step: the host AdamW's 26 B per parameter
-    (28 with the bf16 copy) plus what the copy engines read and write.  The
-    reference rate is a streaming AdamW on the same cores in the same run
-    (the CPU baseline's), the nearest this host gets to its DRAM peak."""
+    (28 with the bf16 copy) plus every host-link transfer, each of which
+    reads or writes host memory once (parameter copies, checkpoints and
+    embedding rows both ways; gradient copies without engine timestamps
+    included).  The reference rate is a streaming AdamW on the same cores in
+    the same run (the CPU baseline's), the nearest this host gets to its
+    DRAM peak."""
     adam_b = (28 if args.h2d_format == "bf16" else 26) * r["total_params"]
-    h2d = r["h2d"][1] / args.steps
-    d2h = r["d2h"][1] / args.steps
+    lk = r.get("link") or {}
+    link_b = sum(sp[2] for d in ("h2d", "d2h") for v in (lk.get(d) or {}).values() for sp in v)
+    link_b += lk.get("untimed_d2h_bytes", 0)
+    if link_b == 0:
+        link_b = r["h2d"][1] + r["d2h"][1]
     step_s = r["elapsed"] / args.steps
-    total = adam_b + h2d + d2h
+    total = adam_b + link_b / args.steps
     ref = None if cpu is None else cpu.get("adam_gbs")
     return {"bytes_per_step": total, "adam_bytes_per_step": adam_b, "achieved_gbs": total / step_s / 1e9,
             "streaming_adam_gbs": ref, "frac_of_streaming_adam": None if not ref else total / step_s / 1e9 / ref}

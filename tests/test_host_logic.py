@@ -473,3 +473,26 @@ def test_checkpoint_slot_kept_on_device_only_when_pinning_runs_out(monkeypatch):
     monkeypatch.setattr(sc, "pinned_empty", refuse(1))
     with pytest.raises(_native.NativeError):
         sc.pin_or_keep((4, 16, 32), torch.bfloat16)
+
+
+def test_bench_host_dram_counts_every_host_link_transfer():
+    """``host_dram``: the AdamW's 26 B per parameter (28 with bf16 H2D) plus
+    every host-link transfer of the timed steps, gradient copies without
+    engine timestamps included; without link records, the copy totals."""
+    from types import SimpleNamespace
+
+    import bench
+
+    r = {"total_params": 1000, "elapsed": 2.0, "h2d": (1.0, 4000), "d2h": (1.0, 2000), "link": {
+        "h2d": {"params": [(0, 1, 4000)], "checkpoints": [(0, 1, 300)], "rows": [(0, 1, 50)]},
+        "d2h": {"grads": [(0, 1, 1500)], "checkpoints": [(0, 1, 300)], "rows": [(0, 1, 25)]},
+        "untimed_d2h_bytes": 500}}
+    args = SimpleNamespace(h2d_format="fp32", steps=2)
+    st = bench.host_dram_stats(r, args, {"adam_gbs": 1e-5})
+    assert st["adam_bytes_per_step"] == 26_000
+    assert st["bytes_per_step"] == 26_000 + (4000 + 300 + 50 + 1500 + 300 + 25 + 500) / 2
+    assert abs(st["achieved_gbs"] - st["bytes_per_step"] / 1.0 / 1e9) < 1e-18
+    assert abs(st["frac_of_streaming_adam"] - st["achieved_gbs"] / 1e-5) < 1e-9
+    r["link"] = {}
+    st = bench.host_dram_stats(r, SimpleNamespace(h2d_format="bf16", steps=2), None)
+    assert st["bytes_per_step"] == 28_000 + 3000 and st["frac_of_streaming_adam"] is None

@@ -106,7 +106,10 @@ def runtime_streams(device: torch.device) -> Tuple[Any, Any, Any]:
     the first's queues, and its casts ran at 0.64 of peak against 0.74
     when it reused the first's streams (the 2-unit pool schedule after the
     default one, Llama-3-8B).  Sharing the streams between runtimes only
-    adds order between their copies."""
+    adds order between their copies.  They come from torch's stream pool
+    (32 per device and priority, handed out in turn), so a process that asks
+    torch for more streams can be handed one of them for other work, which
+    likewise only adds order."""
     dev = torch.device(device)
     key = dev.index if dev.index is not None else torch.cuda.current_device()
     with _RUNTIME_STREAMS_LOCK:

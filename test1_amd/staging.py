@@ -32,7 +32,6 @@ def _new_event() -> torch.cuda.Event:
     return torch.cuda.Event(enable_timing=False, blocking=False)
 
 
-
 class LayerBufferPool:
     """Fixed set of device units ``{"param", "grad"}`` reused round-robin.
 
@@ -75,7 +74,6 @@ class LayerBufferPool:
             return len(self.pool)
 
 
-
 _BACKLOG_LOCK = threading.Lock()
 
 
@@ -87,7 +85,6 @@ def _backlog(copies: deque) -> int:
         while copies and copies[0].query():
             copies.popleft()
         return len(copies)
-
 
 
 def split_into_pieces(sizes: Sequence[int], piece_elems: int) -> List[Tuple[int, int]]:
@@ -121,8 +118,6 @@ def overlap_ranges(spans: Sequence[Tuple[int, int]], a: int, b: int) -> List[Tup
         if hi > lo:
             out.append((i, lo, hi))
     return out
-
-
 
 
 class _StageTicket:

@@ -20,7 +20,6 @@ from typing import Any, Callable, Optional
 EARLY_UPDATE_PRIORITY = 1 << 30
 
 
-
 class PriorityUpdateExecutor:
     """One worker thread that runs queued host updates lowest priority value
     first, among those whose input is ready.

@@ -201,7 +201,8 @@ int sf_copy_segs_b16(const sf_seg* segs, int nsegs, int max_workgroups,
                      sf_stream_t stream);
 
 /* dst[i] = value for i < n (16-bit elements), as a kernel rather than a
- * memset node so it is safe inside captured graphs.  Replaces
+ * memset node so it is safe inside captured graphs (a GPU test replays a
+ * captured fill and cast four times with eager work between).  Replaces
  * `_current_gpu_cache["grad"].zero_()`, layer_state.py:296-297. */
 int sf_fill_b16(uint16_t* dst, size_t n, uint16_t value,
                 sf_stream_t stream);

@@ -211,6 +211,42 @@ def test_copy_segs_and_fill(dev):
     assert np.array_equal(b.cpu().numpy(), exp)
 
 
+def test_fill_and_cast_in_a_captured_graph(dev):
+    """``sf_fill_b16`` and ``sf_cast_f32_bf16`` are plain kernel launches, so
+    they can be captured in a HIP graph: four replays, each after eager work
+    that overwrites both outputs and a synchronisation, give the fill pattern
+    and the oracle's cast every time."""
+    n = (1 << 20) + 13
+    src = rand_f32(n, seed=11).to(dev)
+    dst = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    buf = torch.zeros(70_000, dtype=torch.int16, device=dev)
+    expect_cast = oracle.cast_f32_bf16(src.cpu().numpy())
+    expect_fill = np.zeros(70_000, np.int16)
+    expect_fill[3:69_998] = 0x1234
+    # warm up on a side stream (the kernels' first launches load their code)
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        kernels.fill_b16_(buf[3:69_998], 0x1234)
+        kernels.cast_f32_bf16_(dst, src)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        kernels.fill_b16_(buf[3:69_998], 0x1234)
+        kernels.cast_f32_bf16_(dst, src)
+    for rep in range(4):
+        buf.fill_(-(rep + 1))
+        buf[:3] = 0
+        buf[69_998:] = 0
+        dst.fill_(float(rep + 7))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(buf.cpu().numpy(), expect_fill), rep
+        assert np.array_equal(bits16(dst), expect_cast), rep
+
+
 def test_pinned_memcpy_round_trip(dev):
     n = 3 * (1 << 20) + 7
     h = pinned_empty(n, torch.float32)

@@ -110,21 +110,27 @@ struct ToF16 {
 // Workgroup b owns groups [b*kCastThreads*kCastUnroll, (b+1)*kCastThreads*kCastUnroll);
 // within it, unroll step k covers one contiguous run of kCastThreads groups,
 // so every load/store instruction of a wave touches one contiguous 2 KiB
-// span.  Loads are ordinary (cached) 128-bit loads and stores are
-// nontemporal.  On gfx950, 218M-element layer, alternating runs on one box:
-// 2 groups per lane 6.16 TB/s, against 5.61 TB/s with nontemporal loads as
-// well, 6.04 TB/s with 4 groups per lane and 5.70 TB/s with 8; 128-lane
-// workgroups (256 groups each) 6.19.  One group per lane (256 groups per
-// workgroup, 106,500 workgroups), measured later on another box in the
-// training step: 0.2172-0.2182 ms per layer alone against 0.2245-0.2253
-// with 2 groups, and 0.245-0.249 against 0.252-0.256 ms beside the
-// backward's kernels.  Workgroup size, one group per lane, same layer, two
-// rounds on one box: 64 lanes 0.214 ms, 128 lanes 0.2124-0.2131 (6.15 TB/s,
-// 0.77 of peak), 256 lanes 0.2144-0.2157, 512 0.216-0.217, 1024 0.221-0.222;
-// a plain fp32 copy of the same bytes reaches 0.79 of peak.  Loads with every
-// lane's 16 bytes contiguous across the wave (then 8-byte stores, or 16-byte
-// stores after a lane-pair exchange), a blockIdx order that gives each XCD
-// one contiguous eighth, and persistent grid-stride loops were no faster.
+// span.  Loads and stores are nontemporal 128-bit accesses.  With cached
+// loads the cast's rate depended on the work before it, falling with the
+// bytes that work had written; with nontemporal loads it does not (one
+// Llama layer, 10 casts per case, two rounds on one box, fraction of HBM
+// peak):
+//                         cached loads   nontemporal loads
+//   back to back          0.759-0.763    0.777-0.780
+//   after 20 bf16 GEMMs   0.733-0.738    0.766-0.768
+//   after 4 x 1 GiB copy  0.676-0.680    0.767-0.769
+// The sc0/sc1 bits changed nothing beside nt; plain stores were slower.
+// Other shapes, one box each: 2 groups per lane 6.16 TB/s (then with
+// nontemporal loads 5.61), 4 groups 6.04, 8 groups 5.70; one group per
+// lane, measured in the training step: 0.2172-0.2182 ms per layer alone
+// against 0.2245-0.2253 with 2 groups.  Workgroup size, one group per lane,
+// two rounds on one box: 64 lanes 0.214 ms, 128 lanes 0.2124-0.2131 (6.15
+// TB/s, 0.77 of peak), 256 lanes 0.2144-0.2157, 512 0.216-0.217, 1024
+// 0.221-0.222; a plain fp32 copy of the same bytes reaches 0.79 of peak.
+// Loads with every lane's 16 bytes contiguous across the wave (then 8-byte
+// stores, or 16-byte stores after a lane-pair exchange), a blockIdx order
+// that gives each XCD one contiguous eighth, and persistent grid-stride
+// loops were no faster.
 // ---------------------------------------------------------------------
 template <typename Fmt>
 __device__ __forceinline__ void cast_flat_body(const float* __restrict__ src, uint16_t* __restrict__ dst,
@@ -143,8 +149,8 @@ __device__ __forceinline__ void cast_flat_body(const float* __restrict__ src, ui
 #pragma unroll
         for (int k = 0; k < kCastUnroll; ++k) {
             const f32x4* p = reinterpret_cast<const f32x4*>(src + (tile0 + k * kCastThreads + threadIdx.x) * kGroup);
-            a[k] = p[0];
-            b[k] = p[1];
+            a[k] = __builtin_nontemporal_load(p);
+            b[k] = __builtin_nontemporal_load(p + 1);
         }
 #pragma unroll
         for (int k = 0; k < kCastUnroll; ++k) {
@@ -156,7 +162,8 @@ __device__ __forceinline__ void cast_flat_body(const float* __restrict__ src, ui
             const uint64_t g = tile0 + k * kCastThreads + threadIdx.x;
             if (g < n8) {
                 const f32x4* p = reinterpret_cast<const f32x4*>(src + g * kGroup);
-                __builtin_nontemporal_store(Fmt::cast8(p[0], p[1]), reinterpret_cast<u32x4*>(dst + g * kGroup));
+                __builtin_nontemporal_store(Fmt::cast8(__builtin_nontemporal_load(p), __builtin_nontemporal_load(p + 1)),
+                                            reinterpret_cast<u32x4*>(dst + g * kGroup));
             }
         }
     }

@@ -139,6 +139,9 @@ class Device:
         self.races = []
         self.skip_waits = {}        # stream name -> True: its waits are dropped (planted mistakes)
         self.skip_dma_waits = False  # True: SDMA completions are not seen (planted mistakes)
+        # True: stream copies that read or write host tensors log those host
+        # ranges too, so host buffers shared by copies are checked as well
+        self.track_host = False
         self._sdma = itertools.count()
         self.default = FakeStream(self, "compute")
         Device.current = self
@@ -262,11 +265,15 @@ class Device:
                     self._access(*self.span(t), stream.name, vc, False, what)
                 elif isinstance(t, torch.Tensor):
                     touches_host = True
+                    if self.track_host:
+                        self._access(*self.host_span(t), stream.name, vc, False, what)
             for t in writes:
                 if self.is_dev(t):
                     self._access(*self.span(t), stream.name, vc, True, what)
                 elif isinstance(t, torch.Tensor):
                     touches_host = True
+                    if self.track_host:
+                        self._access(*self.host_span(t), stream.name, vc, True, what)
             if touches_host:
                 self.host_copies.append((stream.name, vc))
             return vc
@@ -355,7 +362,7 @@ def fake_kernels(dev: Device):
             return (0, 0)
 
     def dma_copy_d2h(pairs, timeout=None):
-        return [dev.sdma_copy(src, dst, what="SDMA gradient copy") for src, dst in pairs]
+        return [dev.sdma_copy(src, dst, what="SDMA copy") for src, dst in pairs]
 
     def wait_event(ev, timeout, what):
         ev.synchronize()

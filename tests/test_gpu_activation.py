@@ -6,6 +6,7 @@ import pytest
 import torch
 from torch.utils.checkpoint import checkpoint
 
+from test1_amd import kernels
 from test1_amd.pinned import pinned_empty
 from test1_amd.sliding_checkpoint import ActivationRing, SlidingCheckpoint, StorageSpill
 
@@ -13,8 +14,13 @@ pytestmark = pytest.mark.gpu
 
 
 def run_layers(dev, L, shape, weights, offload, seen, use_ring=True, spill_dir=None, mask=None):
-    """``offload``: None (plain checkpointing), "host" (pinned slots) or
+    """``offload``: None (plain checkpointing), "host" (pinned slots, packed by
+    the kernel), "host_sdma" (pinned slots, packed by SDMA copies) or
     "storage" (files under ``spill_dir`` through a 3-slot StorageSpill)."""
+    pack_engine = "sdma" if offload == "host_sdma" else "kernel"
+    if offload == "host_sdma":
+        offload = "host"
+        kernels.dma_init(dev)
     h = torch.randn(shape, generator=torch.Generator().manual_seed(0)).bfloat16().to(dev).requires_grad_(True)
     slots = [[pinned_empty(shape, torch.bfloat16)] for _ in range(L)] if offload == "host" else None
     paths = ([[f"{spill_dir}/act-{i}-{c}.bin" for c in range(4)] for i in range(L)]
@@ -33,19 +39,21 @@ def run_layers(dev, L, shape, weights, offload, seen, use_ring=True, spill_dir=N
         if offload:
             with SlidingCheckpoint(layer_idx=i + 1, layer_tensors=slots, gds_offload=offload == "storage",
                                    file_paths=paths, is_last_layer=(i == L - 1), no_mask=mask is None,
-                                   device=str(dev), prefetch_ring=ring, spill=spill):
+                                   device=str(dev), prefetch_ring=ring, spill=spill, pack_engine=pack_engine):
                 x = checkpoint(layer_fn, *args, use_reentrant=False)
         else:
             x = checkpoint(layer_fn, *args, use_reentrant=False)
     x.float().sum().backward()
     torch.cuda.synchronize()
+    if ring is not None:
+        ring.close()
     if spill is not None:
         spill.close()
     return [w.grad.clone() for w in weights], h.grad.clone(), slots
 
 
 @pytest.mark.parametrize("use_ring", [True, False])
-@pytest.mark.parametrize("mode", ["host", "storage"])
+@pytest.mark.parametrize("mode", ["host", "host_sdma", "storage"])
 def test_round_trip_bit_exact_small(dev, use_ring, mode, tmp_path):
     L, shape = 6, (2, 128, 256)
     ws = [torch.randn(shape[-1], generator=torch.Generator().manual_seed(10 + i)).bfloat16().to(dev).requires_grad_(True)
@@ -55,7 +63,7 @@ def test_round_trip_bit_exact_small(dev, use_ring, mode, tmp_path):
     for i in range(L):
         fwd, rec = seen[i]
         assert torch.equal(fwd.view(torch.int16), rec.view(torch.int16)), f"layer {i} input changed"
-        if i < L - 1 and mode == "host":  # every layer but the last went through its host slot
+        if i < L - 1 and mode != "storage":  # every layer but the last went through its host slot
             assert torch.equal(slots[i][0].view(torch.int16), fwd.cpu().view(torch.int16))
     for w in ws:
         w.grad = None
@@ -86,12 +94,12 @@ def test_storage_two_tensors_per_layer(dev, tmp_path):
     assert torch.equal(hg_off.view(torch.int16), hg_ref.view(torch.int16))
 
 
-@pytest.mark.parametrize("mode", ["host", "storage"])
+@pytest.mark.parametrize("mode", ["host", "host_sdma", "storage"])
 @pytest.mark.parametrize("L,shape", [(32, (4, 1024, 4096)), (48, (2, 4096, 5120))],
                          ids=["llama3-8b", "qwen2.5-14b"])
 def test_round_trip_model_checkpoint_shapes(dev, L, shape, mode, tmp_path):
-    """The models' checkpoints through the pinned slots (or through files on
-    local storage) and back, bit-exact: 32 layers of [4, 1024, 4096] bf16
+    """The models' checkpoints through the pinned slots (packed by the kernel
+    or by SDMA copies, or through files on local storage) and back, bit-exact: 32 layers of [4, 1024, 4096] bf16
     (32 MiB each, Llama-3-8B at batch 4 x 1024) and 48 layers of
     [2, 4096, 5120] (80 MiB each, Qwen2.5-14B at batch 2 x 4096)."""
     ws = [torch.full((shape[-1],), 1.0 + 1e-2 * i, dtype=torch.bfloat16, device=dev, requires_grad=True)

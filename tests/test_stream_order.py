@@ -17,7 +17,10 @@ Each protocol is checked as the runtime runs it and with one planted mistake
   reloads, ``to_device_async`` / ``wait_for_h2d``);
 * checkpoint packs and the two-set prefetch ring of ``SlidingCheckpoint``:
   the pack source kept from reuse by ``record_stream``, a ring set refilled
-  only after the recompute that read it;
+  only after the recompute that read it, each prefetch ordered after its
+  decoder's last pack (an event), and with SDMA packs the copy started after
+  its source's producer, the source held and the slot read only after the
+  copy was seen complete;
 * gradient offload on SDMA engines (``_d2h_task`` / ``_do_update``): the copy
   reads the gradients after their event, the host AdamW reads the slot after
   the copy, and the slot and the gradients' memory are reused only after it;
@@ -222,10 +225,20 @@ def test_backward_bf16_reload_without_the_units_fence_races(dev, monkeypatch):
 # ---------------------------------------------------------------------------
 
 def _checkpoint_round_trip(dev, L=6, shape=(2, 8, 64), one_set=False, drop_record_stream=False,
-                           before_pin=None, pin_check=None, monkeypatch=None):
+                           before_pin=None, pin_check=None, monkeypatch=None, pack_engine="kernel",
+                           free_sources_early=None, drain_before_pin=False):
+    """L decoders' checkpoints packed in the forward (kernel on the D2H stream
+    or SDMA copies issued by the ring's worker) and prefetched back on the
+    H2D stream in the backward, the host slots' ranges tracked as well.  The
+    autograd graph keeps only the packed copy: a source is freed right after
+    its pack (the kernel path; its ``record_stream`` fences the reuse) or
+    once the ring has released it (the SDMA path)."""
     from test1_amd import sliding_checkpoint as sc_mod
     from test1_amd.sliding_checkpoint import ActivationRing, SlidingCheckpoint
 
+    dev.track_host = True
+    if free_sources_early is None:
+        free_sources_early = pack_engine == "kernel"
     if monkeypatch is not None:
         def pinned(shape_, dtype):
             if pin_check is not None:
@@ -244,33 +257,90 @@ def _checkpoint_round_trip(dev, L=6, shape=(2, 8, 64), one_set=False, drop_recor
     comp = dev.default
     d2h, h2d = hb_model.FakeStream(dev, "d2h"), hb_model.FakeStream(dev, "h2d")
     ring = ActivationRing("cuda:0")
+    if drain_before_pin:
+        def before_pin():
+            dev.synchronize()
+            ring.drain_packs()
     slots = [[None] for _ in range(L)]
-    scs, packed = [], []
+    scs, packed, held = [], [], []
     x = dev.alloc(shape, torch.bfloat16)
     dev.op(comp, writes=[x], what="embedding writing the first layer's input")
-    for i in range(L):
-        sc = SlidingCheckpoint(layer_idx=i + 1, layer_tensors=slots, is_last_layer=(i == L - 1), no_mask=True,
-                               device="cuda:0", stream=d2h, prefetch_stream=h2d, prefetch_ring=ring,
-                               before_pin=before_pin)
-        packed.append(sc.pack_hook(x))
-        scs.append(sc)
-        y = dev.alloc(shape, torch.bfloat16)
-        dev.op(comp, reads=[x], writes=[y], what=f"layer {i} forward")
-        if i < L - 1:
-            dev.free(x)       # the autograd graph keeps only the packed copy
-        x = y
-    for i in range(L - 1, -1, -1):
-        t = scs[i].unpack_hook(packed[i])
-        dev.op(comp, reads=[t], what=f"layer {i} recompute")
-        tmp = dev.alloc(shape, torch.bfloat16)      # the recompute's own activations
-        dev.op(comp, writes=[tmp], what=f"layer {i} backward")
-        dev.free(tmp)
+    try:
+        for i in range(L):
+            sc = SlidingCheckpoint(layer_idx=i + 1, layer_tensors=slots, is_last_layer=(i == L - 1), no_mask=True,
+                                   device="cuda:0", stream=d2h, prefetch_stream=h2d, prefetch_ring=ring,
+                                   before_pin=before_pin, pack_engine=pack_engine)
+            packed.append(sc.pack_hook(x))
+            scs.append(sc)
+            y = dev.alloc(shape, torch.bfloat16)
+            dev.op(comp, reads=[x], writes=[y], what=f"layer {i} forward")
+            if i < L - 1:
+                if free_sources_early:
+                    dev.free(x)   # the autograd graph keeps only the packed copy
+                else:
+                    held.append(x)
+            x = y
+        for i in range(L - 1, -1, -1):
+            t = scs[i].unpack_hook(packed[i])
+            dev.op(comp, reads=[t], what=f"layer {i} recompute")
+            tmp = dev.alloc(shape, torch.bfloat16)      # the recompute's own activations
+            dev.op(comp, writes=[tmp], what=f"layer {i} backward")
+            dev.free(tmp)
+    finally:
+        ring.close()
     return slots
 
 
-def test_checkpoint_round_trip_is_ordered(dev, monkeypatch):
-    _checkpoint_round_trip(dev, monkeypatch=monkeypatch)
+@pytest.mark.parametrize("free_sources_early", [True, False])
+def test_checkpoint_round_trip_is_ordered(dev, monkeypatch, free_sources_early):
+    _checkpoint_round_trip(dev, monkeypatch=monkeypatch, free_sources_early=free_sources_early)
     assert dev.races == []
+
+
+def test_checkpoint_prefetch_without_the_pack_event_races(dev, monkeypatch):
+    """The prefetch on the H2D stream reads a host slot that the pack kernel
+    on the D2H stream wrote: without the event recorded after the decoder's
+    last pack the two copies are unordered.  (They were ordered only while
+    both ran on one stream, or when the source's memory happened to be
+    reused first: the caching allocator then waits for the pack; here the
+    sources stay allocated.)"""
+    from test1_amd.sliding_checkpoint import ActivationRing
+
+    class _Forgetful(dict):
+        def __setitem__(self, k, v):
+            pass
+
+    real_init = ActivationRing.__init__
+
+    def init(self, *a, **kw):
+        real_init(self, *a, **kw)
+        self.packed_events = _Forgetful()
+    monkeypatch.setattr(ActivationRing, "__init__", init)
+    _checkpoint_round_trip(dev, monkeypatch=monkeypatch, free_sources_early=False)
+    assert any("copy on h2d" in r and "pack on d2h" in r for r in dev.races), dev.races
+
+
+def test_checkpoint_round_trip_on_sdma_is_ordered(dev, monkeypatch):
+    """Packs by SDMA copies: each starts after its source's producer (a host
+    wait on the compute stream's event), the prefetch reads the slot after
+    the copy was seen complete, and the source is freed only then."""
+    _checkpoint_round_trip(dev, monkeypatch=monkeypatch, pack_engine="sdma")
+    assert dev.races == []
+
+
+def test_checkpoint_sdma_prefetch_without_settling_races(dev, monkeypatch):
+    from test1_amd.sliding_checkpoint import ActivationRing
+
+    monkeypatch.setattr(ActivationRing, "settle_packs", lambda self, key, layer, timing=None: None)
+    _checkpoint_round_trip(dev, monkeypatch=monkeypatch, pack_engine="sdma")
+    assert any("copy on h2d" in r and "SDMA copy" in r for r in dev.races), dev.races
+
+
+def test_checkpoint_sdma_source_freed_before_its_copy_races(dev, monkeypatch):
+    """The autograd graph drops a checkpoint's source after the pack; the
+    ring must keep it until its SDMA copy has been seen complete."""
+    _checkpoint_round_trip(dev, monkeypatch=monkeypatch, pack_engine="sdma", free_sources_early=True)
+    assert any("forward" in r and "SDMA copy" in r for r in dev.races), dev.races
 
 
 def test_prefetch_ring_of_one_set_races(dev, monkeypatch):
@@ -288,14 +358,17 @@ def test_pack_source_without_record_stream_races(dev, monkeypatch):
     assert any("pack on d2h" in r for r in dev.races), dev.races
 
 
-def test_checkpoint_slots_pinned_only_with_no_host_copy_in_flight(dev, monkeypatch):
+@pytest.mark.parametrize("pack_engine", ["kernel", "sdma"])
+def test_checkpoint_slots_pinned_only_with_no_host_copy_in_flight(dev, monkeypatch, pack_engine):
     """Slots pinned inside the forward (first step, new batch shape) are
-    pinned after ``before_pin`` (the model drains its copies there), never
-    while a copy into or out of host memory is in flight."""
+    pinned after ``before_pin`` (the model drains its copies there: the
+    device and the ring's SDMA packs), never while a copy into or out of
+    host memory is in flight."""
     def check():
         assert dev.outstanding_host_copies() == [], "pinned while host copies were in flight"
 
-    _checkpoint_round_trip(dev, before_pin=dev.synchronize, pin_check=check, monkeypatch=monkeypatch)
+    _checkpoint_round_trip(dev, pin_check=check, monkeypatch=monkeypatch, pack_engine=pack_engine,
+                           drain_before_pin=True)
     assert dev.races == []
 
 
@@ -391,8 +464,8 @@ def test_gradient_slot_read_before_the_copy_lands_races(dev):
     """An update (and a slot reuse) that does not wait for the SDMA copies:
     the host AdamW reads the slot while an engine may still write it."""
     _grad_offload(dev, skip_dma_waits=True)
-    assert any("host AdamW" in r and "SDMA gradient copy" in r for r in dev.races), dev.races
-    assert any("backward writing" in r and "SDMA gradient copy" in r for r in dev.races), dev.races
+    assert any("host AdamW" in r and "SDMA copy" in r for r in dev.races), dev.races
+    assert any("backward writing" in r and "SDMA copy" in r for r in dev.races), dev.races
 
 
 # ---------------------------------------------------------------------------

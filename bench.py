@@ -985,16 +985,19 @@ def run_child_workload(workload: str, steps: int, warmup: int, env_hw_queues: Op
     }
 
 
-def secondary_rooflines(r: dict, alone: Optional[dict] = None) -> list:
-    """Host-link-bound kernels besides the staging cast: achieved rate over
-    their own intervals in the step (timing events around each launch on its
-    stream; the link is shared with the copies running beside them) and, in
-    ``alone``, on an idle GPU."""
+def secondary_rooflines(r: dict, alone: Optional[dict] = None, checkpoint_d2h: str = "kernel") -> list:
+    """Host-link-bound work besides the staging cast: achieved rate over its
+    own intervals in the step (timing events around each launch on its
+    stream, or an SDMA engine's timestamps; the link is shared with the
+    copies running beside it) and, in ``alone``, on an idle GPU."""
     lk = r["link"]
     rows = []
+    if checkpoint_d2h == "sdma":
+        ckpt = ("checkpoints", "d2h", "SDMA copy (ROCr, engine 3)", "checkpoint copy: HBM -> pinned host slot")
+    else:
+        ckpt = ("checkpoints", "d2h", "seg_kernel<OpCopy16> (16 workgroups)", "checkpoint pack: HBM -> pinned host slot")
     for kind, d, kernel, what in (
-            ("checkpoints", "d2h", "seg_kernel<OpCopy16> (16 workgroups)",
-             "checkpoint pack: HBM -> pinned host slot"),
+            ckpt,
             ("rows", "h2d", "gather_rows_kernel<cast>", "embedding lookup: batch rows of the pinned fp32 host "
                                                           "table -> bf16 hidden states in HBM"),
             ("rows", "d2h", "gather_rows_kernel<copy> (16 workgroups)",
@@ -1247,7 +1250,8 @@ def main():
                         "update)")
                      + "; alone: one decoder layer's cast on an idle GPU after the timed steps"),
         },
-        "roofline_secondary": secondary_rooflines(r, kernels_alone),
+        "roofline_secondary": secondary_rooflines(
+            r, kernels_alone, args.checkpoint_d2h or ("sdma" if args.d2h_engine == "sdma" else "kernel")),
         "host_link": dict(link_stats(r, args.steps, link_alone_gbs), h2d_idle=r["h2d_idle"]),
         "model_tflops": {
             "flops_per_step": megatron_flops_per_step(w),

@@ -801,8 +801,9 @@ def param_streaming(sf, dev, passes: int = 3, seq: int = 1024) -> dict:
 def activation_round_trip(dev, L: int = 32, shape=(4, 1024, 4096), rounds: int = 4, warmup: int = 2) -> dict:
     """The activation-offload configuration: ``L`` checkpointed layers whose
     bf16 inputs of ``shape`` (N(0,1)) go to pinned host slots through
-    ``SlidingCheckpoint`` in the forward (pack kernel on the offload stream)
-    and come back one layer ahead in the backward (prefetch on the H2D stream,
+    ``SlidingCheckpoint`` in the forward (SDMA copies, as SlideFSDP makes
+    them with its default engines) and come back one layer ahead in the
+    backward (prefetch on the H2D stream,
     reference sliding_checkpoint.py:51-131), on the runtime's streams.  The layers compute an
     elementwise ``tanh(x) * w``, so the copies dominate.  The first
     ``warmup`` rounds are not timed (in a fresh process the first call's
@@ -813,10 +814,13 @@ def activation_round_trip(dev, L: int = 32, shape=(4, 1024, 4096), rounds: int =
     import torch
     from torch.utils.checkpoint import checkpoint
 
+    from test1_amd import kernels as _k
     from test1_amd.layer_state import runtime_streams
     from test1_amd.pinned import pinned_empty
     from test1_amd.sliding_checkpoint import ActivationRing, SlidingCheckpoint
 
+    _k.dma_init(dev)
+    _k.dma_enable_timing(True)
     slots = [[pinned_empty(shape, torch.bfloat16)] for _ in range(L)]
     # the streams SlideFSDP gives the checkpoint offload and its prefetch
     h2d, _, d2h = runtime_streams(dev)
@@ -849,7 +853,7 @@ def activation_round_trip(dev, L: int = 32, shape=(4, 1024, 4096), rounds: int =
                 inputs.append(x.detach())
             with SlidingCheckpoint(layer_idx=i + 1, layer_tensors=slots, is_last_layer=(i == L - 1), no_mask=True,
                                    device=str(dev), stream=d2h, prefetch_stream=h2d, prefetch_ring=ring,
-                                   link_timing=lt, served=served):
+                                   link_timing=lt, served=served, pack_engine="sdma"):
                 x = checkpoint(layer_fn, x, ws[i], use_reentrant=False)
         loss = x.float().sum()
         torch.cuda.synchronize()
@@ -864,8 +868,8 @@ def activation_round_trip(dev, L: int = 32, shape=(4, 1024, 4096), rounds: int =
             continue
         fwd_ms += (t1 - t0) * 1e3
         bwd_ms += (t2 - t1) * 1e3
-        d2h_sp += [(anchor.elapsed_time(a) + 1e6 * rnd, anchor.elapsed_time(b) + 1e6 * rnd, n)
-                   for a, b, n in lt["act_d2h"]]
+        # SDMA copies: engine timestamps (ns of the system clock)
+        d2h_sp += [(rec[1] * 1e-6, rec[2] * 1e-6, rec[3]) for rec in lt["act_d2h"] if rec[0] == "interval_ns"]
         h2d_sp += [(anchor.elapsed_time(a) + 1e6 * rnd, anchor.elapsed_time(b) + 1e6 * rnd, n)
                    for a, b, n in lt["act_h2d"]]
         if check:
@@ -880,6 +884,7 @@ def activation_round_trip(dev, L: int = 32, shape=(4, 1024, 4096), rounds: int =
         out[d] = {"bytes_per_round": nb / timed, "transfers_per_round": len(sp) / timed,
                   "busy_ms_per_round": busy / timed, "gbs_while_busy": gbs,
                   "frac": None if gbs is None else gbs / LINK_PEAK_GBS}
+    ring.close()
     del slots
     per_layer = 2 * math.prod(shape)
     return {
@@ -891,9 +896,9 @@ def activation_round_trip(dev, L: int = 32, shape=(4, 1024, 4096), rounds: int =
         "unit": "GB/s (the slower direction, while busy)", "rounds_timed": timed,
         "forward_ms_per_round": fwd_ms / timed, "backward_ms_per_round": bwd_ms / timed,
         "d2h": out["d2h"], "h2d": out["h2d"], "bit_exact": exact,
-        "note": ("d2h: the pack kernel (seg_kernel<OpCopy16>, 16 workgroups) into the pinned slots; h2d: "
-                 "hipMemcpyAsync of each slot into a 2-set device ring; rates over the union of each "
-                 "direction's transfer intervals (HIP events on their streams)"),
+        "note": ("d2h: SDMA copies (ROCr, engine 3) into the pinned slots, started by the ring's worker "
+                 "thread; h2d: hipMemcpyAsync of each slot into a 2-set device ring; rates over the union of "
+                 "each direction's transfer intervals (engine timestamps, HIP events on the H2D stream)"),
     }
 
 

@@ -496,7 +496,8 @@ def link_timeline(rt, anchor, anchor_ns: int) -> dict:
                 "rows": spans(lt.get("rows_d2h"))},
         "compute": [(ns(a), ns(b)) for a, b in lt.get("compute", [])],
         "common_clock": anchor_ns != 0,
-        "untimed_d2h_bytes": sum(rec[1] for rec in rt.d2h_timing or [] if _untimed(rec)),
+        "untimed_d2h_bytes": sum(rec[1] for rec in list(rt.d2h_timing or []) + list(lt.get("act_d2h") or [])
+                                 if _untimed(rec)),
     }
 
 
@@ -616,8 +617,9 @@ def link_stats(r: dict, steps: int, alone: Optional[dict] = None) -> dict:
         untimed = lk.get(f"untimed_{d}_bytes", 0)
         if untimed:
             out[d]["untimed_bytes_per_step"] = untimed / steps
-            out[d]["untimed_note"] = ("gradient copies without SDMA engine timestamps (a profiler tracing async "
-                                      "copies takes them over): the rates above cover the timed transfers only")
+            out[d]["untimed_note"] = ("SDMA copies (gradients, checkpoints) without engine timestamps (a profiler "
+                                      "tracing async copies takes them over): the rates above cover the timed "
+                                      "transfers only")
     out["compute_busy_frac_of_step"] = _length(comp) * 1e-9 / r["elapsed"]
     out["note"] = ("rates over the union of all transfers of a direction (h2d: parameter copies, checkpoint "
                    "prefetches, embedding lookup rows; d2h: SDMA gradient copies, checkpoint packs, embedding "

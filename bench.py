@@ -262,7 +262,8 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
     sf = SlideFSDP(model, cfg, d2h_engine=d2h_engine, h2d_format=h2d_format, resident_layers=resident_layers,
                    fused_cross_entropy=args.fused_ce, update_piece_elems=args.piece_elems,
                    cast_at_use=not args.cast_on_copy, early_embedding_update=not args.no_early_embedding,
-                   bf16_reload=False if args.no_bf16_reload else None, checkpoint_d2h=args.checkpoint_d2h, **kw)
+                   bf16_reload=False if args.no_bf16_reload else None, checkpoint_d2h=args.checkpoint_d2h,
+                   h2d_issue_limit=args.h2d_issue_limit, **kw)
     uses_storage = args.ac_offload == "nvme" or args.opt_nvme_fraction > 0
     log(f"[bench] SlideFSDP ({h2d_format} H2D, {sf.resident_layers} resident decoders, {d2h_engine} D2H) "
         f"ready in {time.time() - t0:.1f}s")
@@ -1056,6 +1057,8 @@ def main():
                          "run piece by piece, one cast per unit), e.g. 67108864; 0: whole units")
     ap.add_argument("--checkpoint-d2h", default=None, choices=("sdma", "kernel"),
                     help="how checkpoints reach their pinned slots (default: sdma with the sdma D2H engine)")
+    ap.add_argument("--h2d-issue-limit", type=int, default=3,
+                    help="unit copies the forward and backward may keep queued before they wait (0: no limit)")
     ap.add_argument("--no-early-embedding", action="store_true",
                     help="update the embedding's untouched rows with its batch rows, after the backward, "
                          "instead of as the backward starts")
@@ -1226,7 +1229,7 @@ def main():
                    "checkpoint_d2h": args.checkpoint_d2h or ("sdma" if args.d2h_engine == "sdma" else "kernel"),
                    "fused_cross_entropy": args.fused_ce,
                    "stage_after_update": r["stage_after_update"],
-                   "update_piece_elems": args.piece_elems,
+                   "update_piece_elems": args.piece_elems, "h2d_issue_limit": args.h2d_issue_limit,
                    "cast_at_use": r["cast_at_use"],
                    "bf16_reload_units": r["bf16_reload_units"],
                    "early_embedding_update": not args.no_early_embedding,

@@ -161,6 +161,9 @@ class StreamingRuntime:
         # Host AdamW team size (0: leave the library's setting alone); see
         # set_adam_threads.
         self.adam_threads = 0
+        # Unit copies the forward and backward may keep queued on the H2D
+        # stream before they hold the host (0: no limit); see ``hold_h2d``.
+        self.h2d_issue_limit = 0
         self._adam_threads_set = 0
         # Workgroups of the kernels that write into pinned host memory (grad
         # rows and checkpoint offload): 16 move 55-56 GB/s alone and 48-49
@@ -294,6 +297,22 @@ class StreamingRuntime:
         if self.bf16_loader is not self.stager:
             n += self.bf16_loader.backlog()
         return n
+
+    def hold_h2d(self, what: str) -> None:
+        """Before the forward or the backward issues a unit copy: while
+        ``h2d_issue_limit`` or more unit copies are queued, wait for the
+        oldest to complete (bounded by the wait limit).  A queued HIP copy
+        holds an SDMA engine until it has run, and the HIP runtime puts each
+        new copy on the first engine not held: with many copies queued, the
+        later ones land on engines that copy slower."""
+        limit = self.h2d_issue_limit
+        if not limit:
+            return
+        while self.h2d_backlog() >= limit:
+            oldest = [q[0] for q in (self.stager._copies, self.bf16_loader._copies) if q]
+            if not oldest:
+                return
+            kernels.wait_event(oldest[0], self.wait_timeout, what)
 
     def init_grad_slots(self, unit_sizes: Dict[int, int], fallback_depth: int = 3) -> None:
         """One pinned slot per unit; if the host cannot pin that much (the
@@ -628,6 +647,8 @@ class LayerRuntimeState(RowSparseEmbedding, nn.Module):
         # The backward of an embedding never reads its weights (its gradient
         # depends only on the indices), so no copy or cast is needed then.
         skip = is_backward and not self.backward_reads_params
+        if not skip:
+            self.runtime.hold_h2d(f"unit {self.layer_idx}: queued copies before its load")
         if self._cpu_params_bf16 is not None:
             unit = self._acquire_unit()
             self._h2d_done = unit["ready"] if skip else stager.load(self._cpu_params_bf16, unit["param"], unit["ready"])

@@ -215,6 +215,17 @@ class SlideFSDP(nn.Module):
                          kernel on the D2H stream.  A kernel writing into host
                          memory slows the kernels beside it (a bf16 GEMM ran
                          24-27 % slower), an SDMA engine does not.  Same bits.
+      h2d_issue_limit    3 (default; 0: no limit): the forward and the
+                         backward wait before a unit's load while that many
+                         unit copies are still queued on the H2D stream.  A
+                         queued HIP copy holds an SDMA engine, and later
+                         copies then land on engines 4-7, which copy slower:
+                         in the 2-unit pool schedule up to eight engines were
+                         held at once.  There (Llama-3.1-8B, alternating, two
+                         boxes) 4,204-4,340 tokens/s against 4,200-4,246,
+                         H2D 52.0-52.6 GB/s against 50.7-51.1 while busy;
+                         units with their own buffers rarely load in the
+                         forward, and the default step was unchanged.
       cast_at_use        True (default): with fp32 H2D, a unit's fp32 master
                          is copied into a device fp32 slot of its own size
                          (right after its update for a unit with its own
@@ -247,7 +258,8 @@ class SlideFSDP(nn.Module):
                  resident_layers: Optional[int] = None, row_sparse_embedding: bool = True,
                  fused_cross_entropy: bool = False, stage_after_update: bool = True,
                  update_piece_elems: int = 0, cast_at_use: bool = True, early_embedding_update: bool = True,
-                 bf16_reload: Optional[bool] = None, checkpoint_d2h: Optional[str] = None):
+                 bf16_reload: Optional[bool] = None, checkpoint_d2h: Optional[str] = None,
+                 h2d_issue_limit: int = 3):
         super().__init__()
         if config.param_transfer_mode != "full":
             raise NotImplementedError("SlideFSDP runs on one GPU: only param_transfer_mode='full' is supported")
@@ -274,6 +286,9 @@ class SlideFSDP(nn.Module):
         if update_piece_elems < 0:
             raise ValueError("update_piece_elems must be >= 0")
         self.runtime.piece_elems = int(update_piece_elems)
+        if h2d_issue_limit < 0:
+            raise ValueError("h2d_issue_limit must be >= 0")
+        self.runtime.h2d_issue_limit = int(h2d_issue_limit)
         self.runtime.cast_at_use = bool(cast_at_use) and h2d_format == "fp32"
         self._early_embedding_update = bool(early_embedding_update)
         self.buffer_pool = self.runtime.pool

@@ -151,12 +151,19 @@ def _unit_state(dev, idx, runtime, master):
     return st
 
 
-def _runtime(dev, stager, pool_size=2):
+def _runtime(dev, stager, pool_size=2, h2d_issue_limit=0):
+    from types import MethodType
+
+    from test1_amd.layer_state import StreamingRuntime
     from test1_amd.staging import BF16Loader, LayerBufferPool
 
-    return SimpleNamespace(stager=stager, pool=LayerBufferPool(N, torch.bfloat16, "cuda:0", pool_size),
-                           bf16_loader=BF16Loader(stager.h2d_stream, timing_source=stager),
-                           cast_at_use=True, wait_timeout=1.0, log=lambda *a: None, mark=lambda *a: None)
+    rt = SimpleNamespace(stager=stager, pool=LayerBufferPool(N, torch.bfloat16, "cuda:0", pool_size),
+                         bf16_loader=BF16Loader(stager.h2d_stream, timing_source=stager),
+                         cast_at_use=True, wait_timeout=1.0, log=lambda *a: None, mark=lambda *a: None,
+                         h2d_issue_limit=h2d_issue_limit)
+    rt.h2d_backlog = MethodType(StreamingRuntime.h2d_backlog, rt)
+    rt.hold_h2d = MethodType(StreamingRuntime.hold_h2d, rt)
+    return rt
 
 
 def _pool_step(dev, rt, states):
@@ -186,8 +193,11 @@ def _pool_step(dev, rt, states):
         st._maybe_release_after_backward()
 
 
-def test_pool_loads_cast_at_use_forward_and_backward(dev):
-    rt = _runtime(dev, _stager(dev))
+@pytest.mark.parametrize("issue_limit", [0, 1, 2])
+def test_pool_loads_cast_at_use_forward_and_backward(dev, issue_limit):
+    """The pool step, also with the host held while ``issue_limit`` unit
+    copies are queued (the hold only waits for issued copies)."""
+    rt = _runtime(dev, _stager(dev), h2d_issue_limit=issue_limit)
     _pool_step(dev, rt, [_unit_state(dev, i, rt, torch.randn(N)) for i in range(5)])
     assert dev.races == []
     assert rt.pool.available() == 2

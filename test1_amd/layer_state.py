@@ -309,10 +309,16 @@ class StreamingRuntime:
         if not limit:
             return
         while self.h2d_backlog() >= limit:
-            oldest = [q[0] for q in (self.stager._copies, self.bf16_loader._copies) if q]
-            if not oldest:
+            oldest = None
+            for q in (self.stager._copies, self.bf16_loader._copies):
+                try:
+                    oldest = q[0]   # other threads may trim the queue meanwhile
+                    break
+                except IndexError:
+                    continue
+            if oldest is None:
                 return
-            kernels.wait_event(oldest[0], self.wait_timeout, what)
+            kernels.wait_event(oldest, self.wait_timeout, what)
 
     def init_grad_slots(self, unit_sizes: Dict[int, int], fallback_depth: int = 3) -> None:
         """One pinned slot per unit; if the host cannot pin that much (the

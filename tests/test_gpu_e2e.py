@@ -599,6 +599,24 @@ def test_piecewise_loss_parity(dev):
     check_loss_parity(dev, "llama", False, {}, dict(resident_layers=L - 1, update_piece_elems=PIECE))
 
 
+# Copy options that change only the speed, in the pool schedule where both
+# matter: checkpoints by the pack kernel beside SDMA gradient copies, and the
+# unit-load issue limit off and at its tightest.
+COPY_OPTIONS = [dict(checkpoint_d2h="kernel"), dict(h2d_issue_limit=0), dict(h2d_issue_limit=1)]
+
+
+@pytest.mark.parametrize("opts", COPY_OPTIONS, ids=["ckpt_kernel", "issue_unlimited", "issue_1"])
+def test_copy_options_match_oracle_and_non_offloaded_run(dev, opts):
+    """Every update the oracle's over 3 steps, and step-1 gradients and 10
+    losses equal to the non-offloaded run's, with each option set."""
+    kw = dict(resident_layers=0, d2h_engine="sdma", **opts)
+    sf = check_updates_against_oracle(dev, "llama", "fp32", {}, kw, keep=True)
+    assert sf._checkpoint_d2h == opts.get("checkpoint_d2h", "sdma")
+    assert sf.runtime.h2d_issue_limit == opts.get("h2d_issue_limit", 3)
+    sf.close()
+    check_loss_parity(dev, "llama", False, {}, kw)
+
+
 @pytest.mark.parametrize("ac_mode,fraction,h2d_format", STORAGE_MODES)
 def test_storage_offload_loss_parity(dev, tmp_path, ac_mode, fraction, h2d_format):
     """The storage modes against the non-offloaded run: first-step gradients

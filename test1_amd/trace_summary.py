@@ -9,16 +9,20 @@ BENCH_JSON is the JSON line the same run printed (its bytes per step and
 figures).  Prints:
   - the staging cast over the timed steps (the dispatches after the warmup
     steps' and before the bench's 23 idle-GPU launches): average duration and
-    rate against 8 TB/s, next to the bench's own event-timed figure;
+    rate against 8 TB/s, next to the bench's own event-timed figure, and
+    split into the forward's casts and the backward's (those after each
+    step's largest cast, the output unit's);
   - the ten kernels with the most time;
   - the host link over the timed steps, from the first timed step's embedding
     lookup to the last one's gradient rows: each direction's busy time (union
     of the DMA copies and the host-link kernels: lookup and checkpoint pack /
     gradient rows), its rate while busy from the bench's bytes per step, and
-    the share of it under other kernels.
+    the share of it under other kernels (skipped for a trace without
+    ``run_memory_copy_trace.csv``).
 """
 import csv
 import json
+import os
 import statistics
 import sys
 
@@ -70,6 +74,18 @@ def main(argv=None) -> None:
     print(f"bench: {B['value']:.0f} tokens/s, {B['ms_per_step']:.1f} ms/step; bench cast avg {B['roofline']['avg_launch_ms']:.4f} ms frac {B['roofline']['frac']:.4f} ({B['roofline']['launches']} launches)")
     print(f"casts per step {n_step}; timed casts {len(timed)} avg {avg:.4f} ms median {statistics.median(dur):.4f} ms; "
           f"bytes/launch {ab:.0f}; {ab / avg / 1e6:.1f} GB/s = {ab / avg / 1e6 / 8000:.4f} of 8 TB/s")
+    # Each step's casts after its largest one (the output unit's, the last
+    # of the forward) are the backward's reloads (fp32 reloads only).
+    for what, pick in (("forward", lambda st, big: st[:big + 1]), ("backward", lambda st, big: st[big + 1:])):
+        part = []
+        for k in range(steps):
+            st = timed[k * n_step:(k + 1) * n_step]
+            big = max(range(len(st)), key=lambda i: int(st[i]["Grid_Size_X"]))
+            part += pick(st, big)
+        if part:
+            pd = sum((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6 for r in part) / len(part)
+            pb = 6 * 8 * sum(int(r["Grid_Size_X"]) for r in part) / len(part)
+            print(f"  {what}: {len(part)} casts avg {pd:.4f} ms, {pb / pd / 1e6 / 8000:.4f} of 8 TB/s")
     alone = cast[-20:]
     ad = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6 for r in alone]
     print(f"last 20 casts (idle GPU, one layer) avg {sum(ad) / len(ad):.4f} ms")
@@ -80,7 +96,9 @@ def main(argv=None) -> None:
     print("top kernels (whole run): name | calls | total ms | avg us | %")
     for r in st[:10]:
         print(f"  {r['Name'][:70]} | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.1f} | {float(r['AverageNs']) / 1e3:.1f} | {r['Percentage']}")
-    # host link over the timed steps
+    # host link over the timed steps (needs the memory-copy trace)
+    if not os.path.exists(f"{d}/run_memory_copy_trace.csv"):
+        return
     C = list(csv.DictReader(open(f"{d}/run_memory_copy_trace.csv")))
     look = sorted(iv(r) for r in rows if "gather_rows_kernel<true" in r["Kernel_Name"])
     grow = sorted(iv(r) for r in rows if "gather_rows_kernel<false" in r["Kernel_Name"])

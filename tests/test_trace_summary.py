@@ -107,3 +107,39 @@ def test_summary_of_a_synthetic_trace(tmp_path, capsys):
     # busy per step: 1 + 1 + [10,70] 60 + [80,95] 15 + 1 = 78 ms of 100
     assert "neither copy nor kernel 21.6 %" in out
     assert "H2D copies longer than 8 ms: 2, durations median 30.0 ms" in out
+
+
+def test_forward_and_backward_casts_of_a_kernel_only_trace(tmp_path, capsys):
+    """Casts after each step's largest (the output unit's) are the
+    backward's; without a memory-copy trace the host-link part is skipped."""
+    kernels = []
+
+    def k(name, s, e, grid):
+        kernels.append({"Kernel_Name": name, "Start_Timestamp": s, "End_Timestamp": e, "Grid_Size_X": grid})
+
+    for step in range(3):   # 1 warmup + 2 timed steps of 100 ms
+        t = step * 100 * MS
+        k("cast_flat_kernel(...)", t, t + MS, 10**8)                      # a decoder, forward
+        k("cast_flat_kernel(...)", t + 10 * MS, t + 13 * MS, 3 * 10**8)   # the output unit
+        k("Cijk_Ailk_Bljk_BBS_MT256x256x64", t + 20 * MS, t + 50 * MS, 1)
+        k("cast_flat_kernel(...)", t + 60 * MS, t + 62 * MS, 10**8)       # a decoder's reload
+    for i in range(23):
+        k("cast_flat_kernel(...)", 400 * MS + i * MS, 400 * MS + i * MS + MS // 2, 10**8)
+    with open(tmp_path / "run_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(kernels[0]))
+        w.writeheader()
+        w.writerows(kernels)
+    with open(tmp_path / "run_kernel_stats.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage"])
+        w.writeheader()
+        w.writerow({"Name": "cast_flat_kernel(...)", "Calls": 32, "TotalDurationNs": 30 * MS,
+                    "AverageNs": 30 * MS / 32, "Percentage": 25.0})
+    bench = {"value": 1.0, "ms_per_step": 100.0, "roofline": {"avg_launch_ms": 2.0, "frac": 0.5, "launches": 6}}
+    (tmp_path / "bench.json").write_text(json.dumps(bench) + "\n")
+    ts.main([str(tmp_path), "1", "2", str(tmp_path / "bench.json")])
+    out = capsys.readouterr().out
+    assert "casts per step 3; timed casts 6 avg 2.0000 ms" in out
+    # forward: 1 and 3 ms for 4.8 and 14.4 GB; backward: 2 ms for 4.8 GB
+    assert "forward: 4 casts avg 2.0000 ms, 0.6000 of 8 TB/s" in out
+    assert "backward: 2 casts avg 2.0000 ms, 0.3000 of 8 TB/s" in out
+    assert "window" not in out and "h2d:" not in out

@@ -12,7 +12,7 @@ import ctypes
 import threading
 import time
 import os
-from typing import Callable, Optional, Sequence, Tuple
+from typing import Callable, List, Optional, Sequence, Tuple
 
 import torch
 
@@ -368,14 +368,34 @@ def dma_init(device: Optional[torch.device] = None) -> None:
     idx = (device.index if device is not None and device.index is not None else torch.cuda.current_device())
     if idx in _dma_ready:
         return
+    engines = engines_from_env(os.environ.get("SF_DMA_ENGINES"))
     _native.check(_native.hip().sf_dma_init(int(idx)), "sf_dma_init")
-    env = os.environ.get("SF_DMA_ENGINES")  # e.g. "3"
-    if env not in (None, ""):
-        mask = 0
-        for e in env.split(","):
-            mask |= 1 << int(e)
-        _native.check(_native.hip().sf_dma_set_engines(mask), "sf_dma_set_engines")
+    if engines is not None:
+        _native.check(_native.hip().sf_dma_set_engines(_engine_mask(engines)), "sf_dma_set_engines")
     _dma_ready.add(idx)
+
+
+def engines_from_env(value: Optional[str]) -> Optional[List[int]]:
+    """The engines ``SF_DMA_ENGINES`` names ("3", "2,3"), or None when it is
+    unset or empty; anything but comma-separated engine numbers 0-15 raises
+    ``ValueError``."""
+    if value is None or value.strip() == "":
+        return None
+    try:
+        engines = [int(e) for e in value.split(",")]
+    except ValueError:
+        raise ValueError(f"SF_DMA_ENGINES={value!r}: expected engine numbers 0-15 separated by commas") from None
+    _engine_mask(engines, f"SF_DMA_ENGINES={value!r}: ")
+    return engines
+
+
+def _engine_mask(engines: Sequence[int], what: str = "") -> int:
+    mask = 0
+    for e in engines:
+        if not 0 <= int(e) < 16:
+            raise ValueError(f"{what}SDMA engine {e} out of range 0..15")
+        mask |= 1 << int(e)
+    return mask
 
 
 def require_routing_off() -> None:
@@ -395,12 +415,7 @@ def dma_engines() -> list:
 
 def dma_set_engines(engines: Sequence[int]) -> None:
     """Select the SDMA engines for device -> host copies ([] : runtime's choice)."""
-    mask = 0
-    for e in engines:
-        if not 0 <= int(e) < 16:
-            raise ValueError(f"SDMA engine {e} out of range 0..15")
-        mask |= 1 << int(e)
-    _native.check(_native.hip().sf_dma_set_engines(mask), "sf_dma_set_engines")
+    _native.check(_native.hip().sf_dma_set_engines(_engine_mask(engines)), "sf_dma_set_engines")
 
 
 def dma_set_avoid_held(mode: int) -> None:

@@ -160,3 +160,29 @@ def test_runtime_refuses_routing_set_through_the_api(monkeypatch):
     finally:
         kernels.dma_set_avoid_held(0)
     kernels.require_routing_off()
+
+
+@pytest.mark.parametrize("value,engines", [(None, None), ("", None), (" ", None), ("3", [3]), ("2,3", [2, 3]),
+                                           (" 2, 3 ", [2, 3]), ("0,15", [0, 15])])
+def test_engines_from_env(value, engines):
+    from test1_amd import kernels
+    assert kernels.engines_from_env(value) == engines
+
+
+@pytest.mark.parametrize("value", ["16", "-1", "x", "2,,3", "2;3", "3.0"])
+def test_engines_from_env_rejects_other_values(value):
+    from test1_amd import kernels
+    with pytest.raises(ValueError, match="SF_DMA_ENGINES"):
+        kernels.engines_from_env(value)
+
+
+def test_dma_init_refuses_a_bad_engine_list(monkeypatch):
+    from test1_amd import _native, kernels
+    stub = _InitStub()
+    monkeypatch.setattr(_native, "hip", lambda: stub)
+    monkeypatch.setattr(kernels, "_dma_ready", set())
+    monkeypatch.delenv("SF_DMA_AVOID_HELD", raising=False)
+    monkeypatch.setenv("SF_DMA_ENGINES", "16")
+    with pytest.raises(ValueError, match="SF_DMA_ENGINES"):
+        kernels.dma_init(__import__("torch").device("cuda", 0))
+    assert stub.calls == []

@@ -115,21 +115,29 @@ def _cpu_count() -> int:
 
 
 def adam_threads() -> int:
-    """Threads of the host AdamW: ``SF_ADAM_THREADS`` if set, else the host's
-    cores (capped by ``OMP_NUM_THREADS``) minus one.  The core left over
+    """Threads of the host AdamW: ``SF_ADAM_THREADS`` if set above 0, else the
+    host's cores (capped by the outer level of ``OMP_NUM_THREADS``) minus one.  The core left over
     keeps the threads that feed the GPU (the training loop / autograd thread
     and the offload thread, which mostly wait) responsive while an update
     saturates the rest; the reference reserves cores the same way with
     numa_launch.sh:255-266.  Measured on a 16-core host, Llama-3-8B step,
     same box: 14 threads 810-830 ms, 15 threads 785-793 ms, 16 threads
     785-796 ms."""
-    env = int(os.environ.get("SF_ADAM_THREADS", "0") or 0)
-    if env > 0:
-        return env
+    raw = os.environ.get("SF_ADAM_THREADS", "").strip()
+    if raw:
+        try:
+            env = int(raw)
+        except ValueError:
+            env = -1
+        if env < 0:
+            raise ValueError(f"SF_ADAM_THREADS={raw!r}: expected a thread count (0: the default)")
+        if env > 0:
+            return env
     n = _cpu_count()
-    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
-    if omp > 0:
-        n = min(n, omp)
+    # OpenMP allows a list per nesting level ("16,4"); the outer level counts
+    omp = os.environ.get("OMP_NUM_THREADS", "").split(",")[0].strip()
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
     return max(1, n - 1)
 
 

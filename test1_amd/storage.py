@@ -193,9 +193,13 @@ _default_lock = threading.Lock()
 
 
 def default_engine() -> IoEngine:
-    """The process's shared engine (8 workers), created on first use."""
+    """The process's shared engine (``SF_IO_THREADS`` workers, default 8),
+    created on first use."""
     global _default
     with _default_lock:
         if _default is None:
-            _default = IoEngine(n_threads=int(os.environ.get("SF_IO_THREADS", "8")))
+            raw = os.environ.get("SF_IO_THREADS", "").strip() or "8"
+            if not raw.isdigit() or int(raw) < 1:
+                raise ValueError(f"SF_IO_THREADS={raw!r}: expected a positive thread count")
+            _default = IoEngine(n_threads=int(raw))
         return _default

@@ -496,3 +496,26 @@ def test_bench_host_dram_counts_every_host_link_transfer():
     r["link"] = {}
     st = bench.host_dram_stats(r, SimpleNamespace(h2d_format="bf16", steps=2), None)
     assert st["bytes_per_step"] == 28_000 + 3000 and st["frac_of_streaming_adam"] is None
+
+
+@pytest.mark.parametrize("adam,omp,cores,expected", [
+    (None, None, 16, 15), ("", "", 16, 15), ("0", None, 16, 15), ("12", None, 16, 12), (" 4 ", "2", 16, 4),
+    (None, "8", 16, 7), (None, "8,2", 16, 7), (None, "32", 16, 15), (None, "x", 16, 15), (None, "1", 16, 1),
+    (None, None, 1, 1)])
+def test_adam_threads_from_the_environment(monkeypatch, adam, omp, cores, expected):
+    from test1_amd import slide_fsdp
+    for name, value in (("SF_ADAM_THREADS", adam), ("OMP_NUM_THREADS", omp)):
+        if value is None:
+            monkeypatch.delenv(name, raising=False)
+        else:
+            monkeypatch.setenv(name, value)
+    monkeypatch.setattr(slide_fsdp, "_cpu_count", lambda: cores)
+    assert slide_fsdp.adam_threads() == expected
+
+
+@pytest.mark.parametrize("adam", ["-2", "four", "2.5"])
+def test_adam_threads_rejects_other_values(monkeypatch, adam):
+    from test1_amd import slide_fsdp
+    monkeypatch.setenv("SF_ADAM_THREADS", adam)
+    with pytest.raises(ValueError, match="SF_ADAM_THREADS"):
+        slide_fsdp.adam_threads()

@@ -262,3 +262,12 @@ def test_layer_adam_offload_row_sparse_update(tmp_path):
     assert torch.equal(pr.data.view(torch.int32), po.data.view(torch.int32))
     for a, b in zip(ref.layer_states(0), off.layer_states(0)):
         assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+@pytest.mark.parametrize("value", ["0", "-1", "many"])
+def test_io_threads_env_rejects_other_values(monkeypatch, value):
+    from test1_amd import storage
+    monkeypatch.setattr(storage, "_default", None)
+    monkeypatch.setenv("SF_IO_THREADS", value)
+    with pytest.raises(ValueError, match="SF_IO_THREADS"):
+        storage.default_engine()

@@ -825,6 +825,9 @@ class SlideFSDP(nn.Module):
         self.wait_for_updates()
         torch.cuda.synchronize(self.device)
         self._act_ring.drain_packs()
+        if self._spill is not None:
+            # checkpoint copies into bounce slots run on the spill's worker
+            self._spill.flush()
 
     def _grow_grad_ring(self) -> None:
         """At the start of the second step, with nothing in flight (``_drain``)

@@ -25,17 +25,20 @@ What is different, and why:
   * events are recorded on the current stream rather than the null stream;
   * the checkpoint's empty placeholder tensor is not round-tripped through
     blocking copies;
-  * 16-bit tensors are packed into their slot by a kernel with a capped grid
-    instead of the runtime's full-device copy kernel.
+  * with ``pack_engine="sdma"`` each checkpoint goes to its slot on an SDMA
+    engine, started by a worker thread once the tensor is produced (a kernel
+    writing into host memory slows the kernels beside it); otherwise 16-bit
+    tensors are packed into their slot by a kernel with a capped grid instead
+    of the runtime's full-device copy kernel.
 
 Storage mode (``gds_offload=True``, reference sliding_checkpoint.py:133-202):
 the reference writes each checkpoint input from device memory straight to
 ``file_paths[layer][counter]`` with kvikio (GPUDirect Storage) and reads layer
 j-1 back into a new device buffer when layer j is first unpacked.  This
 platform has no GPU-to-storage DMA, so a ``StorageSpill`` stages through a few
-pinned bounce slots instead: pack copies the tensor into a slot on the
-offload stream, and a worker thread writes the slot to the file once the copy
-has landed; the prefetch of layer j-1 waits for that layer's writes, reads
+pinned bounce slots instead: pack copies the tensor into a slot (on the
+offload stream, or on an SDMA engine started by the worker thread), and a
+worker thread writes the slot to the file once the copy has landed; the prefetch of layer j-1 waits for that layer's writes, reads
 each file into a slot and copies it to the device on the prefetch stream.
 The consumer waits for the prefetch on its stream, as in host mode.  Files
 are opened through the native storage engine (O_DIRECT where available) and
@@ -237,6 +240,18 @@ class _OnStorage:
         self.path, self.shape, self.dtype = path, shape, dtype
 
 
+class _Unless:
+    """A waitable that is complete while ``flags`` is empty."""
+
+    __slots__ = ("flags",)
+
+    def __init__(self, flags: List[Any]):
+        self.flags = flags
+
+    def query(self) -> bool:
+        return not self.flags
+
+
 class _BounceSlot:
     __slots__ = ("buf", "held", "pending")
 
@@ -323,6 +338,40 @@ class StorageSpill:
         with self._lock:
             self._writes[path] = fut
             slot.pending = [fut]
+            slot.held = False
+        self.bytes_written += padded
+
+    def write_after_dma(self, path: str, slot: _BounceSlot, src: torch.Tensor, ready: torch.cuda.Event,
+                        nbytes: int, timeout: Optional[float], timing: Optional[list] = None) -> None:
+        """Copy the contiguous device tensor ``src`` (``nbytes``) into ``slot``
+        on an SDMA engine once ``ready`` (recorded after its producer) has
+        completed, then write it to ``path``; all on the worker thread, which
+        keeps ``src`` referenced until the copy has landed.  ``timing``
+        receives the copy's ("interval_ns", start, end, bytes), or
+        ("untimed", bytes) without engine timestamps.  A copy that does not
+        complete within ``timeout`` keeps the slot and ``src`` for good."""
+        f = self._file(path)
+        padded = storage.align_up(nbytes)
+        stuck: List[Any] = []
+
+        def task():
+            kernels.wait_event(ready, timeout, f"checkpoint {path}: before its copy to the host")
+            dma = kernels.DmaReady(kernels.dma_copy_d2h([(src.reshape(-1), slot.buf[:nbytes])], timeout=timeout),
+                                   timeout=timeout)
+            try:
+                t0, t1 = dma.release()
+            except BaseException:
+                stuck.append((dma, src))
+                raise
+            if timing is not None:
+                timing.append(("interval_ns", t0, t1, nbytes) if t1 > t0 else ("untimed", nbytes))
+            return f.write(slot.buf, 0, padded)
+
+        fut = self._worker.submit(task)
+        with self._lock:
+            self._writes[path] = fut
+            # never idle again if the copy is stuck
+            slot.pending = [fut, _Unless(stuck)]
             slot.held = False
         self.bytes_written += padded
 
@@ -465,9 +514,11 @@ class SlidingCheckpoint(saved_tensors_hooks):
         # checkpoint tensor the recompute is given, taken on its stream after
         # the prefetch wait (what the recompute reads); for checking only.
         self.served = served
-        # How a checkpoint reaches its pinned slot: "kernel", a capped-grid
-        # kernel on ``stream``; "sdma", an SDMA engine (``ActivationRing.
-        # issue_pack``; needs ``prefetch_ring``, else the kernel is used).
+        # How a checkpoint reaches its pinned slot (or, on storage, its bounce
+        # slot): "kernel", a capped-grid kernel on ``stream``; "sdma", an SDMA
+        # engine (``ActivationRing.issue_pack``, ``StorageSpill.
+        # write_after_dma``; needs ``prefetch_ring`` and a contiguous tensor,
+        # else the kernel is used).
         self.pack_engine = pack_engine
 
         def pack_hook(tensor: torch.Tensor) -> Tuple[torch.device, Any]:
@@ -510,15 +561,19 @@ class SlidingCheckpoint(saved_tensors_hooks):
                 self._counts[(self._key, self.layer_idx)] = self.pack_counter
                 return (tensor.device, tensor)
             src = tensor.detach()
-            if (self.pack_engine == "sdma" and self.ring is not None and not self.gds_offload
-                    and src.is_contiguous()):
+            if self.pack_engine == "sdma" and self.ring is not None and src.is_contiguous():
                 # an SDMA engine copies it once the compute stream has produced it
                 ready = torch.cuda.Event()
                 ready.record(cur)
-                self.ring.issue_pack(self._key, self.layer_idx, src, slot, ready)
                 self.pack_counter += 1
                 self._counts[(self._key, self.layer_idx)] = self.pack_counter
-                return (tensor.device, slot)
+                if not self.gds_offload:
+                    self.ring.issue_pack(self._key, self.layer_idx, src, slot, ready)
+                    return (tensor.device, slot)
+                path = self.file_paths[self.layer_idx][self.pack_counter - 1]
+                self.spill.write_after_dma(path, bounce, src, ready, nbytes, self.ring.wait_timeout,
+                                           None if self.link_timing is None else self.link_timing["act_d2h"])
+                return (tensor.device, self._on_storage(path, tensor))
             if not src.is_contiguous():
                 with torch.cuda.stream(self.stream):
                     src = src.contiguous()
@@ -550,10 +605,7 @@ class SlidingCheckpoint(saved_tensors_hooks):
                 copied = torch.cuda.Event()
                 copied.record(self.stream)
                 self.spill.write_after(path, bounce, copied, nbytes)
-                meta = self._meta.setdefault((self._key, self.layer_idx), [])
-                del meta[self.pack_counter - 1:]
-                meta.append((path, tuple(tensor.shape), tensor.dtype))
-                return (tensor.device, _OnStorage(path, tuple(tensor.shape), tensor.dtype))
+                return (tensor.device, self._on_storage(path, tensor))
             return (tensor.device, slot)
 
         def unpack_hook(packed: Tuple[torch.device, Any]) -> torch.Tensor:
@@ -658,6 +710,13 @@ class SlidingCheckpoint(saved_tensors_hooks):
             return result
 
         super().__init__(pack_hook, unpack_hook)
+
+    def _on_storage(self, path: str, tensor: torch.Tensor) -> _OnStorage:
+        """Record that this layer's current pack went to ``path``."""
+        meta = self._meta.setdefault((self._key, self.layer_idx), [])
+        del meta[self.pack_counter - 1:]
+        meta.append((path, tuple(tensor.shape), tensor.dtype))
+        return _OnStorage(path, tuple(tensor.shape), tensor.dtype)
 
     def _record_served(self, t: torch.Tensor) -> None:
         if self.served is not None:

@@ -15,11 +15,12 @@ pytestmark = pytest.mark.gpu
 
 def run_layers(dev, L, shape, weights, offload, seen, use_ring=True, spill_dir=None, mask=None):
     """``offload``: None (plain checkpointing), "host" (pinned slots, packed by
-    the kernel), "host_sdma" (pinned slots, packed by SDMA copies) or
-    "storage" (files under ``spill_dir`` through a 3-slot StorageSpill)."""
-    pack_engine = "sdma" if offload == "host_sdma" else "kernel"
-    if offload == "host_sdma":
-        offload = "host"
+    the kernel), "storage" (files under ``spill_dir`` through a 3-slot
+    StorageSpill, bounce slots packed by the kernel), or either with "_sdma"
+    (copies by an SDMA engine; the kernel without a ring)."""
+    pack_engine = "kernel"
+    if offload is not None and offload.endswith("_sdma"):
+        offload, pack_engine = offload[:-len("_sdma")], "sdma"
         kernels.dma_init(dev)
     h = torch.randn(shape, generator=torch.Generator().manual_seed(0)).bfloat16().to(dev).requires_grad_(True)
     slots = [[pinned_empty(shape, torch.bfloat16)] for _ in range(L)] if offload == "host" else None
@@ -53,7 +54,7 @@ def run_layers(dev, L, shape, weights, offload, seen, use_ring=True, spill_dir=N
 
 
 @pytest.mark.parametrize("use_ring", [True, False])
-@pytest.mark.parametrize("mode", ["host", "host_sdma", "storage"])
+@pytest.mark.parametrize("mode", ["host", "host_sdma", "storage", "storage_sdma"])
 def test_round_trip_bit_exact_small(dev, use_ring, mode, tmp_path):
     L, shape = 6, (2, 128, 256)
     ws = [torch.randn(shape[-1], generator=torch.Generator().manual_seed(10 + i)).bfloat16().to(dev).requires_grad_(True)
@@ -63,7 +64,7 @@ def test_round_trip_bit_exact_small(dev, use_ring, mode, tmp_path):
     for i in range(L):
         fwd, rec = seen[i]
         assert torch.equal(fwd.view(torch.int16), rec.view(torch.int16)), f"layer {i} input changed"
-        if i < L - 1 and mode != "storage":  # every layer but the last went through its host slot
+        if i < L - 1 and mode.startswith("host"):  # every layer but the last went through its host slot
             assert torch.equal(slots[i][0].view(torch.int16), fwd.cpu().view(torch.int16))
     for w in ws:
         w.grad = None
@@ -73,7 +74,8 @@ def test_round_trip_bit_exact_small(dev, use_ring, mode, tmp_path):
     assert torch.equal(hg_off.view(torch.int16), hg_ref.view(torch.int16))
 
 
-def test_storage_two_tensors_per_layer(dev, tmp_path):
+@pytest.mark.parametrize("mode", ["storage", "storage_sdma"])
+def test_storage_two_tensors_per_layer(dev, tmp_path, mode):
     """Storage mode with a second, non-16-bit checkpoint input per layer (a
     bool mask of an odd byte size, so files and slots are padded): inputs and
     gradients equal plain checkpointing's."""
@@ -82,7 +84,7 @@ def test_storage_two_tensors_per_layer(dev, tmp_path):
     ws = [torch.randn(shape[-1], generator=torch.Generator().manual_seed(20 + i)).bfloat16().to(dev).requires_grad_(True)
           for i in range(L)]
     seen = {}
-    g_off, hg_off, _ = run_layers(dev, L, shape, ws, "storage", seen, spill_dir=str(tmp_path), mask=mask)
+    g_off, hg_off, _ = run_layers(dev, L, shape, ws, mode, seen, spill_dir=str(tmp_path), mask=mask)
     for i in range(L):
         fwd, rec = seen[i]
         assert torch.equal(fwd.view(torch.int16), rec.view(torch.int16)), f"layer {i} input changed"
@@ -94,12 +96,13 @@ def test_storage_two_tensors_per_layer(dev, tmp_path):
     assert torch.equal(hg_off.view(torch.int16), hg_ref.view(torch.int16))
 
 
-@pytest.mark.parametrize("mode", ["host", "host_sdma", "storage"])
+@pytest.mark.parametrize("mode", ["host", "host_sdma", "storage", "storage_sdma"])
 @pytest.mark.parametrize("L,shape", [(32, (4, 1024, 4096)), (48, (2, 4096, 5120))],
                          ids=["llama3-8b", "qwen2.5-14b"])
 def test_round_trip_model_checkpoint_shapes(dev, L, shape, mode, tmp_path):
-    """The models' checkpoints through the pinned slots (packed by the kernel
-    or by SDMA copies, or through files on local storage) and back, bit-exact: 32 layers of [4, 1024, 4096] bf16
+    """The models' checkpoints through the pinned slots or through files on
+    local storage (packed by the kernel or by SDMA copies) and back,
+    bit-exact: 32 layers of [4, 1024, 4096] bf16
     (32 MiB each, Llama-3-8B at batch 4 x 1024) and 48 layers of
     [2, 4096, 5120] (80 MiB each, Qwen2.5-14B at batch 2 x 4096)."""
     ws = [torch.full((shape[-1],), 1.0 + 1e-2 * i, dtype=torch.bfloat16, device=dev, requires_grad=True)

@@ -271,3 +271,77 @@ def test_io_threads_env_rejects_other_values(monkeypatch, value):
     monkeypatch.setenv("SF_IO_THREADS", value)
     with pytest.raises(ValueError, match="SF_IO_THREADS"):
         storage.default_engine()
+
+
+class _FakeDma:
+    """Stands in for the SDMA copy of ``StorageSpill.write_after_dma`` on the
+    CPU: copies at once; ``release`` returns engine times or raises."""
+
+    def __init__(self, stuck):
+        self.stuck = stuck
+
+    def copy(self, pairs, timeout=None):
+        for src, dst in pairs:
+            dst.copy_(src.view(torch.uint8).reshape(-1))
+        return "handle"
+
+    def ready(self, handle, timeout=None):
+        fake = self
+
+        class Ready:
+            def release(self):
+                if fake.stuck:
+                    raise kernels_mod().DmaCopiesOutstanding("1 SDMA copies not complete")
+                return 10, 20
+        return Ready()
+
+
+def kernels_mod():
+    from test1_amd import kernels
+    return kernels
+
+
+def _spill_with_fake_dma(monkeypatch, tmp_path, stuck):
+    from test1_amd import sliding_checkpoint as sc
+
+    fake = _FakeDma(stuck)
+    k = kernels_mod()
+    monkeypatch.setattr(k, "wait_event", lambda ev, timeout, what: None)
+    monkeypatch.setattr(k, "dma_copy_d2h", fake.copy)
+    monkeypatch.setattr(k, "DmaReady", fake.ready)
+    spill = sc.StorageSpill(n_slots=2, engine=storage.IoEngine(n_threads=2), direct=False)
+    slot = object.__new__(sc._BounceSlot)
+    slot.buf, slot.held, slot.pending = torch.zeros(storage.align_up(4096), dtype=torch.uint8), True, []
+    return spill, slot
+
+
+def test_checkpoint_to_storage_by_sdma_copy(monkeypatch, tmp_path):
+    """The spill's worker waits for the producer, copies into the bounce
+    slot, records the copy's engine times, then writes the file; the slot is
+    free again after the write."""
+    spill, slot = _spill_with_fake_dma(monkeypatch, tmp_path, stuck=False)
+    src = torch.arange(2048, dtype=torch.int16).view(torch.bfloat16)
+    timing = []
+    path = str(tmp_path / "ckpt.bin")
+    spill.write_after_dma(path, slot, src, None, 4096, 5.0, timing)
+    spill.flush()
+    assert timing == [("interval_ns", 10, 20, 4096)]
+    assert slot.idle()
+    back = torch.zeros(storage.align_up(4096), dtype=torch.uint8)
+    spill._file(path).read(back, 0, storage.align_up(4096)).wait()
+    assert torch.equal(back[:4096], src.view(torch.uint8))
+    spill.close()
+
+
+def test_stuck_sdma_copy_keeps_its_bounce_slot(monkeypatch, tmp_path):
+    """A copy not seen complete within the limit: the write fails with the
+    copy's error, and the slot is never handed out again (an engine may still
+    write into it)."""
+    spill, slot = _spill_with_fake_dma(monkeypatch, tmp_path, stuck=True)
+    src = torch.zeros(2048, dtype=torch.bfloat16)
+    spill.write_after_dma(str(tmp_path / "ckpt.bin"), slot, src, None, 4096, 5.0)
+    with pytest.raises(kernels_mod().DmaCopiesOutstanding):
+        spill.flush()
+    assert not slot.idle()
+    spill._writes.clear()
+    spill.close()

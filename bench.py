@@ -251,7 +251,7 @@ def timed_run(model, w: dict, args, dev, h2d_format: str, resident_layers, d2h_e
 
     t0 = time.time()
     cfg = SlideFSDPConfig(device=dev, lr=1e-5, weight_decay=0.01, attention_implementation="sdpa",
-                          ac_offload_mode=args.ac_offload,
+                          ac_offload_mode=args.ac_offload, gpu_buffer_pool_size=args.pool_size,
                           ac_offload_dir=os.path.join(args.offload_dir, "activations"),
                           optimizer_nvme_offload_fraction=args.opt_nvme_fraction,
                           optimizer_offload_dir=os.path.join(args.offload_dir, "optimizer"),
@@ -1057,6 +1057,8 @@ def main():
                          "run piece by piece, one cast per unit), e.g. 67108864; 0: whole units")
     ap.add_argument("--checkpoint-d2h", default=None, choices=("sdma", "kernel"),
                     help="how checkpoints reach their pinned slots (default: sdma with the sdma D2H engine)")
+    ap.add_argument("--pool-size", type=int, default=2,
+                    help="units in the device buffer pool (the reference's gpu_buffer_pool_size, default 2)")
     ap.add_argument("--h2d-issue-limit", type=int, default=3,
                     help="unit copies the forward and backward may keep queued before they wait (0: no limit)")
     ap.add_argument("--no-early-embedding", action="store_true",
@@ -1229,7 +1231,7 @@ def main():
                    "checkpoint_d2h": args.checkpoint_d2h or ("sdma" if args.d2h_engine == "sdma" else "kernel"),
                    "fused_cross_entropy": args.fused_ce,
                    "stage_after_update": r["stage_after_update"],
-                   "update_piece_elems": args.piece_elems, "h2d_issue_limit": args.h2d_issue_limit,
+                   "update_piece_elems": args.piece_elems, "h2d_issue_limit": args.h2d_issue_limit, "gpu_buffer_pool_size": args.pool_size,
                    "cast_at_use": r["cast_at_use"],
                    "bf16_reload_units": r["bf16_reload_units"],
                    "early_embedding_update": not args.no_early_embedding,
